@@ -1,0 +1,110 @@
+"""ctypes binding of libaxs6.so (C ABI declared in include/axs6.h).
+
+The library is built in-tree by ``python axs-6_amd/build.py`` into
+``axs-6_amd/axs/_lib/libaxs6.so``.  There is no fallback: if the library is
+missing or fails to load, every entry point raises.
+
+torch is imported first so that the HIP runtime torch ships
+(libamdhip64.so.7) is the one the library binds to; device pointers and
+streams are then shared with torch.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libaxs6.so")
+
+F32, BF16, F16 = 0, 1, 2
+DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_f32p = ctypes.POINTER(ctypes.c_float)
+
+# name -> argtypes; every entry point returns int (axs6_status)
+_SIGNATURES: dict[str, list] = {
+    "axs6_init": [],
+    "axs6_get_tables": [_f32p, _f32p, _u8p, _u8p],
+    "axs6_nf5_fake_quantize": [_vp, _vp, _i32, _i64, _i64, _i32, _i32, _u64, _u64, _vp],
+    "axs6_nf5_quantize": [_vp, _i32, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _vp, _vp, _vp],
+    "axs6_nf5_dequantize": [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
+}
+
+
+class LibraryError(RuntimeError):
+    """libaxs6.so is missing, failed to load, or a call returned an error."""
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise LibraryError(
+                    f"libaxs6.so not found at {LIB_PATH}; build it with "
+                    "`python axs-6_amd/build.py` (hipcc, gfx950)")
+            try:
+                L = ctypes.CDLL(LIB_PATH)
+            except OSError as e:  # pragma: no cover - environment problem
+                raise LibraryError(f"failed to load {LIB_PATH}: {e}") from e
+            L.axs6_version.restype = ctypes.c_char_p
+            L.axs6_version.argtypes = []
+            L.axs6_last_error.restype = ctypes.c_char_p
+            L.axs6_last_error.argtypes = []
+            for name, argt in _SIGNATURES.items():
+                fn = getattr(L, name, None)
+                if fn is not None:
+                    fn.argtypes = argt
+                    fn.restype = ctypes.c_int
+            _lib = L
+    return _lib
+
+
+def has(name: str) -> bool:
+    return hasattr(lib(), name)
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point and raise RuntimeError on a non-zero status."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().axs6_last_error().decode(errors="replace")
+        raise LibraryError(f"{name} failed (status {rc}): {msg}")
+
+
+def version() -> str:
+    return lib().axs6_version().decode()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """Raw hipStream_t of torch's current stream on t's device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def host_tables():
+    """(codebook f32[32], lut f32[1024], reverse_lut u8[1024], log2_band u8[278])."""
+    cb = (ctypes.c_float * 32)()
+    lut = (ctypes.c_float * 1024)()
+    rev = (ctypes.c_uint8 * 1024)()
+    band = (ctypes.c_uint8 * 278)()
+    call("axs6_get_tables", cb, lut, rev, band)
+    return (torch.tensor(list(cb), dtype=torch.float32),
+            torch.tensor(list(lut), dtype=torch.float32),
+            torch.tensor(list(rev), dtype=torch.uint8),
+            torch.tensor(list(band), dtype=torch.uint8))

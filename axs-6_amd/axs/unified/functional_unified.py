@@ -1,0 +1,96 @@
+"""Autograd ops: NF5 fake-quantize with a straight-through gradient and the
+AXS-6 quantized linear / matmul.
+
+Mirrors ``axs/unified/functional_unified.py`` of the reference
+(``_FusedQuantizeSTE`` :38-60, ``fake_quantize_unified`` :63-82,
+``_AXSLinearUnifiedFunction`` :89-170, ``axs_linear_unified`` :173-197,
+``axs_matmul_unified`` :204-227): same signatures, same gradient semantics.
+The linear runs on the HIP kernels of libaxs6.so: NF5 fake-quantize fused
+with the fp16 operand packing, then an MFMA GEMM (``axs.unified.hip_linear``).
+"""
+from __future__ import annotations
+
+from typing import Literal
+
+import torch
+
+from axs.core import DEFAULT_BLOCK_SIZE
+from axs.unified import hip_linear
+from axs.unified.backend import accelerated_fake_quantize as _accel_fq
+
+
+class _FusedQuantizeSTE(torch.autograd.Function):
+    """Forward: NF5 fake-quantize.  Backward: the incoming gradient, unchanged."""
+
+    @staticmethod
+    def forward(ctx, tensor: torch.Tensor, block_size: int, rounding: str) -> torch.Tensor:  # type: ignore[override]
+        return _accel_fq(tensor, block_size=block_size, rounding=rounding)  # type: ignore[arg-type]
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor):  # type: ignore[override]
+        return grad_output, None, None
+
+
+def fake_quantize_unified(
+    tensor: torch.Tensor,
+    block_size: int = DEFAULT_BLOCK_SIZE,
+    rounding: Literal["nearest", "stochastic"] = "nearest",
+) -> torch.Tensor:
+    """NF5 fake-quantize with a straight-through gradient."""
+    return _FusedQuantizeSTE.apply(tensor, block_size, rounding)
+
+
+class _AXSLinearUnifiedFunction(torch.autograd.Function):
+    """Y = FQ(X) FQ(W)^T + b.
+
+    Backward (straight-through): dY is fake-quantized with stochastic
+    rounding when ``quantize_grad``; dX = dYq FQ(W), dW = dYq^T FQ(X),
+    db = sum of dYq over the batch dims.  The fp16 operands packed in the
+    forward are kept for the backward instead of the fp32 FQ(X) the
+    reference saves (half the activation memory; FQ(W) is not recomputed).
+    """
+
+    @staticmethod
+    def forward(ctx, input, weight, bias, block_size, quantize_input, quantize_grad):  # type: ignore[override]
+        out, saved = hip_linear.forward_train(input, weight, bias, block_size, quantize_input)
+        ctx.save_for_backward(*saved.tensors())
+        ctx.meta = saved.meta()
+        ctx.block_size = block_size
+        ctx.quantize_grad = quantize_grad
+        ctx.has_bias = bias is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):  # type: ignore[override]
+        saved = hip_linear.Saved.restore(ctx.saved_tensors, ctx.meta)
+        need_x, need_w, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[2]
+        dx, dw, db = hip_linear.backward(
+            grad_output, saved, ctx.block_size, ctx.quantize_grad,
+            need_x, need_w, need_b and ctx.has_bias)
+        return dx, dw, db, None, None, None
+
+
+def axs_linear_unified(
+    input: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    block_size: int = DEFAULT_BLOCK_SIZE,
+    quantize_input: bool = True,
+    quantize_grad: bool = True,
+) -> torch.Tensor:
+    """AXS-6 quantized linear: ``input (*, in) -> (*, out)``."""
+    return _AXSLinearUnifiedFunction.apply(input, weight, bias, block_size, quantize_input, quantize_grad)
+
+
+def axs_matmul_unified(
+    a: torch.Tensor,
+    b: torch.Tensor,
+    block_size: int = DEFAULT_BLOCK_SIZE,
+    quantize_inputs: bool = True,
+) -> torch.Tensor:
+    """``FQ(a) @ FQ(b)`` (blocks along each operand's last dim, as the
+    reference) on the HIP GEMM; no autograd."""
+    if quantize_inputs:
+        a = _accel_fq(a, block_size, "nearest")
+        b = _accel_fq(b, block_size, "nearest")
+    return hip_linear.matmul(a, b)

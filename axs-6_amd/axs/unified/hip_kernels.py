@@ -1,0 +1,164 @@
+"""Host wrappers of the gfx950 NF5 kernels (libaxs6.so).
+
+These replace the reference's Triton entry points
+``triton_fused_fake_quantize`` (``axs/unified/triton_kernels.py:295-370``)
+and ``triton_fused_linear`` (``:385-482``) with the same argument meaning
+and error behaviour:
+
+* a CPU tensor raises ``RuntimeError`` mentioning CUDA (ROCm reports GPU
+  tensors as ``is_cuda``), as ``triton_kernels.py:326-327,422-423`` do;
+* an invalid ``block_size`` fails the ``assert`` (``:328-330``);
+* output keeps the input's shape and dtype, computing in float32;
+* padding of a ragged last dim is virtual (handled inside the kernels).
+
+Nothing here computes on the CPU: if libaxs6.so is absent these raise.
+"""
+from __future__ import annotations
+
+from typing import Literal
+
+import torch
+
+from axs import _lib
+from axs.core import DEFAULT_BLOCK_SIZE, VALID_BLOCK_SIZES
+
+
+def has_hip() -> bool:
+    """True when libaxs6.so loads and a ROCm GPU is visible."""
+    try:
+        _lib.lib()
+    except _lib.LibraryError:
+        return False
+    return torch.cuda.is_available()
+
+
+def _require_device(t: torch.Tensor, fn: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{fn} requires a CUDA (ROCm/HIP) device tensor, got device {t.device}")
+
+
+def _check_rounding(rounding: str) -> bool:
+    if rounding not in ("nearest", "stochastic"):
+        raise ValueError(f"rounding must be 'nearest' or 'stochastic', got {rounding!r}")
+    return rounding == "stochastic"
+
+
+class _on_device:
+    """Makes t's device current for the duration of a library call."""
+
+    def __init__(self, t: torch.Tensor):
+        self.idx = t.device.index
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if self.idx is not None and self.idx != cur:
+            self.prev = cur
+            torch.cuda.set_device(self.idx)
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+
+
+def next_seed() -> int:
+    """Seed for one stochastic call, drawn from torch's default CPU
+    generator (so torch.manual_seed reproduces it) -- a host-side draw, with
+    no device synchronisation (the reference's Triton path does a .item()
+    on a device tensor for this, triton_kernels.py:351)."""
+    return int(torch.randint(0, 2**62, (1,)).item())
+
+
+def as_rows(tensor: torch.Tensor) -> tuple[torch.Tensor, int, int]:
+    """Contiguous view of ``tensor`` as (rows, cols) over its last dim, in a
+    dtype the kernels take (f32 / bf16 / f16; anything else is computed in
+    float32 like the reference's ``.float()``)."""
+    x = tensor
+    if x.dtype not in _lib.DTYPE_CODE:
+        x = x.float()
+    x = x.contiguous()
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    return x, rows, cols
+
+
+def hip_fused_fake_quantize(
+    tensor: torch.Tensor,
+    block_size: int = DEFAULT_BLOCK_SIZE,
+    rounding: Literal["nearest", "stochastic"] = "nearest",
+    *,
+    n_blocks: int | None = None,
+    seed: int | None = None,
+) -> torch.Tensor:
+    """NF5 fused fake-quantize on the GPU (one streaming HIP kernel).
+
+    Bit-exact with the reference's eager ``fused_fake_quantize`` for
+    ``rounding="nearest"``.  ``rounding="stochastic"`` dithers with the
+    library's counter-based generator; ``seed`` fixes the draw (default: a
+    fresh seed from torch's CPU generator).  ``n_blocks`` is accepted for
+    signature compatibility with the reference's Triton wrapper; the launch
+    shape is chosen by the library.
+    """
+    fn = "hip_fused_fake_quantize"
+    _require_device(tensor, fn)
+    assert block_size in VALID_BLOCK_SIZES, f"block_size must be one of {VALID_BLOCK_SIZES}"
+    stochastic = _check_rounding(rounding)
+    orig_dtype = tensor.dtype
+    x, rows, cols = as_rows(tensor)
+    y = torch.empty_like(x)
+    if rows and cols:
+        s = (next_seed() if seed is None else int(seed)) if stochastic else 0
+        with _on_device(x):
+            _lib.call("axs6_nf5_fake_quantize", x.data_ptr(), y.data_ptr(), _lib.DTYPE_CODE[x.dtype],
+                      rows, cols, block_size, int(stochastic), s, 0, _lib.stream_of(x))
+    y = y.reshape(tensor.shape)
+    return y if y.dtype == orig_dtype else y.to(orig_dtype)
+
+
+def hip_quantize(
+    tensor: torch.Tensor,
+    block_size: int = DEFAULT_BLOCK_SIZE,
+    rounding: Literal["nearest", "stochastic"] = "nearest",
+    *,
+    with_fake_quantized: bool = False,
+    seed: int | None = None,
+):
+    """Runs the quantize kernel: returns (exponents u8 (R, nblk), codes u8
+    (R, nblk, bs), signs bool (R, nblk, bs), fq or None)."""
+    fn = "hip_quantize"
+    _require_device(tensor, fn)
+    assert block_size in VALID_BLOCK_SIZES, f"block_size must be one of {VALID_BLOCK_SIZES}"
+    stochastic = _check_rounding(rounding)
+    x, rows, cols = as_rows(tensor)
+    nblk = (cols + block_size - 1) // block_size
+    dev = x.device
+    exps = torch.empty((rows, nblk), dtype=torch.uint8, device=dev)
+    codes = torch.empty((rows, nblk, block_size), dtype=torch.uint8, device=dev)
+    signs = torch.empty((rows, nblk, block_size), dtype=torch.uint8, device=dev)
+    fq = torch.empty_like(x) if with_fake_quantized else None
+    if rows and cols:
+        s = (next_seed() if seed is None else int(seed)) if stochastic else 0
+        with _on_device(x):
+            _lib.call("axs6_nf5_quantize", x.data_ptr(), _lib.DTYPE_CODE[x.dtype], rows, cols,
+                      block_size, int(stochastic), s, 0, exps.data_ptr(), codes.data_ptr(),
+                      signs.data_ptr(), _lib.ptr(fq), _lib.stream_of(x))
+    if fq is not None:
+        fq = fq.reshape(tensor.shape)
+        if fq.dtype != tensor.dtype:
+            fq = fq.to(tensor.dtype)
+    return exps, codes, signs.view(torch.bool), fq
+
+
+def hip_dequantize(exps: torch.Tensor, codes: torch.Tensor, signs: torch.Tensor | None,
+                   rows: int, cols: int, block_size: int) -> torch.Tensor:
+    _require_device(codes, "hip_dequantize")
+    assert block_size in VALID_BLOCK_SIZES, f"block_size must be one of {VALID_BLOCK_SIZES}"
+    e = exps.contiguous()
+    c = codes.contiguous()
+    s = None if signs is None else signs.contiguous().view(torch.uint8)
+    y = torch.empty((rows, cols), dtype=torch.float32, device=codes.device)
+    if rows and cols:
+        with _on_device(c):
+            _lib.call("axs6_nf5_dequantize", e.data_ptr(), c.data_ptr(), _lib.ptr(s), y.data_ptr(),
+                      rows, cols, block_size, _lib.stream_of(c))
+    return y

@@ -1,0 +1,563 @@
+// NF5 fake-quantize, quantize and dequantize kernels for gfx950.
+//
+// Per block of 8/16/32 values along the last dim (the arithmetic of
+// fused_fake_quantize, axs/unified/quantize_unified.py:121-204):
+//   amax   = max |x|                     (NaN if any element is NaN)
+//   e1     = floor(log2(max(amax, 2^-149))) + 1, taken from the exponent
+//            bits plus the log2 rounding band (see axs6_runtime.hip)
+//   scale  = 2^e1 (inf when e1 >= 128; 1 for all-zero blocks)
+//   idx    = clamp(trunc((|x| / scale) * 1023), 0, 1023)
+//            (stochastic: trunc((|x|/scale + (U - 0.5)/1023) * 1023))
+//   y      = (sign(x) * lut[idx]) * scale
+// Every step rounds exactly as torch's CPU float32 ops do, so the output is
+// bit-identical to the reference's eager path (FP contraction is off).
+//
+// Layout and launch.  Fast path (cols % block == 0, 16-byte aligned
+// pointers): the tensor is one contiguous run of blocks; each lane loads one
+// 16-byte vector (4 x f32 or 8 x bf16/f16), so a 32-value f32 block spans 8
+// neighbouring lanes and its amax is a 3-step DPP butterfly (quad_perm x2,
+// row_half_mirror) -- no LDS round trip.  A wave instruction moves 1 KiB of
+// contiguous HBM; each thread keeps kUnroll vectors in flight.  The 4 KiB
+// LUT and the band table are staged in LDS once per workgroup and the grid
+// is capped (grid-stride loop) so that staging is amortised.
+// General path (ragged last dim or unaligned views): one element per lane,
+// one block per `block` lanes, shuffle reductions.
+#include <math.h>
+#include <stdlib.h>
+
+#include "axs6_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace axs6 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- element types ------------------------------------------------------
+
+template <int DT> struct Elem;
+
+template <> struct Elem<AXS6_F32> {
+    using S = float;
+    static constexpr int V = 4;
+    __device__ static float to_f(S v) { return v; }
+    __device__ static S from_f(float f) { return f; }
+    __device__ static void unpack(u32x4 r, float* f) {
+        f[0] = __uint_as_float(r.x); f[1] = __uint_as_float(r.y);
+        f[2] = __uint_as_float(r.z); f[3] = __uint_as_float(r.w);
+    }
+    __device__ static u32x4 pack(const float* f) {
+        u32x4 r;
+        r.x = __float_as_uint(f[0]); r.y = __float_as_uint(f[1]);
+        r.z = __float_as_uint(f[2]); r.w = __float_as_uint(f[3]);
+        return r;
+    }
+};
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    // torch's c10::BFloat16 rounding: NaN -> 0x7FC0, otherwise round to
+    // nearest even on the upper 16 bits.
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7FC0;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+template <> struct Elem<AXS6_BF16> {
+    using S = uint16_t;
+    static constexpr int V = 8;
+    __device__ static float to_f(S v) { return __uint_as_float((uint32_t)v << 16); }
+    __device__ static S from_f(float f) { return f32_to_bf16_rne(f); }
+    __device__ static void unpack(u32x4 r, float* f) {
+        uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = __uint_as_float(w[i] << 16);
+            f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+    __device__ static u32x4 pack(const float* f) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = (uint32_t)f32_to_bf16_rne(f[2 * i]) | ((uint32_t)f32_to_bf16_rne(f[2 * i + 1]) << 16);
+        u32x4 r;
+        r.x = w[0]; r.y = w[1]; r.z = w[2]; r.w = w[3];
+        return r;
+    }
+};
+
+template <> struct Elem<AXS6_F16> {
+    using S = _Float16;
+    static constexpr int V = 8;
+    __device__ static float to_f(S v) { return (float)v; }
+    __device__ static S from_f(float f) { return (_Float16)f; }  // v_cvt_f16_f32: RNE
+    __device__ static void unpack(u32x4 r, float* f) {
+        uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint16_t lo = (uint16_t)(w[i] & 0xffffu), hi = (uint16_t)(w[i] >> 16);
+            f[2 * i] = (float)__builtin_bit_cast(_Float16, lo);
+            f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, hi);
+        }
+    }
+    __device__ static u32x4 pack(const float* f) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint16_t lo = __builtin_bit_cast(uint16_t, (_Float16)f[2 * i]);
+            uint16_t hi = __builtin_bit_cast(uint16_t, (_Float16)f[2 * i + 1]);
+            w[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        u32x4 r;
+        r.x = w[0]; r.y = w[1]; r.z = w[2]; r.w = w[3];
+        return r;
+    }
+};
+
+// ---- block arithmetic ------------------------------------------------------
+
+// Unsigned max across a group of G neighbouring lanes (G in {1,2,4,8}) with
+// DPP: quad_perm [1,0,3,2], quad_perm [2,3,0,1], then row_half_mirror pairs
+// each quad with the other quad of its 8-lane half-row.
+template <int G>
+__device__ __forceinline__ uint32_t group_umax(uint32_t v) {
+    if constexpr (G >= 2) {
+        uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false);
+        v = v > o ? v : o;
+    }
+    if constexpr (G >= 4) {
+        uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false);
+        v = v > o ? v : o;
+    }
+    if constexpr (G >= 8) {
+        uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false);
+        v = v > o ? v : o;
+    }
+    return v;
+}
+
+// Same reduction for groups of up to 32 lanes through cross-lane shuffles
+// (general path only).
+template <int BS>
+__device__ __forceinline__ uint32_t group_umax_shfl(uint32_t v) {
+#pragma unroll
+    for (int off = 1; off < BS; off <<= 1) {
+        uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
+        v = v > o ? v : o;
+    }
+    return v;
+}
+
+constexpr uint32_t kInfBits = 0x7f800000u;
+constexpr uint32_t kNanBits = 0x7fc00000u;
+
+// floor(torch.log2(a)) for a positive finite float32 given by its bits.
+__device__ __forceinline__ int floor_log2_torch(uint32_t a, const uint8_t* band) {
+    int f = a >= 0x00800000u ? (int)(a >> 23) - 127 : (31 - __clz((int)a)) - 149;
+    int k = f + 1;
+    uint32_t kb = k >= -126 ? (uint32_t)(k + 127) << 23 : 1u << (k + 149);
+    return (kb - a <= (uint32_t)band[k + 149]) ? k : f;
+}
+
+__device__ __forceinline__ float pow2_float(int e) {
+    // exact 2^e for e in [-149, 127]; inf above.
+    return e >= 128 ? __uint_as_float(kInfBits)
+                    : (e >= -126 ? __uint_as_float((uint32_t)(e + 127) << 23)
+                                 : __uint_as_float(1u << (e + 149)));
+}
+
+// The per-block scale of fused_fake_quantize (quantize_unified.py:172-179).
+struct FqScale {
+    float scale;    // torch's `scales` entry: 2^e1, 1 (zero block), inf, NaN
+    int e1;         // exponent used to normalise when scale is finite
+    bool inf_scale;
+    bool nan_block;
+};
+
+__device__ __forceinline__ FqScale fq_scale(uint32_t amax, const uint8_t* band) {
+    FqScale s;
+    s.nan_block = amax > kInfBits;
+    bool zero = amax == 0u;
+    bool inf_amax = amax == kInfBits;
+    int e1 = (zero || amax >= kInfBits) ? 0 : floor_log2_torch(amax, band) + 1;
+    s.inf_scale = inf_amax || e1 >= 128;
+    s.e1 = s.inf_scale ? 0 : e1;
+    s.scale = s.nan_block ? __uint_as_float(kNanBits)
+                          : (s.inf_scale ? __uint_as_float(kInfBits) : (zero ? 1.0f : pow2_float(e1)));
+    return s;
+}
+
+// |x| / scale exactly, for power-of-two scales.
+__device__ __forceinline__ float normalise(uint32_t abits, const FqScale& s) {
+    if (s.inf_scale) return abits >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;
+    return __builtin_amdgcn_ldexpf(__uint_as_float(abits), -s.e1);
+}
+
+__device__ __forceinline__ int lut_index(float n, bool stochastic, float u) {
+    float t;
+    if (stochastic) {
+        float d = (u - 0.5f) / 1023.0f;   // IEEE division, as torch
+        t = (n + d) * 1023.0f;
+    } else {
+        t = n * 1023.0f;
+    }
+    t = (t == t) ? t : 0.0f;              // NaN -> INT_MIN -> clamped to 0 in torch
+    int i = (int)t;                       // truncation toward zero
+    return i < 0 ? 0 : (i > kLutMax ? kLutMax : i);
+}
+
+__device__ __forceinline__ float torch_sign(float x) {
+    return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
+}
+
+__device__ __forceinline__ float fq_value(float x, const FqScale& s, const float* lut, bool stochastic, float u) {
+    uint32_t ab = __float_as_uint(x) & 0x7fffffffu;
+    float n = normalise(ab, s);
+    float rec = lut[lut_index(n, stochastic, u)];
+    float r = (torch_sign(x) * rec) * s.scale;
+    return s.nan_block ? __uint_as_float(kNanBits) : r;
+}
+
+// splitmix64 mix of (seed + i * golden); top 24 bits -> U[0,1).
+__device__ __forceinline__ float dither_uniform(uint64_t seed, uint64_t i) {
+    uint64_t z = seed + i * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (float)(uint32_t)(z >> 40) * (1.0f / 16777216.0f);
+}
+
+// Stages the LUT (and the band table) in LDS; needs kThreads == 256.
+__device__ __forceinline__ void stage_tables(float* lut_s, uint32_t* band_w, const float* lut_g,
+                                             const uint8_t* band_g) {
+    const int tid = threadIdx.x;
+    reinterpret_cast<float4*>(lut_s)[tid] = reinterpret_cast<const float4*>(lut_g)[tid];
+    if (tid < kBandSize / 4) band_w[tid] = reinterpret_cast<const uint32_t*>(band_g)[tid];
+    __syncthreads();
+}
+
+// ---- fake-quantize kernels -----------------------------------------------
+
+template <int DT, int BS, bool STOCH>
+__global__ __launch_bounds__(kThreads) void fq_vec_kernel(const typename Elem<DT>::S* x,
+                                                          typename Elem<DT>::S* y, int64_t n_vec,
+                                                          const float* __restrict__ lut_g,
+                                                          const uint8_t* __restrict__ band_g,
+                                                          uint64_t seed, uint64_t offset) {
+    using E = Elem<DT>;
+    constexpr int V = E::V;
+    constexpr int G = BS / V;
+    static_assert(G >= 1 && G <= 8, "group size");
+    __shared__ float lut_s[kLutSize];
+    __shared__ uint32_t band_w[kBandSize / 4];
+    stage_tables(lut_s, band_w, lut_g, band_g);
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+
+    const u32x4* xv = reinterpret_cast<const u32x4*>(x);
+    u32x4* yv = reinterpret_cast<u32x4*>(y);
+    const int tid = threadIdx.x;
+    const int64_t step = (int64_t)gridDim.x * (kThreads * kUnroll);
+    for (int64_t base = (int64_t)blockIdx.x * (kThreads * kUnroll); base < n_vec; base += step) {
+        u32x4 raw[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            int64_t vi = base + u * kThreads + tid;
+            raw[u] = vi < n_vec ? __builtin_nontemporal_load(xv + vi) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            int64_t vi = base + u * kThreads + tid;
+            float f[V];
+            E::unpack(raw[u], f);
+            uint32_t m = 0;
+#pragma unroll
+            for (int j = 0; j < V; ++j) {
+                uint32_t a = __float_as_uint(f[j]) & 0x7fffffffu;
+                m = m > a ? m : a;
+            }
+            m = group_umax<G>(m);
+            FqScale s = fq_scale(m, band_s);
+            float o[V];
+#pragma unroll
+            for (int j = 0; j < V; ++j) {
+                float uu = STOCH ? dither_uniform(seed, offset + (uint64_t)(vi * V + j)) : 0.0f;
+                o[j] = fq_value(f[j], s, lut_s, STOCH, uu);
+            }
+            if (vi < n_vec) __builtin_nontemporal_store(E::pack(o), yv + vi);
+        }
+    }
+}
+
+template <int DT, int BS, bool STOCH>
+__global__ __launch_bounds__(kThreads) void fq_scalar_kernel(const typename Elem<DT>::S* x,
+                                                             typename Elem<DT>::S* y, int64_t rows,
+                                                             int64_t cols, int64_t nblk,
+                                                             const float* __restrict__ lut_g,
+                                                             const uint8_t* __restrict__ band_g,
+                                                             uint64_t seed, uint64_t offset) {
+    using E = Elem<DT>;
+    __shared__ float lut_s[kLutSize];
+    __shared__ uint32_t band_w[kBandSize / 4];
+    stage_tables(lut_s, band_w, lut_g, band_g);
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+
+    constexpr int BPW = 64 / BS;  // blocks per wave and iteration
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t total = rows * nblk;
+    const int64_t wstep = (int64_t)gridDim.x * (kThreads / 64) * BPW;
+    for (int64_t wb = ((int64_t)blockIdx.x * (kThreads / 64) + wave) * BPW; wb < total; wb += wstep) {
+        const int64_t blk = wb + lane / BS;
+        const int j = lane % BS;
+        const bool vb = blk < total;
+        const int64_t r = vb ? blk / nblk : 0;
+        const int64_t c = (vb ? blk - r * nblk : 0) * BS + j;
+        const bool valid = vb && c < cols;
+        const int64_t gi = r * cols + c;
+        float f = valid ? E::to_f(x[gi]) : 0.0f;
+        uint32_t m = group_umax_shfl<BS>(__float_as_uint(f) & 0x7fffffffu);
+        FqScale s = fq_scale(m, band_s);
+        float uu = STOCH ? dither_uniform(seed, offset + (uint64_t)gi) : 0.0f;
+        float o = fq_value(f, s, lut_s, STOCH, uu);
+        if (valid) y[gi] = E::from_f(o);
+    }
+}
+
+// ---- quantize / dequantize -------------------------------------------------
+
+// quantize_unified (quantize_unified.py:211-282): shared exponent
+// e = clamp(floor(log2(amax)) + 1 + 127, 0, 255) (0 for zero blocks and for
+// NaN / inf amax, whose int32 cast is INT_MIN), scale = 2^(e-127),
+// idx as above with the normalised value clamped to [0, 1], code =
+// reverse_lut[idx], sign = x < 0.  Optionally also writes FQ(x).
+template <int DT, int BS, bool STOCH>
+__global__ __launch_bounds__(kThreads) void quantize_kernel(
+    const typename Elem<DT>::S* x, int64_t rows, int64_t cols, int64_t nblk,
+    const float* __restrict__ lut_g, const uint8_t* __restrict__ band_g,
+    const uint8_t* __restrict__ rev_g, uint64_t seed, uint64_t offset, uint8_t* __restrict__ exps,
+    uint8_t* __restrict__ codes, uint8_t* __restrict__ signs, typename Elem<DT>::S* fq) {
+    using E = Elem<DT>;
+    __shared__ float lut_s[kLutSize];
+    __shared__ uint32_t band_w[kBandSize / 4];
+    __shared__ uint8_t rev_s[kLutSize];
+    reinterpret_cast<uint32_t*>(rev_s)[threadIdx.x] = reinterpret_cast<const uint32_t*>(rev_g)[threadIdx.x];
+    stage_tables(lut_s, band_w, lut_g, band_g);
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+
+    constexpr int BPW = 64 / BS;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t total = rows * nblk;
+    const int64_t wstep = (int64_t)gridDim.x * (kThreads / 64) * BPW;
+    for (int64_t wb = ((int64_t)blockIdx.x * (kThreads / 64) + wave) * BPW; wb < total; wb += wstep) {
+        const int64_t blk = wb + lane / BS;
+        const int j = lane % BS;
+        const bool vb = blk < total;
+        const int64_t r = vb ? blk / nblk : 0;
+        const int64_t c = (vb ? blk - r * nblk : 0) * BS + j;
+        const bool valid = vb && c < cols;
+        const int64_t gi = r * cols + c;
+        float f = valid ? E::to_f(x[gi]) : 0.0f;
+        uint32_t ab = __float_as_uint(f) & 0x7fffffffu;
+        uint32_t m = group_umax_shfl<BS>(ab);
+        float uu = STOCH ? dither_uniform(seed, offset + (uint64_t)gi) : 0.0f;
+
+        // shared exponent
+        int e = (m == 0u || m >= kInfBits) ? 0 : floor_log2_torch(m, band_s) + 1 + kExpBias;
+        e = e < 0 ? 0 : (e > 255 ? 255 : e);
+        const int se = e - kExpBias;               // scale = 2^se, se in [-127, 128]
+        float n;
+        if (se >= 128) n = ab >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;   // x / inf
+        else n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -se);
+        n = (n > 1.0f) ? 1.0f : n;                 // clamp(0, 1); NaN passes through
+        const int idx = lut_index(n, STOCH, uu);
+        if (vb) {
+            const int64_t o = blk * BS + j;
+            codes[o] = rev_s[idx];
+            if (signs) signs[o] = f < 0.0f ? 1 : 0;
+            if (j == 0) exps[blk] = (uint8_t)e;
+        }
+        if (fq) {
+            FqScale s = fq_scale(m, band_s);
+            float v = fq_value(f, s, lut_s, STOCH, uu);
+            if (valid) fq[gi] = E::from_f(v);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t* __restrict__ exps,
+                                                              const uint8_t* __restrict__ codes,
+                                                              const uint8_t* __restrict__ signs,
+                                                              float* __restrict__ y, int64_t rows,
+                                                              int64_t cols, int64_t nblk, int bs,
+                                                              const float* __restrict__ cb_g) {
+    __shared__ float cb[kLevels];
+    if (threadIdx.x < kLevels) cb[threadIdx.x] = cb_g[threadIdx.x];
+    __syncthreads();
+    const int64_t total = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kThreads) {
+        const int64_t r = i / cols;
+        const int64_t c = i - r * cols;
+        const int64_t b = c / bs;
+        const float scale = pow2_float((int)exps[r * nblk + b] - kExpBias);
+        const int64_t o = r * nblk * bs + c;
+        const float v = cb[codes[o] & 31] * scale;
+        y[i] = (signs && signs[o]) ? -v : v;
+    }
+}
+
+// ---- launch helpers ---------------------------------------------------------
+
+int num_cus() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// Workgroups per CU the grid-stride kernels are capped at (tunable through
+// AXS6_FQ_WG_PER_CU for launch-shape sweeps; default 8).
+int wg_per_cu() {
+    static int v = [] {
+        const char* s = getenv("AXS6_FQ_WG_PER_CU");
+        int n = s ? atoi(s) : 0;
+        return (n > 0 && n <= 1024) ? n : 8;
+    }();
+    return v;
+}
+
+int64_t capped_grid(int64_t work_items, int64_t per_wg) {
+    int64_t need = (work_items + per_wg - 1) / per_wg;
+    int64_t cap = (int64_t)num_cus() * wg_per_cu();
+    if (need < 1) need = 1;
+    return need < cap ? need : cap;
+}
+
+template <int DT, int BS>
+void launch_fq_typed(const void* x, void* y, int64_t rows, int64_t cols, bool stochastic, uint64_t seed,
+                     uint64_t offset, const DeviceTables& t, hipStream_t st) {
+    using S = typename Elem<DT>::S;
+    constexpr int V = Elem<DT>::V;
+    const bool aligned = (cols % BS == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
+    if (aligned) {
+        const int64_t n_vec = rows * cols / V;
+        const dim3 grid((unsigned)capped_grid(n_vec, (int64_t)kThreads * kUnroll));
+        if (stochastic)
+            fq_vec_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, seed, offset);
+        else
+            fq_vec_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, seed, offset);
+    } else {
+        const int64_t nblk = (cols + BS - 1) / BS;
+        const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));
+        if (stochastic)
+            fq_scalar_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, seed, offset);
+        else
+            fq_scalar_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, seed, offset);
+    }
+}
+
+template <int DT>
+void launch_fq(const void* x, void* y, int64_t rows, int64_t cols, int bs, bool stochastic, uint64_t seed,
+               uint64_t offset, const DeviceTables& t, hipStream_t st) {
+    if (bs == 8) launch_fq_typed<DT, 8>(x, y, rows, cols, stochastic, seed, offset, t, st);
+    else if (bs == 16) launch_fq_typed<DT, 16>(x, y, rows, cols, stochastic, seed, offset, t, st);
+    else launch_fq_typed<DT, 32>(x, y, rows, cols, stochastic, seed, offset, t, st);
+}
+
+template <int DT, int BS>
+void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochastic, uint64_t seed,
+                        uint64_t offset, uint8_t* exps, uint8_t* codes, uint8_t* signs, void* fq,
+                        const DeviceTables& t, hipStream_t st) {
+    using S = typename Elem<DT>::S;
+    const int64_t nblk = (cols + BS - 1) / BS;
+    const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));
+    if (stochastic)
+        quantize_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, seed, offset, exps, codes, signs, (S*)fq);
+    else
+        quantize_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, seed, offset, exps, codes, signs, (S*)fq);
+}
+
+template <int DT>
+void launch_quant(const void* x, int64_t rows, int64_t cols, int bs, bool stochastic, uint64_t seed,
+                  uint64_t offset, uint8_t* exps, uint8_t* codes, uint8_t* signs, void* fq,
+                  const DeviceTables& t, hipStream_t st) {
+    if (bs == 8) launch_quant_typed<DT, 8>(x, rows, cols, stochastic, seed, offset, exps, codes, signs, fq, t, st);
+    else if (bs == 16) launch_quant_typed<DT, 16>(x, rows, cols, stochastic, seed, offset, exps, codes, signs, fq, t, st);
+    else launch_quant_typed<DT, 32>(x, rows, cols, stochastic, seed, offset, exps, codes, signs, fq, t, st);
+}
+
+int check_shape(const char* fn, int64_t rows, int64_t cols, int bs) {
+    if (!valid_block(bs)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: block_size must be 8, 16 or 32 (got %d)", fn, bs);
+    if (rows < 0 || cols < 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: negative shape (%lld, %lld)", fn, (long long)rows, (long long)cols);
+    if (cols > 0 && rows > ((int64_t)1 << 50) / (cols + 32))
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: tensor too large (%lld x %lld)", fn, (long long)rows, (long long)cols);
+    return AXS6_OK;
+}
+
+}  // namespace
+}  // namespace axs6
+
+using namespace axs6;
+
+extern "C" int axs6_nf5_fake_quantize(const void* x, void* y, int32_t dtype, int64_t rows, int64_t cols,
+                                      int32_t block_size, int32_t stochastic, uint64_t seed,
+                                      uint64_t offset, void* stream) {
+    const char* fn = "axs6_nf5_fake_quantize";
+    if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
+    int rc = check_shape(fn, rows, cols, block_size);
+    if (rc) return rc;
+    if (rows == 0 || cols == 0) return AXS6_OK;
+    if (!x || !y) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null tensor pointer", fn);
+    DeviceTables t;
+    if ((rc = device_tables(&t))) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == AXS6_F32) launch_fq<AXS6_F32>(x, y, rows, cols, block_size, stochastic != 0, seed, offset, t, st);
+    else if (dtype == AXS6_BF16) launch_fq<AXS6_BF16>(x, y, rows, cols, block_size, stochastic != 0, seed, offset, t, st);
+    else launch_fq<AXS6_F16>(x, y, rows, cols, block_size, stochastic != 0, seed, offset, t, st);
+    return check_launch(fn);
+}
+
+extern "C" int axs6_nf5_quantize(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
+                                 int32_t stochastic, uint64_t seed, uint64_t offset, uint8_t* exponents,
+                                 uint8_t* codes, uint8_t* signs, void* fq, void* stream) {
+    const char* fn = "axs6_nf5_quantize";
+    if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
+    int rc = check_shape(fn, rows, cols, block_size);
+    if (rc) return rc;
+    if (rows == 0 || cols == 0) return AXS6_OK;
+    if (!x || !exponents || !codes) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null tensor pointer", fn);
+    DeviceTables t;
+    if ((rc = device_tables(&t))) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == AXS6_F32) launch_quant<AXS6_F32>(x, rows, cols, block_size, stochastic != 0, seed, offset, exponents, codes, signs, fq, t, st);
+    else if (dtype == AXS6_BF16) launch_quant<AXS6_BF16>(x, rows, cols, block_size, stochastic != 0, seed, offset, exponents, codes, signs, fq, t, st);
+    else launch_quant<AXS6_F16>(x, rows, cols, block_size, stochastic != 0, seed, offset, exponents, codes, signs, fq, t, st);
+    return check_launch(fn);
+}
+
+extern "C" int axs6_nf5_dequantize(const uint8_t* exponents, const uint8_t* codes, const uint8_t* signs, float* y,
+                                   int64_t rows, int64_t cols, int32_t block_size, void* stream) {
+    const char* fn = "axs6_nf5_dequantize";
+    int rc = check_shape(fn, rows, cols, block_size);
+    if (rc) return rc;
+    if (rows == 0 || cols == 0) return AXS6_OK;
+    if (!exponents || !codes || !y) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null tensor pointer", fn);
+    DeviceTables t;
+    if ((rc = device_tables(&t))) return rc;
+    const int64_t nblk = (cols + block_size - 1) / block_size;
+    const dim3 grid((unsigned)capped_grid(rows * cols, kThreads));
+    dequantize_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(exponents, codes, signs, y, rows, cols, nblk,
+                                                                  block_size, t.codebook);
+    return check_launch(fn);
+}

@@ -1,0 +1,240 @@
+#!/usr/bin/env python3
+"""Benchmark of the AXS-6 NF5 hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-linear]
+
+Workload (BASELINE.json metric "NF5 fake-quant GB/s @8192x4096 fp32; AXS-6
+linear TFLOP/s @4096^3 bf16"):
+  * headline ("value"): NF5 fake-quantize forward + STE backward of one
+    8192x4096 fp32 tensor (config 2's largest shape, N(0,1) with 1% x100
+    outliers).  One step = one fake-quantize pass; the STE backward is the
+    identity and launches nothing.  Algorithmic bytes per step = 8 B/elem
+    (4 read + 4 written) = 268,435,456 B.
+  * "linear": the fused AXS-6 linear forward at M=N=K=4096 (config 3), FLOPs
+    per step = 2*M*N*K, timed the same way.
+Inputs are synthetic, resident in HBM before the timed region.  K steps are
+timed between device synchronisations; per-kernel time comes from HIP events
+on the stream the kernels run on (torch's current stream).
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "axs-6_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E, published
+BF16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 MFMA, published
+
+FQ_SHAPE = (8192, 4096)
+LIN_SHAPE = (4096, 4096, 4096)   # M, K, N
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return platform.processor() or "unknown"
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (profiles/<name>)."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def time_steps(fn, steps: int, warmup: int):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        fn()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    wall_ms = (t1 - t0) * 1e3 / steps
+    gpu_ms = ev0.elapsed_time(ev1) / steps
+    return wall_ms, gpu_ms
+
+
+def bench_fq(steps: int, warmup: int):
+    import torch
+
+    from axs.unified.functional_unified import fake_quantize_unified
+
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(*FQ_SHAPE, device="cuda", generator=g)
+    m = torch.rand(*FQ_SHAPE, device="cuda", generator=g) < 0.01
+    x[m] *= 100.0
+    x.requires_grad_(True)
+    grad = torch.randn(*FQ_SHAPE, device="cuda", generator=g)
+
+    def step():
+        y = fake_quantize_unified(x, 32, "nearest")
+        y.backward(grad)   # STE: identity, no kernel
+
+    wall_ms, gpu_ms = time_steps(step, steps, warmup)
+    nbytes = 8 * x.numel()
+    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "bytes": nbytes}
+
+
+def bench_linear(steps: int, warmup: int):
+    import torch
+
+    from axs.unified import hip_linear
+
+    M, K, N = LIN_SHAPE
+    g = torch.Generator(device="cuda").manual_seed(4)
+    X = torch.randn(M, K, device="cuda", generator=g)
+    W = torch.randn(N, K, device="cuda", generator=g) * K ** -0.5
+    b = torch.zeros(N, device="cuda")
+
+    def step():
+        hip_linear.linear_forward(X, W, b, 32, True)
+
+    wall_ms, gpu_ms = time_steps(step, steps, warmup)
+    kern = hip_linear.last_forward_kernel_times(X, W, b, reps=max(steps, 10))
+    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "flops": 2.0 * M * N * K, "kernels": kern}
+
+
+def cpu_baseline_fq(budget_s: float = 12.0):
+    import torch
+
+    from oracle import eager_torch
+
+    torch.set_num_threads(torch.get_num_threads())
+    threads = torch.get_num_threads()
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(*FQ_SHAPE, generator=g)
+    m = torch.rand(*FQ_SHAPE, generator=g) < 0.01
+    x[m] *= 100.0
+    eager_torch.fake_quantize(x, 32)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 10 and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        eager_torch.fake_quantize(x, 32)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(8 * x.numel() / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"torch-eager restatement of the reference's fused_fake_quantize "
+                   f"(oracle/eager_torch.py) on the full 8192x4096 fp32 tensor, median of "
+                   f"{len(times)} calls after 1 warm-up, {threads} threads, {cpu_model()}; "
+                   f"{med * 1e3:.1f} ms/call"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-linear", action="store_true")
+    a = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (got --gpus {a.gpus}, WORLD_SIZE {world}); the NF5 "
+              "fake-quantize shards by rows with no exchange, so N GPUs run N copies of this "
+              "workload.  Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    log(f"device: {torch.cuda.get_device_name()}  steps={a.steps} warmup={a.warmup}")
+
+    fq = bench_fq(a.steps, a.warmup)
+    gbs = fq["bytes"] / (fq["wall_ms"] * 1e-3) / 1e9
+    achieved = fq["bytes"] / (fq["gpu_ms"] * 1e-3) / 1e9
+    log(f"fq 8192x4096: {fq['wall_ms']*1e3:.1f} us/step wall, {fq['gpu_ms']*1e3:.1f} us/launch, "
+        f"{achieved:.0f} GB/s")
+    traffic = load_traffic("fq_8192x4096_traffic.json")
+    out = {
+        "metric": "NF5 fake-quant GB/s @8192x4096 fp32; AXS-6 linear TFLOP/s @4096^3 bf16",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(fq["wall_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: N(0,1) with 1% of elements x100, seeded",
+        "config": {"workload": "NF5 fake-quantize fwd + STE bwd, 8192x4096 fp32, block 32",
+                   "shape": list(FQ_SHAPE), "block_size": 32},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic},
+    }
+
+    if not a.no_linear:
+        try:
+            lin = bench_linear(max(a.steps // 2, 10), max(a.warmup // 2, 3))
+            tflops = lin["flops"] / (lin["wall_ms"] * 1e-3) / 1e12
+            log(f"linear 4096^3 fwd: {lin['wall_ms']*1e3:.1f} us/step, {tflops:.0f} TFLOP/s")
+            k = lin["kernels"]
+            gemm_tf = lin["flops"] / (k["gemm_ms"] * 1e-3) / 1e12 if k.get("gemm_ms") else None
+            out["linear"] = {
+                "metric": "AXS-6 linear forward TFLOP/s @4096^3",
+                "value": round(tflops, 1), "unit": "TFLOP/s",
+                "ms_per_step": round(lin["wall_ms"], 5),
+                "dtype": k.get("compute_dtype"),
+                "kernels_ms": {kk: round(v, 5) for kk, v in k.items() if kk.endswith("_ms")},
+                "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1) if gemm_tf else None,
+                             "peak": BF16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(gemm_tf / BF16_DENSE_PEAK_TFLOPS, 4) if gemm_tf else None,
+                             "end_to_end_frac": round(tflops / BF16_DENSE_PEAK_TFLOPS, 4),
+                             "traffic": load_traffic("linear_4096_traffic.json")},
+            }
+        except NotImplementedError as e:
+            log(f"linear: skipped ({e})")
+
+    if not a.no_cpu_baseline:
+        log("cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline_fq()
+        log(f"cpu baseline: {out['cpu_baseline']['value']} GB/s")
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,107 @@
+"""The C-ABI library loads, exports every entry point include/axs6.h
+declares, carries the same constant tables as the oracle, and rejects bad
+arguments before touching a device (no compute calls: runs without a GPU)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch  # noqa: F401  (loads the HIP runtime libaxs6 binds to)
+
+import oracle
+from axs import _lib
+from conftest import ROOT, bits_equal
+
+
+def declared_symbols() -> list[str]:
+    names = []
+    for f in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if f.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", f)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names += re.findall(r"\b(axs6_\w+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_symbols()
+    assert "axs6_nf5_fake_quantize" in names
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_every_declared_symbol_has_a_binding_signature():
+    names = set(declared_symbols()) - {"axs6_version", "axs6_last_error"}
+    assert names <= set(_lib._SIGNATURES), sorted(names - set(_lib._SIGNATURES))
+
+
+def test_version_string():
+    assert "gfx950" in _lib.version()
+
+
+def test_tables_match_oracle():
+    cb, lut, rev, band = _lib.host_tables()
+    ocb, olut, orev = oracle.tables()
+    assert bits_equal(cb.numpy(), ocb)
+    assert bits_equal(lut.numpy(), olut)
+    assert np.array_equal(rev.numpy(), orev)
+    # band[k+149]: floats just below 2^k whose floor(log2) is k, by the oracle
+    want = np.zeros(278, np.uint8)
+    for k in range(-148, 129):
+        top = (k + 127) << 23 if k >= -126 else 1 << (k + 149)
+        xs = np.arange(max(top - 64, 1), top, dtype=np.uint32)[::-1].view(np.float32)
+        fl = oracle.floor_log2(xs)
+        n = 0
+        for v in fl:
+            if v == k:
+                n += 1
+            else:
+                break
+        want[k + 149] = n
+    assert np.array_equal(band.numpy(), want)
+    assert band[127 + 149] == 44 and band[0 + 149] == 0
+
+
+def test_band_matches_torch_log2_directly():
+    _, _, _, band = _lib.host_tables()
+    for k in (-130, -126, -100, -64, -63, -4, -2, 3, 8, 9, 17, 33, 64, 65, 127, 128):
+        top = (k + 127) << 23 if k >= -126 else 1 << (k + 149)
+        c = int(band[k + 149])
+        inside = np.array([top - m for m in range(1, c + 1)], np.uint32).view(np.float32)
+        outside = np.array([top - c - 1], np.uint32).view(np.float32)
+        if c:
+            assert np.all(torch.floor(torch.log2(torch.from_numpy(inside))).numpy() == k)
+        assert torch.floor(torch.log2(torch.from_numpy(outside))).item() == k - 1
+
+
+def _status(name, *args):
+    fn = getattr(_lib.lib(), name)
+    rc = fn(*args)
+    return rc, _lib.lib().axs6_last_error().decode()
+
+
+def test_invalid_arguments_rejected_without_device():
+    rc, msg = _status("axs6_nf5_fake_quantize", 1, 1, 0, 4, 32, 17, 0, 0, 0, None)
+    assert rc == 1 and "block_size" in msg
+    rc, msg = _status("axs6_nf5_fake_quantize", 1, 1, 9, 4, 32, 32, 0, 0, 0, None)
+    assert rc == 1 and "dtype" in msg
+    rc, msg = _status("axs6_nf5_fake_quantize", 1, 1, 0, -1, 32, 32, 0, 0, 0, None)
+    assert rc == 1 and "negative" in msg
+    rc, msg = _status("axs6_nf5_fake_quantize", None, None, 0, 4, 32, 32, 0, 0, 0, None)
+    assert rc == 1 and "null" in msg
+    # empty tensors are a no-op, not an error
+    rc, _ = _status("axs6_nf5_fake_quantize", None, None, 0, 0, 32, 32, 0, 0, 0, None)
+    assert rc == 0
+    rc, msg = _status("axs6_nf5_quantize", 1, 0, 4, 32, 12, 0, 0, 0, 1, 1, None, None, None)
+    assert rc == 1 and "block_size" in msg
+    rc, msg = _status("axs6_nf5_dequantize", 1, 1, None, 1, 4, 32, 7, None)
+    assert rc == 1
+
+
+def test_error_raises_runtime_error():
+    with pytest.raises(RuntimeError, match="block_size"):
+        _lib.call("axs6_nf5_fake_quantize", 1, 1, 0, 4, 32, 17, 0, 0, 0, None)

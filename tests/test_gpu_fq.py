@@ -1,0 +1,228 @@
+"""GPU parity of the NF5 fake-quantize / quantize / dequantize kernels
+against the CPU oracle and the golden vectors: bit-exact (NaN matched by
+position), per BASELINE configs 1-2 and the reference's own test cases
+(tests/test_triton_kernels.py:78-259 of the reference)."""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import bits_equal, first_mismatch, load_golden
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _fq(x: torch.Tensor, bs=32, rounding="nearest", seed=None) -> torch.Tensor:
+    from axs.unified.hip_kernels import hip_fused_fake_quantize
+
+    return hip_fused_fake_quantize(x, bs, rounding, seed=seed)
+
+
+def config2_input(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, generator=g)
+    m = torch.rand(*shape, generator=g) < 0.01
+    x[m] *= 100.0
+    return x
+
+
+@pytest.mark.parametrize("shape,seed", [((256, 256), 1), ((4096, 4096), 2), ((8192, 4096), 3)],
+                         ids=["256x256", "4096x4096", "8192x4096"])
+def test_config2_fake_quantize_bitexact(shape, seed):
+    print(f"[fq config2 {shape}]", flush=True)
+    x = config2_input(shape, seed)
+    got = _fq(x.to(DEV)).cpu().numpy()
+    want = oracle.fake_quantize(x.numpy(), 32)
+    assert bits_equal(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_block_sizes_bitexact(bs):
+    x = config2_input((512, 512), 10 + bs)
+    got = _fq(x.to(DEV), bs).cpu().numpy()
+    assert bits_equal(got, oracle.fake_quantize(x.numpy(), bs))
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32])
+@pytest.mark.parametrize("unaligned", [False, True], ids=["vector", "general"])
+def test_edge_golden(bs, unaligned):
+    g = load_golden("edge_cases.npz")
+    x = torch.from_numpy(g["x"])
+    if unaligned:
+        # a view one element into a buffer forces the general (scalar) kernel
+        buf = torch.zeros(x.numel() + 1, dtype=torch.float32, device=DEV)
+        buf[1:] = x.reshape(-1).to(DEV)
+        xd = buf[1:].view(x.shape)
+        assert xd.data_ptr() % 16 != 0
+    else:
+        xd = x.to(DEV)
+    got = _fq(xd, bs).cpu().numpy()
+    want = g[f"fq_bs{bs}"]
+    assert bits_equal(got, want), first_mismatch(got, want)
+
+
+def test_ragged_golden_all_dtypes():
+    g = load_golden("ragged.npz")
+    for i in range(8):
+        x = torch.from_numpy(g[f"x{i}"])
+        for bs in (8, 16, 32):
+            got = _fq(x.to(DEV), bs).cpu().numpy()
+            assert bits_equal(got, g[f"x{i}_fq_bs{bs}"]), (i, bs, first_mismatch(got, g[f"x{i}_fq_bs{bs}"]))
+        for tag, dt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+            xin = torch.from_numpy(g[f"x{i}_in_{tag}"]).view(dt)
+            y = _fq(xin.to(DEV), 32)
+            assert y.dtype == dt and y.shape == xin.shape
+            assert np.array_equal(y.cpu().view(torch.int16).numpy(), g[f"x{i}_fq_{tag}"]), (i, tag)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_half_dtypes_vs_oracle(dt, bs):
+    x = config2_input((1024, 2048), 20 + bs).to(dt)
+    got = _fq(x.to(DEV), bs).cpu()
+    want = torch.from_numpy(oracle.fake_quantize(x.float().numpy(), bs)).to(dt)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_exponent_range_and_bands():
+    # blocks spanning the whole float32 range, incl. subnormals and overflow
+    rng = np.random.default_rng(5)
+    rows = []
+    for e in range(-160, 130, 2):
+        rows.append((rng.standard_normal(32) * 2.0 ** e).astype(np.float32))
+    for k in range(-148, 129):
+        top = (k + 127) << 23 if k >= -126 else 1 << (k + 149)
+        for d in (1, 2, 11, 22, 44, 45):
+            if d >= top:
+                continue
+            v = np.array([top - d], np.uint32).view(np.float32)[0]
+            if not np.isfinite(v):
+                continue
+            r = (rng.uniform(-1, 1, 32) * v).astype(np.float32)
+            r[rng.integers(32)] = -v if d % 2 else v
+            rows.append(r)
+    x = np.stack(rows)
+    for bs in (8, 16, 32):
+        got = _fq(torch.from_numpy(x).to(DEV), bs).cpu().numpy()
+        want = oracle.fake_quantize(x, bs)
+        assert bits_equal(got, want), (bs, first_mismatch(got, want))
+
+
+@pytest.mark.parametrize("shape", [(1024, 4096), (37, 100)], ids=["vector", "general"])
+@pytest.mark.parametrize("bs", [8, 32])
+def test_stochastic_bitexact_given_stream(shape, bs):
+    x = config2_input(shape, 40)
+    seed = 0x1234ABCD5678
+    got = _fq(x.to(DEV), bs, "stochastic", seed=seed).cpu().numpy()
+    want = oracle.fake_quantize(x.numpy(), bs, oracle.uniform(seed, 0, x.numel()))
+    assert bits_equal(got, want), first_mismatch(got, want)
+
+
+def test_stochastic_statistics():
+    torch.manual_seed(0)
+    x = torch.randn(1024, 1024, device=DEV)
+    nearest = _fq(x)
+    sto = _fq(x, rounding="stochastic")
+    assert not torch.equal(nearest, sto)
+    ratio = ((x - sto).pow(2).mean() / (x - nearest).pow(2).mean()).item()
+    assert 0.5 < ratio < 2.0, ratio
+    xs = torch.randn(256, 256, device=DEV)
+    errs = [(xs - _fq(xs, rounding="stochastic")).mean().item() for _ in range(20)]
+    assert abs(sum(errs) / len(errs)) < 0.01
+    # same seed reproduces, different seeds differ
+    assert torch.equal(_fq(x, rounding="stochastic", seed=7), _fq(x, rounding="stochastic", seed=7))
+    assert not torch.equal(_fq(x, rounding="stochastic", seed=7), _fq(x, rounding="stochastic", seed=8))
+
+
+@pytest.mark.parametrize("shape", [(64,), (32, 64), (4, 8, 16), (2, 3, 4, 32), (7, 13), (3, 100, 17)])
+def test_shape_dtype_device_preserved(shape):
+    x = torch.randn(*shape, device=DEV)
+    y = _fq(x)
+    assert y.shape == x.shape and y.dtype == x.dtype and y.device == x.device
+    assert bits_equal(y.cpu().numpy(), oracle.fake_quantize(x.cpu().numpy(), 32))
+
+
+def test_non_contiguous_and_float64():
+    x = torch.randn(96, 64, device=DEV).t()
+    assert not x.is_contiguous()
+    assert bits_equal(_fq(x).cpu().numpy(), oracle.fake_quantize(x.cpu().contiguous().numpy(), 32))
+    xd = torch.randn(16, 64, dtype=torch.float64, device=DEV)
+    y = _fq(xd)
+    assert y.dtype == torch.float64
+    want = oracle.fake_quantize(xd.float().cpu().numpy(), 32).astype(np.float64)
+    assert bits_equal(y.cpu().numpy(), want)
+
+
+def test_zero_and_empty():
+    z = torch.zeros(128, 128, device=DEV)
+    assert (_fq(z) == 0).all()
+    e = torch.zeros(0, 32, device=DEV)
+    assert _fq(e).shape == (0, 32)
+
+
+# ------------------------------------------------------------- quantize --
+
+def _quant(x: torch.Tensor, bs=32, rounding="nearest", seed=None):
+    from axs.unified.hip_kernels import hip_quantize
+
+    e, c, s, fq = hip_quantize(x, bs, rounding, with_fake_quantized=True, seed=seed)
+    return e.cpu().numpy(), c.cpu().numpy(), s.cpu().numpy(), fq.cpu().numpy()
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_quantize_edge_golden(bs):
+    g = load_golden("edge_cases.npz")
+    e, c, s, fq = _quant(torch.from_numpy(g["x"]).to(DEV), bs)
+    assert np.array_equal(e, g[f"exp_bs{bs}"]), first_mismatch(e, g[f"exp_bs{bs}"])
+    assert np.array_equal(c, g[f"code_bs{bs}"])
+    assert np.array_equal(s, g[f"sign_bs{bs}"])
+    assert bits_equal(fq, g[f"fq_bs{bs}"])
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32])
+@pytest.mark.parametrize("shape", [(300, 256), (37, 100)])
+def test_quantize_vs_oracle(bs, shape):
+    x = config2_input(shape, 60 + bs)
+    x[0, :5] = torch.tensor([float("nan"), 0.0, -0.0, 1e-40, -3e38])
+    for rounding, seed in (("nearest", None), ("stochastic", 99)):
+        e, c, s, fq = _quant(x.to(DEV), bs, rounding, seed)
+        u = oracle.uniform(seed, 0, x.numel()) if seed else None
+        oe, oc, os_ = oracle.quantize(x.numpy(), bs, u)
+        assert np.array_equal(e, oe) and np.array_equal(c, oc) and np.array_equal(s, os_)
+        assert bits_equal(fq, oracle.fake_quantize(x.numpy(), bs, u))
+
+
+def test_config1_golden():
+    g = load_golden("config1.npz")
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(1024, 1024, generator=gen) * 0.02
+    sha = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()  # noqa: E731
+    e, c, s, fq = _quant(x.to(DEV), 32)
+    oe, oc, os_ = oracle.quantize(x.numpy(), 32)
+    assert np.array_equal(e, oe) and np.array_equal(c, oc) and np.array_equal(s, os_)
+    assert bits_equal(fq, oracle.fake_quantize(x.numpy(), 32))
+    if sha(x.numpy()) == str(g["input_sha"]):
+        assert np.array_equal(e, g["exps"])
+        assert sha(c) == str(g["codes_sha"]) and sha(s) == str(g["signs_sha"])
+        assert sha(fq) == str(g["fq_sha"])
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_dequantize_vs_oracle(bs):
+    from axs.unified.quantize_unified import dequantize_unified, quantize_unified
+
+    x = config2_input((200, 96 + 5), 80 + bs)
+    q = quantize_unified(x.to(DEV), bs)
+    d = dequantize_unified(q).cpu().numpy()
+    oe, oc, os_ = oracle.quantize(x.numpy(), bs)
+    want = oracle.dequantize(oe, oc, os_, x.shape[1], bs)
+    assert bits_equal(d, want), first_mismatch(d, want)
+    g = load_golden("edge_cases.npz")
+    q = quantize_unified(torch.from_numpy(g["x"]).to(DEV), bs)
+    assert bits_equal(dequantize_unified(q).cpu().numpy(), g[f"deq_bs{bs}"])
