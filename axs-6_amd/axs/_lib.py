@@ -38,7 +38,17 @@ _SIGNATURES: dict[str, list] = {
     "axs6_nf5_fake_quantize": [_vp, _vp, _i32, _i64, _i64, _i32, _i32, _u64, _u64, _vp],
     "axs6_nf5_quantize": [_vp, _i32, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _vp, _vp, _vp],
     "axs6_nf5_dequantize": [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
+    "axs6_linear_padded_k": [_i64],
+    "axs6_nf5_pack_rows": [_vp, _i32, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _i64, _i64, _vp, _vp],
+    "axs6_gemm_f16_nt": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i32, _vp],
+    "axs6_nf5_linear_forward": [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp,
+                                _vp, _vp],
+    "axs6_nf5_linear_backward_workspace": [_i64, _i64, _i64, _i32, _i32, _i32],
+    "axs6_nf5_linear_backward": [_vp, _i32, _i64, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _vp, _vp,
+                                 _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp],
 }
+# entry points that return a value rather than an axs6_status
+_RESTYPES = {"axs6_linear_padded_k": _i64, "axs6_nf5_linear_backward_workspace": ctypes.c_size_t}
 
 
 class LibraryError(RuntimeError):
@@ -67,7 +77,7 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(L, name, None)
                 if fn is not None:
                     fn.argtypes = argt
-                    fn.restype = ctypes.c_int
+                    fn.restype = _RESTYPES.get(name, ctypes.c_int)
             _lib = L
     return _lib
 

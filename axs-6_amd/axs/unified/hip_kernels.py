@@ -162,3 +162,25 @@ def hip_dequantize(exps: torch.Tensor, codes: torch.Tensor, signs: torch.Tensor 
             _lib.call("axs6_nf5_dequantize", e.data_ptr(), c.data_ptr(), _lib.ptr(s), y.data_ptr(),
                       rows, cols, block_size, _lib.stream_of(c))
     return y
+
+
+def hip_fused_linear(
+    input: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    block_size: int = DEFAULT_BLOCK_SIZE,
+    quantize_input: bool = True,
+) -> torch.Tensor:
+    """``FQ(input) @ FQ(weight).T + bias`` on the fused HIP linear, for the
+    argument conventions of the reference's ``triton_fused_linear``
+    (``axs/unified/triton_kernels.py:385-482``): CUDA tensors only,
+    ``block_size`` must be 32 (ValueError otherwise), output in the input's
+    dtype."""
+    if not input.is_cuda:
+        raise RuntimeError("hip_fused_linear requires CUDA (ROCm/HIP) tensors")
+    if block_size != 32:
+        raise ValueError(f"hip_fused_linear requires block_size=32, got {block_size}. "
+                         "Use accelerated_linear for other block sizes.")
+    from axs.unified import hip_linear
+
+    return hip_linear.linear_forward(input, weight, bias, block_size, quantize_input)

@@ -1,14 +1,234 @@
-"""Quantized linear on the HIP GEMM (filled in with the GEMM kernels)."""
+"""Quantized linear and matmul on the HIP kernels of libaxs6.so.
+
+``forward_train`` / ``backward`` implement the reference's
+``_AXSLinearUnifiedFunction`` (``axs/unified/functional_unified.py:107-170``);
+``linear_forward`` is ``accelerated_linear`` (``axs/unified/backend.py:540``)
+and ``matmul`` is ``accelerated_matmul`` (``backend.py:621``).
+
+The GEMMs run on fp16 MFMA with operands packed as power-of-two-scaled fp16
+rows (see include/axs6.h); results are float32-accumulated and land within
+rel-L2 ~3e-4 of the fp32 product of the fake-quantized operands.
+Ragged K or N (not a multiple of the block size) are zero-padded on the
+device first -- NF5 pads the last block with zeros, so this changes nothing.
+"""
 from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from axs import _lib
+from axs.core import VALID_BLOCK_SIZES
+from axs.unified.hip_kernels import _on_device, _require_device, next_seed
+
+_SUPPORTED = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _lib_sigs():
+    return _lib.lib()
+
+
+def padded_k(k: int) -> int:
+    return int(_lib_sigs().axs6_linear_padded_k(k))
+
+
+def _pad_last(t: torch.Tensor, mult: int) -> torch.Tensor:
+    pad = (-t.shape[-1]) % mult
+    return F.pad(t, (0, pad)) if pad else t
+
+
+def _pad_rows(t: torch.Tensor, mult: int) -> torch.Tensor:
+    pad = (-t.shape[0]) % mult
+    return F.pad(t, (0, 0, 0, pad)) if pad else t
+
+
+class Saved:
+    """Packed operands of a forward, kept for its backward."""
+
+    def __init__(self, xq, sx, wq, sw, M, N, K, n_true, k_true, dtype, x_shape, w_dtype):
+        self.xq, self.sx, self.wq, self.sw = xq, sx, wq, sw
+        self.M, self.N, self.K = M, N, K
+        self.n_true, self.k_true = n_true, k_true
+        self.dtype, self.x_shape, self.w_dtype = dtype, x_shape, w_dtype
+
+    def tensors(self):
+        return (self.xq, self.sx, self.wq, self.sw)
+
+    def meta(self):
+        return (self.M, self.N, self.K, self.n_true, self.k_true, self.dtype, self.x_shape, self.w_dtype)
+
+    @staticmethod
+    def restore(tensors, meta) -> "Saved":
+        return Saved(*tensors, *meta)
+
+
+def _forward(input, weight, bias, block_size, quantize_input):
+    fn = "axs_linear"
+    _require_device(input, fn)
+    _require_device(weight, fn)
+    assert block_size in VALID_BLOCK_SIZES, f"block_size must be one of {VALID_BLOCK_SIZES}"
+    K = input.shape[-1]
+    N, Kw = weight.shape
+    if Kw != K:
+        raise RuntimeError(f"{fn}: input has {K} features but weight expects {Kw}")
+    dtype = input.dtype if input.dtype in _SUPPORTED else torch.float32
+    x2 = input.reshape(-1, K).to(dtype)
+    w2 = weight.to(dtype)
+    k_true, n_true = K, N
+    x2 = _pad_last(x2, block_size).contiguous()
+    w2 = _pad_rows(_pad_last(w2, block_size), block_size).contiguous()
+    M, Kb = x2.shape
+    Nb = w2.shape[0]
+    b = None
+    if bias is not None:
+        b = bias.to(torch.float32)
+        if Nb != N:
+            b = F.pad(b, (0, Nb - N))
+        b = b.contiguous()
+    Kp = padded_k(Kb)
+    dev = x2.device
+    xq = torch.empty((M, Kp), dtype=torch.float16, device=dev)
+    wq = torch.empty((Nb, Kp), dtype=torch.float16, device=dev)
+    sx = torch.empty((M,), dtype=torch.int32, device=dev)
+    sw = torch.empty((Nb,), dtype=torch.int32, device=dev)
+    y = torch.empty((M, Nb), dtype=dtype, device=dev)
+    if M and Nb:
+        with _on_device(x2):
+            _lib.call("axs6_nf5_linear_forward", x2.data_ptr(), w2.data_ptr(), _lib.ptr(b), y.data_ptr(),
+                      _lib.DTYPE_CODE[dtype], M, Nb, Kb, block_size, int(bool(quantize_input)),
+                      xq.data_ptr(), sx.data_ptr(), wq.data_ptr(), sw.data_ptr(), _lib.stream_of(x2))
+    if Nb != N:
+        y = y[:, :N]
+    out = y.reshape(*input.shape[:-1], N)
+    saved = Saved(xq, sx, wq, sw, M, Nb, Kb, n_true, k_true, dtype, tuple(input.shape), weight.dtype)
+    return out, saved
+
+
+def forward_train(input, weight, bias, block_size=32, quantize_input=True):
+    """(Y, Saved) -- Y = FQ(input) FQ(weight)^T + bias."""
+    return _forward(input, weight, bias, block_size, quantize_input)
 
 
 def linear_forward(input, weight, bias=None, block_size=32, quantize_input=True):
-    raise NotImplementedError("HIP quantized linear not built yet")
+    """Y = FQ(input) FQ(weight)^T + bias (no autograd bookkeeping)."""
+    out, _ = _forward(input, weight, bias, block_size, quantize_input)
+    return out if input.dtype == out.dtype or input.dtype not in _SUPPORTED else out.to(input.dtype)
 
 
-def matmul(a, b):
-    raise NotImplementedError("HIP GEMM not built yet")
+def backward(grad_output, saved: Saved, block_size: int, quantize_grad: bool,
+             need_x: bool, need_w: bool, need_b: bool, seed: int | None = None):
+    """(dX, dW, db) of the quantized linear, each None when not needed.
+    ``seed`` fixes the stochastic rounding of dY (default: a fresh draw)."""
+    M, N, K = saved.M, saved.N, saved.K
+    dev = saved.xq.device
+    dy = grad_output.reshape(-1, saved.n_true).to(saved.dtype)
+    if N != saved.n_true:
+        dy = _pad_last(dy, block_size)
+    dy = dy.contiguous()
+    dx = torch.empty((M, K), dtype=saved.dtype, device=dev) if need_x else None
+    dw = torch.empty((N, K), dtype=torch.float32, device=dev) if need_w else None
+    db = torch.empty((N,), dtype=torch.float32, device=dev) if need_b else None
+    if M and N and (need_x or need_w or need_b):
+        L = _lib_sigs()
+        ws_bytes = int(L.axs6_nf5_linear_backward_workspace(M, N, K, int(need_x), int(need_w), int(need_b)))
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+        seed = (next_seed() if seed is None else int(seed)) if quantize_grad else 0
+        with _on_device(dy):
+            _lib.call("axs6_nf5_linear_backward", dy.data_ptr(), _lib.DTYPE_CODE[saved.dtype], M, N, K,
+                      block_size, int(bool(quantize_grad)), seed, 0,
+                      saved.xq.data_ptr(), saved.sx.data_ptr(), saved.wq.data_ptr(), saved.sw.data_ptr(),
+                      _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), ws.data_ptr(), ws_bytes,
+                      _lib.stream_of(dy))
+    elif need_w:
+        dw.zero_()
+    if dx is not None:
+        if K != saved.k_true:
+            dx = dx[:, :saved.k_true]
+        dx = dx.reshape(*saved.x_shape[:-1], saved.k_true)
+    if dw is not None:
+        dw = dw[:saved.n_true, :saved.k_true]
+        if saved.w_dtype != torch.float32:
+            dw = dw.to(saved.w_dtype)
+    if db is not None:
+        db = db[:saved.n_true]
+    return dx, dw, db
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``a (*, K) @ b (K, N)`` -> float32, fp16 MFMA with per-row power-of-two
+    scaled operands (no NF5 step)."""
+    fn = "axs_matmul"
+    _require_device(a, fn)
+    _require_device(b, fn)
+    if b.dim() != 2:
+        raise RuntimeError(f"{fn}: b must be 2-D, got shape {tuple(b.shape)}")
+    K = a.shape[-1]
+    if b.shape[0] != K:
+        raise RuntimeError(f"{fn}: shapes {tuple(a.shape)} and {tuple(b.shape)} do not contract")
+    N = b.shape[1]
+    a2 = _pad_last(a.reshape(-1, K).float(), 32).contiguous()
+    bt = _pad_last(b.float().t(), 32).contiguous()          # [N, K'] rows along the contraction
+    M, Kb = a2.shape
+    Kp = padded_k(Kb)
+    dev = a2.device
+    aq = torch.empty((M, Kp), dtype=torch.float16, device=dev)
+    bq = torch.empty((N, Kp), dtype=torch.float16, device=dev)
+    sa = torch.empty((M,), dtype=torch.int32, device=dev)
+    sb = torch.empty((N,), dtype=torch.int32, device=dev)
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    if M and N:
+        st = _lib.stream_of(a2)
+        with _on_device(a2):
+            _lib.call("axs6_nf5_pack_rows", a2.data_ptr(), _lib.F32, M, Kb, 32, 0, 0, 0, None,
+                      aq.data_ptr(), Kp, Kp, sa.data_ptr(), st)
+            _lib.call("axs6_nf5_pack_rows", bt.data_ptr(), _lib.F32, N, Kb, 32, 0, 0, 0, None,
+                      bq.data_ptr(), Kp, Kp, sb.data_ptr(), st)
+            _lib.call("axs6_gemm_f16_nt", aq.data_ptr(), Kp, bq.data_ptr(), Kp, M, N, Kp,
+                      sa.data_ptr(), sb.data_ptr(), None, out.data_ptr(), N, _lib.F32, st)
+    return out.reshape(*a.shape[:-1], N)
+
+
+def last_forward_kernel_times(X, W, b, reps: int = 20) -> dict:
+    """Per-kernel device times (ms) of the forward at this shape, measured
+    with HIP events on torch's current stream: pack X, pack W, GEMM."""
+    M, K = X.shape
+    N = W.shape[0]
+    Kp = padded_k(K)
+    dev = X.device
+    xq = torch.empty((M, Kp), dtype=torch.float16, device=dev)
+    wq = torch.empty((N, Kp), dtype=torch.float16, device=dev)
+    sx = torch.empty((M,), dtype=torch.int32, device=dev)
+    sw = torch.empty((N,), dtype=torch.int32, device=dev)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    st = _lib.stream_of(X)
+    code = _lib.DTYPE_CODE[X.dtype]
+
+    def pack_x():
+        _lib.call("axs6_nf5_pack_rows", X.data_ptr(), code, M, K, 32, 1, 0, 0, None, xq.data_ptr(), Kp, Kp,
+                  sx.data_ptr(), st)
+
+    def pack_w():
+        _lib.call("axs6_nf5_pack_rows", W.data_ptr(), code, N, K, 32, 1, 0, 0, None, wq.data_ptr(), Kp, Kp,
+                  sw.data_ptr(), st)
+
+    def gemm():
+        _lib.call("axs6_gemm_f16_nt", xq.data_ptr(), Kp, wq.data_ptr(), Kp, M, N, Kp, sx.data_ptr(),
+                  sw.data_ptr(), _lib.ptr(b), y.data_ptr(), N, _lib.F32, st)
+
+    out = {"compute_dtype": "fp16 MFMA operands (power-of-two row scaled), fp32 accumulate"}
+    for name, fn in (("pack_x_ms", pack_x), ("pack_w_ms", pack_w), ("gemm_ms", gemm)):
+        for _ in range(3):
+            fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) / reps
+    return out
 
 
 def clear_weight_cache() -> None:
+    """No cached weight encodings are kept between calls."""
     return None

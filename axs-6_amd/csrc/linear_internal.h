@@ -1,0 +1,68 @@
+// Launchers shared by the quantized-linear translation units.
+#pragma once
+
+#include "axs6_internal.h"
+
+namespace axs6 {
+
+// Row pack: per row r of x [rows, cols] (cols % block == 0, 16-byte aligned
+// rows), v = FQ(x) (or x when !fake_quant), and
+//   out[r, c] = fp16(v * 2^(colx[c] - S[r]))      for c < cols
+//   out[r, c] = 0                                  for cols <= c < cols_pad
+// with S[r] = max_c(e1(block of c) + colx[c]) - 15, where 2^e1 bounds the
+// block's magnitudes, so |out| <= 2^15 < fp16 max.  S[r] goes to s_out.
+// rmax_out[r] (optional) = max block e1 of the row (colx ignored);
+// gmax (optional) receives atomicMax(rmax + rowx[r]).
+// `out` may be null (statistics only).
+struct PackRowsArgs {
+    const void* x; int dtype; int64_t rows; int64_t cols; int block;
+    bool fake_quant; bool stochastic; uint64_t seed; uint64_t offset;
+    const int32_t* colx;            // nullable
+    _Float16* out; int64_t ld_out; int64_t cols_pad;
+    int32_t* s_out;                 // [rows]
+    int32_t* rmax_out;              // nullable
+    const int32_t* rowx; int32_t* gmax;  // nullable pair
+};
+int launch_pack_rows(const PackRowsArgs& a, const DeviceTables& t, hipStream_t st);
+
+// Global pack: out[r, c] = fp16(FQ(x)[r, c] * 2^(rowx[r] - (*gmax - 15))),
+// zero for cols <= c < cols_pad; optional column partial sums of FQ(x):
+// partial[chunk, c] = sum over rows of chunk (fixed order).
+struct PackGlobalArgs {
+    const void* x; int dtype; int64_t rows; int64_t cols; int block;
+    bool fake_quant; bool stochastic; uint64_t seed; uint64_t offset;
+    const int32_t* rowx;            // nullable (0)
+    const int32_t* gmax;            // device scalar
+    _Float16* out; int64_t ld_out; int64_t cols_pad;   // out nullable
+    float* partial; int rows_per_chunk;                 // nullable
+};
+int launch_pack_global(const PackGlobalArgs& a, const DeviceTables& t, hipStream_t st);
+int64_t pack_global_chunks(int64_t rows);
+
+// db[c] = sum_k partial[k, c], k in order.
+int launch_reduce_partials(const float* partial, int64_t chunks, int64_t cols, float* out, hipStream_t st);
+
+// out[c, r] = in[r, c] for r < rows, c < out_rows; zero for rows <= r < rows_pad.
+int launch_transpose_f16(const _Float16* in, int64_t rows, int64_t cols, int64_t ld_in,
+                         _Float16* out, int64_t out_rows, int64_t rows_pad, int64_t ld_out,
+                         hipStream_t st);
+
+// *p = INT32_MIN (graph-capture safe: a kernel, not a memset).
+int launch_init_gmax(int32_t* p, hipStream_t st);
+
+// C[M, N] = epilogue(A[M, Kp] . B[N, Kp]^T); fp16 operands, fp32 accumulate.
+// Epilogue: v = ldexp(acc, row_exp[m] + col_exp[n] + (glob ? *glob + glob_add : 0)) + bias[n].
+struct GemmArgs {
+    const _Float16* A; int64_t lda; const _Float16* B; int64_t ldb;
+    int64_t M; int64_t N; int64_t Kp;
+    const int32_t* row_exp; const int32_t* col_exp;
+    const int32_t* glob_exp; int32_t glob_add;
+    const float* bias;
+    void* out; int64_t ldo; int out_dtype;
+};
+int launch_gemm_f16(const GemmArgs& g, hipStream_t st);
+
+constexpr int64_t kGemmK = 64;   // contraction padding unit
+inline int64_t pad_to(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+}  // namespace axs6

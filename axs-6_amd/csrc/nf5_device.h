@@ -1,0 +1,228 @@
+// Device-side NF5 arithmetic shared by the fake-quantize kernels and the
+// operand-packing kernels of the quantized linear.  Every function rounds
+// exactly as the torch CPU operation it replaces (see nf5_fq.hip for the
+// per-step mapping to axs/unified/quantize_unified.py); include only from
+// translation units compiled with FP contraction off.
+#pragma once
+
+#include "axs6_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace axs6 {
+namespace {
+
+constexpr int kThreads = 256;
+#ifndef AXS6_FQ_UNROLL
+#define AXS6_FQ_UNROLL 2
+#endif
+constexpr int kUnroll = AXS6_FQ_UNROLL;  // 16-byte vectors in flight per thread
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- element types ------------------------------------------------------
+
+template <int DT> struct Elem;
+
+template <> struct Elem<AXS6_F32> {
+    using S = float;
+    static constexpr int V = 4;
+    __device__ static float to_f(S v) { return v; }
+    __device__ static S from_f(float f) { return f; }
+    __device__ static void unpack(u32x4 r, float* f) {
+        f[0] = __uint_as_float(r.x); f[1] = __uint_as_float(r.y);
+        f[2] = __uint_as_float(r.z); f[3] = __uint_as_float(r.w);
+    }
+    __device__ static u32x4 pack(const float* f) {
+        u32x4 r;
+        r.x = __float_as_uint(f[0]); r.y = __float_as_uint(f[1]);
+        r.z = __float_as_uint(f[2]); r.w = __float_as_uint(f[3]);
+        return r;
+    }
+};
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    // torch's c10::BFloat16 rounding: NaN -> 0x7FC0, otherwise round to
+    // nearest even on the upper 16 bits.
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7FC0;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+template <> struct Elem<AXS6_BF16> {
+    using S = uint16_t;
+    static constexpr int V = 8;
+    __device__ static float to_f(S v) { return __uint_as_float((uint32_t)v << 16); }
+    __device__ static S from_f(float f) { return f32_to_bf16_rne(f); }
+    __device__ static void unpack(u32x4 r, float* f) {
+        uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = __uint_as_float(w[i] << 16);
+            f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+    __device__ static u32x4 pack(const float* f) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = (uint32_t)f32_to_bf16_rne(f[2 * i]) | ((uint32_t)f32_to_bf16_rne(f[2 * i + 1]) << 16);
+        u32x4 r;
+        r.x = w[0]; r.y = w[1]; r.z = w[2]; r.w = w[3];
+        return r;
+    }
+};
+
+template <> struct Elem<AXS6_F16> {
+    using S = _Float16;
+    static constexpr int V = 8;
+    __device__ static float to_f(S v) { return (float)v; }
+    __device__ static S from_f(float f) { return (_Float16)f; }  // v_cvt_f16_f32: RNE
+    __device__ static void unpack(u32x4 r, float* f) {
+        uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint16_t lo = (uint16_t)(w[i] & 0xffffu), hi = (uint16_t)(w[i] >> 16);
+            f[2 * i] = (float)__builtin_bit_cast(_Float16, lo);
+            f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, hi);
+        }
+    }
+    __device__ static u32x4 pack(const float* f) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint16_t lo = __builtin_bit_cast(uint16_t, (_Float16)f[2 * i]);
+            uint16_t hi = __builtin_bit_cast(uint16_t, (_Float16)f[2 * i + 1]);
+            w[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        u32x4 r;
+        r.x = w[0]; r.y = w[1]; r.z = w[2]; r.w = w[3];
+        return r;
+    }
+};
+
+// ---- block arithmetic ------------------------------------------------------
+
+// Unsigned max across a group of G neighbouring lanes (G in {1,2,4,8}) with
+// DPP: quad_perm [1,0,3,2], quad_perm [2,3,0,1], then row_half_mirror pairs
+// each quad with the other quad of its 8-lane half-row.
+template <int G>
+__device__ __forceinline__ uint32_t group_umax(uint32_t v) {
+    if constexpr (G >= 2) {
+        uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false);
+        v = v > o ? v : o;
+    }
+    if constexpr (G >= 4) {
+        uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false);
+        v = v > o ? v : o;
+    }
+    if constexpr (G >= 8) {
+        uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false);
+        v = v > o ? v : o;
+    }
+    return v;
+}
+
+// Same reduction for groups of up to 32 lanes through cross-lane shuffles
+// (general path only).
+template <int BS>
+__device__ __forceinline__ uint32_t group_umax_shfl(uint32_t v) {
+#pragma unroll
+    for (int off = 1; off < BS; off <<= 1) {
+        uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
+        v = v > o ? v : o;
+    }
+    return v;
+}
+
+constexpr uint32_t kInfBits = 0x7f800000u;
+constexpr uint32_t kNanBits = 0x7fc00000u;
+
+// floor(torch.log2(a)) for a positive finite float32 given by its bits.
+__device__ __forceinline__ int floor_log2_torch(uint32_t a, const uint8_t* band) {
+    int f = a >= 0x00800000u ? (int)(a >> 23) - 127 : (31 - __clz((int)a)) - 149;
+    int k = f + 1;
+    uint32_t kb = k >= -126 ? (uint32_t)(k + 127) << 23 : 1u << (k + 149);
+    return (kb - a <= (uint32_t)band[k + 149]) ? k : f;
+}
+
+__device__ __forceinline__ float pow2_float(int e) {
+    // exact 2^e for e in [-149, 127]; inf above.
+    return e >= 128 ? __uint_as_float(kInfBits)
+                    : (e >= -126 ? __uint_as_float((uint32_t)(e + 127) << 23)
+                                 : __uint_as_float(1u << (e + 149)));
+}
+
+// The per-block scale of fused_fake_quantize (quantize_unified.py:172-179).
+struct FqScale {
+    float scale;    // torch's `scales` entry: 2^e1, 1 (zero block), inf, NaN
+    int e1;         // exponent used to normalise when scale is finite
+    bool inf_scale;
+    bool nan_block;
+};
+
+__device__ __forceinline__ FqScale fq_scale(uint32_t amax, const uint8_t* band) {
+    FqScale s;
+    s.nan_block = amax > kInfBits;
+    bool zero = amax == 0u;
+    bool inf_amax = amax == kInfBits;
+    int e1 = (zero || amax >= kInfBits) ? 0 : floor_log2_torch(amax, band) + 1;
+    s.inf_scale = inf_amax || e1 >= 128;
+    s.e1 = s.inf_scale ? 0 : e1;
+    s.scale = s.nan_block ? __uint_as_float(kNanBits)
+                          : (s.inf_scale ? __uint_as_float(kInfBits) : (zero ? 1.0f : pow2_float(e1)));
+    return s;
+}
+
+// |x| / scale exactly, for power-of-two scales.
+__device__ __forceinline__ float normalise(uint32_t abits, const FqScale& s) {
+    if (s.inf_scale) return abits >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;
+    return __builtin_amdgcn_ldexpf(__uint_as_float(abits), -s.e1);
+}
+
+__device__ __forceinline__ int lut_index(float n, bool stochastic, float u) {
+    float t;
+    if (stochastic) {
+        float d = (u - 0.5f) / 1023.0f;   // IEEE division, as torch
+        t = (n + d) * 1023.0f;
+    } else {
+        t = n * 1023.0f;
+    }
+    t = (t == t) ? t : 0.0f;              // NaN -> INT_MIN -> clamped to 0 in torch
+    int i = (int)t;                       // truncation toward zero
+    return i < 0 ? 0 : (i > kLutMax ? kLutMax : i);
+}
+
+__device__ __forceinline__ float torch_sign(float x) {
+    return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
+}
+
+__device__ __forceinline__ float fq_value(float x, const FqScale& s, const float* lut, bool stochastic, float u) {
+    uint32_t ab = __float_as_uint(x) & 0x7fffffffu;
+    float n = normalise(ab, s);
+    float rec = lut[lut_index(n, stochastic, u)];
+    float r = (torch_sign(x) * rec) * s.scale;
+    return s.nan_block ? __uint_as_float(kNanBits) : r;
+}
+
+// splitmix64 mix of (seed + i * golden); top 24 bits -> U[0,1).
+__device__ __forceinline__ float dither_uniform(uint64_t seed, uint64_t i) {
+    uint64_t z = seed + i * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (float)(uint32_t)(z >> 40) * (1.0f / 16777216.0f);
+}
+
+// Stages the LUT (and the band table) in LDS; needs kThreads == 256.
+__device__ __forceinline__ void stage_tables(float* lut_s, uint32_t* band_w, const float* lut_g,
+                                             const uint8_t* band_g) {
+    const int tid = threadIdx.x;
+    reinterpret_cast<float4*>(lut_s)[tid] = reinterpret_cast<const float4*>(lut_g)[tid];
+    if (tid < kBandSize / 4) band_w[tid] = reinterpret_cast<const uint32_t*>(band_g)[tid];
+    __syncthreads();
+}
+
+}  // namespace
+}  // namespace axs6

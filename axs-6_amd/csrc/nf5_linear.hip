@@ -1,0 +1,189 @@
+// Quantized linear (forward, backward) and plain matmul: host-side
+// composition of the packing kernels and the fp16 MFMA GEMM, exported
+// through the C ABI of include/axs6.h.
+//
+// Forward  Y = FQ(X) FQ(W)^T + b:
+//   pack_rows(X) -> Xq16 [M, Kp], sx[M]      (FQ + row scale, one HBM pass)
+//   pack_rows(W) -> Wq16 [N, Kp], sw[N]
+//   GEMM(Xq16, Wq16) with epilogue 2^(sx[m] + sw[n]) and + b
+// Xq16/sx/Wq16/sw are caller-owned and reused by the backward.
+//
+// Backward (dYq = stochastic FQ(dY) when quantize_grad, else dY):
+//   dX = dYq FQ(W):   pack_rows(dY, colx = sw) -> A1 [M, Np] (row shift t[m]),
+//                     transpose Wq16 -> [Kp, Np], GEMM, epilogue 2^t[m];
+//   dW = dYq^T FQ(X): pack_global(dY, rowx = sx) -> A2 [M, Np] with one
+//                     tensor-wide shift G (max over rows of the row maxima,
+//                     gathered by the first pack), transposes A2 -> [N, Mp]
+//                     and Xq16 -> [Kp, Mp], GEMM, epilogue 2^G;
+//   db = column sums of dYq, in a fixed order (partials + reduce).
+#include <string.h>
+
+#include "linear_internal.h"
+
+namespace axs6 {
+namespace {
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct BwdLayout {
+    size_t gmax, t, a1, wqt, a2, a2t, xqt, partial, total;
+};
+
+BwdLayout bwd_layout(int64_t M, int64_t N, int64_t K, bool dx, bool dw, bool db) {
+    const int64_t Kp = pad_to(K, kGemmK), Np = pad_to(N, kGemmK), Mp = pad_to(M, kGemmK);
+    BwdLayout L{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
+    L.gmax = take(sizeof(int32_t));
+    L.t = take(sizeof(int32_t) * (size_t)M);
+    L.a1 = dx ? take(2 * (size_t)M * Np) : 0;
+    L.wqt = dx ? take(2 * (size_t)Kp * Np) : 0;
+    L.a2 = dw ? take(2 * (size_t)M * Np) : 0;
+    L.a2t = dw ? take(2 * (size_t)N * Mp) : 0;
+    L.xqt = dw ? take(2 * (size_t)Kp * Mp) : 0;
+    L.partial = db ? take(sizeof(float) * (size_t)pack_global_chunks(M) * N) : 0;
+    L.total = off;
+    return L;
+}
+
+int check_dims(const char* fn, int64_t M, int64_t N, int64_t K, int block, int dtype) {
+    if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
+    if (!valid_block(block)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: block_size must be 8, 16 or 32 (got %d)", fn, block);
+    if (M < 0 || N < 0 || K < 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: negative dimension", fn);
+    if (K % block != 0 || N % block != 0)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: K (%lld) and N (%lld) must be multiples of block_size %d "
+                    "(pad them with zeros first)", fn, (long long)K, (long long)N, block);
+    if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: dimension too large", fn);
+    return AXS6_OK;
+}
+
+}  // namespace
+}  // namespace axs6
+
+using namespace axs6;
+
+extern "C" int64_t axs6_linear_padded_k(int64_t k) { return pad_to(k, kGemmK); }
+
+extern "C" int axs6_nf5_pack_rows(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
+                                  int32_t mode, uint64_t seed, uint64_t offset, const int32_t* col_exp,
+                                  void* out_f16, int64_t ld_out, int64_t cols_pad, int32_t* row_shift,
+                                  void* stream) {
+    const char* fn = "axs6_nf5_pack_rows";
+    if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
+    if (!valid_block(block_size)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: block_size must be 8, 16 or 32", fn);
+    if (mode < 0 || mode > 2) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: mode must be 0 (raw), 1 (nearest) or 2 (stochastic)", fn);
+    if (rows < 0 || cols < 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: negative shape", fn);
+    if (rows == 0) return AXS6_OK;
+    if (!x || !row_shift) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    DeviceTables t;
+    int rc = device_tables(&t);
+    if (rc) return rc;
+    PackRowsArgs a{x, dtype, rows, cols, block_size, mode != 0, mode == 2, seed, offset, col_exp,
+                   (_Float16*)out_f16, ld_out, cols_pad, row_shift, nullptr, nullptr, nullptr};
+    return launch_pack_rows(a, t, (hipStream_t)stream);
+}
+
+extern "C" int axs6_gemm_f16_nt(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
+                                int64_t Kp, const int32_t* row_exp, const int32_t* col_exp, const float* bias,
+                                void* out, int64_t ldo, int32_t out_dtype, void* stream) {
+    const char* fn = "axs6_gemm_f16_nt";
+    if (!valid_dtype(out_dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, out_dtype);
+    if (M < 0 || N < 0 || Kp < 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: negative dimension", fn);
+    if (M == 0 || N == 0) return AXS6_OK;
+    if (!a || !b || !out) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    GemmArgs g{(const _Float16*)a, lda, (const _Float16*)b, ldb, M, N, Kp, row_exp, col_exp, nullptr, 0, bias,
+               out, ldo, out_dtype};
+    return launch_gemm_f16(g, (hipStream_t)stream);
+}
+
+extern "C" int axs6_nf5_linear_forward(const void* x, const void* w, const float* bias, void* y, int32_t dtype,
+                                       int64_t M, int64_t N, int64_t K, int32_t block_size,
+                                       int32_t quantize_input, void* xq_f16, int32_t* x_shift, void* wq_f16,
+                                       int32_t* w_shift, void* stream) {
+    const char* fn = "axs6_nf5_linear_forward";
+    int rc = check_dims(fn, M, N, K, block_size, dtype);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return AXS6_OK;
+    if (!x || !w || !y || !xq_f16 || !x_shift || !wq_f16 || !w_shift)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    DeviceTables t;
+    if ((rc = device_tables(&t))) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t Kp = pad_to(K, kGemmK);
+    PackRowsArgs px{x, dtype, M, K, block_size, quantize_input != 0, false, 0, 0, nullptr,
+                    (_Float16*)xq_f16, Kp, Kp, x_shift, nullptr, nullptr, nullptr};
+    if ((rc = launch_pack_rows(px, t, st))) return rc;
+    PackRowsArgs pw{w, dtype, N, K, block_size, true, false, 0, 0, nullptr,
+                    (_Float16*)wq_f16, Kp, Kp, w_shift, nullptr, nullptr, nullptr};
+    if ((rc = launch_pack_rows(pw, t, st))) return rc;
+    GemmArgs g{(const _Float16*)xq_f16, Kp, (const _Float16*)wq_f16, Kp, M, N, Kp, x_shift, w_shift, nullptr, 0,
+               bias, y, N, dtype};
+    return launch_gemm_f16(g, st);
+}
+
+extern "C" size_t axs6_nf5_linear_backward_workspace(int64_t M, int64_t N, int64_t K, int32_t need_dx,
+                                                     int32_t need_dw, int32_t need_db) {
+    if (M < 0 || N < 0 || K < 0) return 0;
+    return bwd_layout(M, N, K, need_dx != 0, need_dw != 0, need_db != 0).total;
+}
+
+extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M, int64_t N, int64_t K,
+                                        int32_t block_size, int32_t quantize_grad, uint64_t seed, uint64_t offset,
+                                        const void* xq_f16, const int32_t* x_shift, const void* wq_f16,
+                                        const int32_t* w_shift, void* dx, float* dw, float* db, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    const char* fn = "axs6_nf5_linear_backward";
+    int rc = check_dims(fn, M, N, K, block_size, dtype);
+    if (rc) return rc;
+    const bool need_dx = dx != nullptr, need_dw = dw != nullptr, need_db = db != nullptr;
+    if (M == 0 || N == 0 || (!need_dx && !need_dw && !need_db)) return AXS6_OK;
+    if (!dy) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null dy", fn);
+    if ((need_dx && (!wq_f16 || !w_shift)) || (need_dw && (!xq_f16 || !x_shift)))
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: packed operands from the forward are required", fn);
+    const BwdLayout L = bwd_layout(M, N, K, need_dx, need_dw, need_db);
+    if (!workspace || workspace_bytes < L.total || (uintptr_t)workspace % kAlign)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: workspace of %zu bytes (256-byte aligned) required, got %zu",
+                    fn, L.total, workspace_bytes);
+    DeviceTables t;
+    if ((rc = device_tables(&t))) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    char* ws = (char*)workspace;
+    const int64_t Kp = pad_to(K, kGemmK), Np = pad_to(N, kGemmK), Mp = pad_to(M, kGemmK);
+    int32_t* gmax = (int32_t*)(ws + L.gmax);
+    int32_t* tshift = (int32_t*)(ws + L.t);
+    const bool fq = quantize_grad != 0;
+
+    if (need_dw && (rc = launch_init_gmax(gmax, st))) return rc;
+    if (need_dx || need_dw) {
+        PackRowsArgs p{dy, dtype, M, N, block_size, fq, fq, seed, offset, need_dx ? w_shift : nullptr,
+                       need_dx ? (_Float16*)(ws + L.a1) : nullptr, Np, Np, tshift, nullptr,
+                       need_dw ? x_shift : nullptr, need_dw ? gmax : nullptr};
+        if ((rc = launch_pack_rows(p, t, st))) return rc;
+    }
+    if (need_dx) {
+        _Float16* wqt = (_Float16*)(ws + L.wqt);
+        if ((rc = launch_transpose_f16((const _Float16*)wq_f16, N, Kp, Kp, wqt, Kp, Np, Np, st))) return rc;
+        GemmArgs g{(const _Float16*)(ws + L.a1), Np, wqt, Np, M, K, Np, tshift, nullptr, nullptr, 0, nullptr,
+                   dx, K, dtype};
+        if ((rc = launch_gemm_f16(g, st))) return rc;
+    }
+    if (need_dw || need_db) {
+        if (!need_dw && (rc = launch_init_gmax(gmax, st))) return rc;
+        PackGlobalArgs p{dy, dtype, M, N, block_size, fq, fq, seed, offset, x_shift, gmax,
+                         need_dw ? (_Float16*)(ws + L.a2) : nullptr, Np, Np,
+                         need_db ? (float*)(ws + L.partial) : nullptr, 0};
+        if ((rc = launch_pack_global(p, t, st))) return rc;
+    }
+    if (need_dw) {
+        _Float16* a2t = (_Float16*)(ws + L.a2t);
+        _Float16* xqt = (_Float16*)(ws + L.xqt);
+        if ((rc = launch_transpose_f16((const _Float16*)(ws + L.a2), M, Np, Np, a2t, N, Mp, Mp, st))) return rc;
+        if ((rc = launch_transpose_f16((const _Float16*)xq_f16, M, Kp, Kp, xqt, Kp, Mp, Mp, st))) return rc;
+        GemmArgs g{a2t, Mp, xqt, Mp, N, K, Mp, nullptr, nullptr, gmax, -15, nullptr, dw, K, AXS6_F32};
+        if ((rc = launch_gemm_f16(g, st))) return rc;
+    }
+    if (need_db && (rc = launch_reduce_partials((const float*)(ws + L.partial), pack_global_chunks(M), N, db, st)))
+        return rc;
+    return AXS6_OK;
+}

@@ -101,7 +101,10 @@ def bench_fq(steps: int, warmup: int):
 
     def step():
         y = fake_quantize_unified(x, 32, "nearest")
-        y.backward(grad)   # STE: identity, no kernel
+        # STE backward: returns `grad` itself (no kernel); autograd.grad
+        # avoids accumulating into a leaf .grad, which is not part of the path
+        (gx,) = torch.autograd.grad(y, x, grad)
+        assert gx.data_ptr() == grad.data_ptr()
 
     wall_ms, gpu_ms = time_steps(step, steps, warmup)
     nbytes = 8 * x.numel()

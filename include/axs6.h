@@ -24,6 +24,7 @@
 #ifndef AXS6_H
 #define AXS6_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -82,6 +83,68 @@ int axs6_nf5_quantize(const void* x, int32_t dtype, int64_t rows, int64_t cols,
  * Replaces: dequantize_unified (axs/unified/quantize_unified.py:285). */
 int axs6_nf5_dequantize(const uint8_t* exponents, const uint8_t* codes, const uint8_t* signs,
                         float* y, int64_t rows, int64_t cols, int32_t block_size, void* stream);
+
+/* ---- quantized linear ------------------------------------------------------
+ * The linear contracts NF5 fake-quantized operands on fp16 MFMA.  Operands are
+ * packed as fp16 rows scaled by an exact power of two (2^-shift per row, so
+ * the row's largest value is <= 2^15); the GEMM epilogue restores the shifts.
+ * "Kp" is K rounded up to the GEMM's contraction unit (axs6_linear_padded_k);
+ * packed rows are zero beyond K.
+ */
+
+/* Contraction padding of the GEMM: K rounded up to a multiple of 64. */
+int64_t axs6_linear_padded_k(int64_t k);
+
+/* Packs rows of x [rows, cols] (cols % block_size == 0, 16-byte aligned):
+ * mode 0 = values as given, 1 = NF5 FQ nearest, 2 = NF5 FQ stochastic;
+ * out_f16[r, c] = fp16(v * 2^(col_exp[c] - row_shift[r])) for c < cols, zero up
+ * to cols_pad (out_f16 may be NULL to compute row_shift only; col_exp may be
+ * NULL).  The FQ(x) + fp16-operand half of the fused Triton linear's tile
+ * prologue (axs/unified/triton_kernels.py:152-180), run once per operand. */
+int axs6_nf5_pack_rows(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
+                       int32_t mode, uint64_t seed, uint64_t offset, const int32_t* col_exp,
+                       void* out_f16, int64_t ld_out, int64_t cols_pad, int32_t* row_shift,
+                       void* stream);
+
+/* out[M, N] = ldexp(A[M, Kp] . B[N, Kp]^T, row_exp[m] + col_exp[n]) + bias[n]
+ * with fp16 A, B (16-byte aligned, lda/ldb multiples of 8, Kp % 64 == 0),
+ * fp32 accumulation, out in out_dtype (row_exp, col_exp, bias may be NULL).
+ * The contraction of the fused Triton linear (triton_kernels.py:185-282) and
+ * of the backward matmuls (axs/unified/backend.py:621-671). */
+int axs6_gemm_f16_nt(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
+                     int64_t Kp, const int32_t* row_exp, const int32_t* col_exp, const float* bias,
+                     void* out, int64_t ldo, int32_t out_dtype, void* stream);
+
+/* Y[M, N] = FQ(X)[M, K] . FQ(W)[N, K]^T + bias, with X, W, Y of `dtype` and an
+ * f32 bias (may be NULL).  K and N must be multiples of block_size.  The
+ * caller provides xq_f16 [M, Kp], x_shift [M], wq_f16 [N, Kp], w_shift [N];
+ * they hold the packed operands afterwards and feed the backward.
+ * quantize_input = 0 packs X without fake-quantizing it.
+ * Replaces: _AXSLinearUnifiedFunction.forward (axs/unified/functional_unified.py:107-131),
+ *           accelerated_linear (axs/unified/backend.py:540), triton_fused_linear
+ *           (axs/unified/triton_kernels.py:385). */
+int axs6_nf5_linear_forward(const void* x, const void* w, const float* bias, void* y, int32_t dtype,
+                            int64_t M, int64_t N, int64_t K, int32_t block_size, int32_t quantize_input,
+                            void* xq_f16, int32_t* x_shift, void* wq_f16, int32_t* w_shift, void* stream);
+
+/* Device workspace (bytes) axs6_nf5_linear_backward needs for the requested
+ * gradients. */
+size_t axs6_nf5_linear_backward_workspace(int64_t M, int64_t N, int64_t K, int32_t need_dx,
+                                          int32_t need_dw, int32_t need_db);
+
+/* Gradients of the quantized linear from dY [M, N] (`dtype`) and the packed
+ * operands of the forward: dYq = NF5 FQ of dY (stochastic, blocks along N)
+ * when quantize_grad, else dY; dx [M, K] (`dtype`) = dYq . FQ(W);
+ * dw [N, K] f32 = dYq^T . FQ(X); db [N] f32 = column sums of dYq.  Any of dx,
+ * dw, db may be NULL.  workspace: 256-byte aligned, at least
+ * axs6_nf5_linear_backward_workspace(...) bytes.
+ * Replaces: _AXSLinearUnifiedFunction.backward (axs/unified/functional_unified.py:134-170)
+ *           with accelerated_matmul (axs/unified/backend.py:621). */
+int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M, int64_t N, int64_t K,
+                             int32_t block_size, int32_t quantize_grad, uint64_t seed, uint64_t offset,
+                             const void* xq_f16, const int32_t* x_shift, const void* wq_f16,
+                             const int32_t* w_shift, void* dx, float* dw, float* db, void* workspace,
+                             size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }
