@@ -86,9 +86,15 @@ def has(name: str) -> bool:
     return hasattr(lib(), name)
 
 
+_fns: dict = {}
+
+
 def call(name: str, *args) -> None:
     """Call an entry point and raise RuntimeError on a non-zero status."""
-    rc = getattr(lib(), name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(lib(), name)
+    rc = fn(*args)
     if rc != 0:
         msg = lib().axs6_last_error().decode(errors="replace")
         raise LibraryError(f"{name} failed (status {rc}): {msg}")
@@ -98,8 +104,13 @@ def version() -> str:
     return lib().axs6_version().decode()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
     """Raw hipStream_t of torch's current stream on t's device."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index if t.device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

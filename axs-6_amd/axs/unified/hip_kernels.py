@@ -46,15 +46,18 @@ def _check_rounding(rounding: str) -> bool:
 class _on_device:
     """Makes t's device current for the duration of a library call."""
 
+    __slots__ = ("idx", "prev")
+
     def __init__(self, t: torch.Tensor):
         self.idx = t.device.index
         self.prev = None
 
     def __enter__(self):
-        cur = torch.cuda.current_device()
-        if self.idx is not None and self.idx != cur:
-            self.prev = cur
-            torch.cuda.set_device(self.idx)
+        if self.idx is not None:
+            cur = torch.cuda.current_device()
+            if self.idx != cur:
+                self.prev = cur
+                torch.cuda.set_device(self.idx)
 
     def __exit__(self, *exc):
         if self.prev is not None:
@@ -76,7 +79,8 @@ def as_rows(tensor: torch.Tensor) -> tuple[torch.Tensor, int, int]:
     x = tensor
     if x.dtype not in _lib.DTYPE_CODE:
         x = x.float()
-    x = x.contiguous()
+    if not x.is_contiguous():
+        x = x.contiguous()
     cols = x.shape[-1]
     rows = x.numel() // cols if cols else 0
     return x, rows, cols

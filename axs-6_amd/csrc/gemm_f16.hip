@@ -3,14 +3,16 @@
 // both operands contraction-contiguous ("NT"), Kp a multiple of 64 with
 // zero padding (the packing kernels write it).
 //
-// Tiling.  A workgroup of 4 waves owns a BM x BN tile of C; the waves form a
-// 2 x 2 grid, each wave a (BM/2) x (BN/2) sub-tile built from 32x32 MFMA
-// blocks (v_mfma_f32_32x32x16_f16: 32x32 fp32 accumulators, K = 16 per
-// instruction, 16 accumulator registers per lane).  Per K-step of 64 the A
-// and B tiles are staged through LDS (row pitch 64 + 8 halves, so the
-// 16-byte fragment reads of 8 consecutive rows hit distinct bank groups);
-// the next K-step's tiles are loaded into registers while the current one
-// is multiplied (two LDS buffers, one barrier per step).
+// Tiling.  A workgroup of WGM x WGN waves owns a BM x BN tile of C; each wave
+// a (BM/WGM) x (BN/WGN) sub-tile of 32x32 MFMA blocks
+// (v_mfma_f32_32x32x16_f16: K = 16 per instruction, 16 fp32 accumulators per
+// lane).  Per K-step of 64 halves the A and B tiles are staged through LDS:
+// each 64-half row is 8 slots of 16 bytes, and chunk c of row r lives in slot
+// c ^ (r & 7), so the 16-byte fragment reads of 8 consecutive rows land in 8
+// distinct bank groups without padding.  The next K-step's tiles are fetched
+// into registers (buffer loads: rows past M/N read as zero through the
+// buffer's range check) while the current one is multiplied; two LDS buffers,
+// one barrier per step.
 //
 // Schedule.  Workgroup ids are dispatched round-robin over the 8 XCDs; the
 // id is remapped so that each XCD receives a contiguous range of the grouped
@@ -21,6 +23,7 @@
 // as fp32, bf16 or fp16; the exponents undo the packing kernels' power-of-two
 // row scales exactly.
 #include <limits.h>
+#include <stdlib.h>
 
 #include "linear_internal.h"
 
@@ -31,10 +34,10 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 64;
-constexpr int kLDK = kBK + 8;       // LDS row pitch in halves
-constexpr int kGemmThreads = 256;
+constexpr int kBK = 64;            // halves per K-step (8 slots of 16 bytes)
+constexpr int kRowBytes = kBK * 2;
 constexpr int kGroupM = 8;
+constexpr int kBufferConfig = 0x00020000;   // raw 32-bit buffer access, gfx9 family
 
 struct GemmK {
     const _Float16* A; int64_t lda; const _Float16* B; int64_t ldb;
@@ -50,18 +53,127 @@ __device__ __forceinline__ uint16_t to_bf16(float f) {
     return (uint16_t)(u >> 16);
 }
 
-template <int BM, int BN>
-__global__ __launch_bounds__(kGemmThreads, 1) void gemm_f16_nt_kernel(GemmK g) {
-    constexpr int WM = BM / 2, WN = BN / 2;
-    constexpr int TM = WM / 32, TN = WN / 32;
-    constexpr int A_LOADS = BM * (kBK / 8) / kGemmThreads;   // 16-byte chunks per thread
-    constexpr int B_LOADS = BN * (kBK / 8) / kGemmThreads;
-    static_assert(A_LOADS >= 1 && B_LOADS >= 1, "tile too small");
-    extern __shared__ __align__(16) _Float16 smem[];
-    _Float16* As = smem;                          // [2][BM * kLDK]
-    _Float16* Bs = smem + 2 * BM * kLDK;          // [2][BN * kLDK]
+// LDS layout of a K-slab: row r of the tile holds BK halves = BK/8 slots of
+// 16 bytes; logical chunk c of row r lives in slot c ^ key(r).  gfx950's LDS
+// serves a 16-lane group of ds_read_b128 from 64 four-byte banks, i.e. 256
+// bytes, which covers 256/(2*BK) consecutive rows; key(r) is taken from the
+// row bits above those so that the 16 rows of a fragment read fill the 64
+// banks exactly once (measured with the key on the low row bits instead:
+// SQ_LDS_BANK_CONFLICT at 50% of LDS-active cycles; with this key, 0).
+template <int BK>
+__device__ __forceinline__ int swz_key(int row) {
+    constexpr int SHIFT = BK == 64 ? 1 : 2;   // log2(256 / (2 * BK))
+    return (row >> SHIFT) & (BK / 8 - 1);
+}
+template <int BK>
+__device__ __forceinline__ int swz(int row, int chunk) {
+    return row * (BK * 2) + ((chunk ^ swz_key<BK>(row)) << 4);
+}
 
-    // ---- tile schedule -----------------------------------------------------
+// One K-step (64 halves = 4 MFMA K-slices) of the wave's TM x TN blocks.
+// SCHED 0: reads then MFMAs per slice (compiler scheduling); 1/2: the same
+// with the compiler's GEMM interleave strategy iglp_opt(0/1); 3: the next
+// slice's fragments are read into a second register set while the current
+// slice's MFMAs issue.
+template <int BK, int TM, int TN, int SCHED>
+__device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const char* as, const char* bs, int a_row0,
+                                         int b_row0, int fh) {
+    if constexpr (SCHED == 3) {
+        f16x8 af[2][TM], bf[2][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[0][i] = *reinterpret_cast<const f16x8*>(as + swz<BK>(a_row0 + i * 32, fh));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[0][j] = *reinterpret_cast<const f16x8*>(bs + swz<BK>(b_row0 + j * 32, fh));
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            const int cur = kk & 1;
+            if (kk + 1 < BK / 16) {
+                const int chunk = (kk + 1) * 2 + fh;
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+                    af[cur ^ 1][i] = *reinterpret_cast<const f16x8*>(as + swz<BK>(a_row0 + i * 32, chunk));
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    bf[cur ^ 1][j] = *reinterpret_cast<const f16x8*>(bs + swz<BK>(b_row0 + j * 32, chunk));
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][i], bf[cur][j], acc[i][j], 0, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            const int chunk = kk * 2 + fh;
+            f16x8 af[TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const f16x8*>(as + swz<BK>(a_row0 + i * 32, chunk));
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const f16x8*>(bs + swz<BK>(b_row0 + j * 32, chunk));
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if constexpr (SCHED == 1) __builtin_amdgcn_iglp_opt(0);
+        if constexpr (SCHED == 2) __builtin_amdgcn_iglp_opt(1);
+    }
+}
+
+// Writes one 32x32 accumulator block.  Lane layout of v_mfma_f32_32x32x16:
+// column = lane % 32, row = 8 * (r / 4) + 4 * (lane / 32) + r % 4 for
+// accumulator register r; `row0` already includes the 4 * (lane / 32) term.
+__device__ __forceinline__ void store_block(const f32x16 a, const GemmK& g, int row0, int col, int gexp) {
+    if (col >= g.N) return;
+    const int cexp = (g.col_exp ? g.col_exp[col] : 0) + gexp;
+    const float bias = g.bias ? g.bias[col] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = row0 + (r >> 2) * 8 + (r & 3);
+        if (row < g.M) {
+            const int e = cexp + (g.row_exp ? g.row_exp[row] : 0);
+            const float v = __builtin_amdgcn_ldexpf(a[r], e) + bias;
+            const int64_t o = (int64_t)row * g.ldo + col;
+            if (g.out_dtype == AXS6_F32) reinterpret_cast<float*>(g.out)[o] = v;
+            else if (g.out_dtype == AXS6_BF16) reinterpret_cast<uint16_t*>(g.out)[o] = to_bf16(v);
+            else reinterpret_cast<_Float16*>(g.out)[o] = (_Float16)v;
+        }
+    }
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Multi-stage variant: operand tiles go from HBM straight into LDS
+// (buffer_load_dwordx4 ... lds, 16 bytes per lane, a wave instruction fills
+// 1 KiB = 8 rows of a 64-half K-slab) with STAGES slabs in flight, so a
+// slab's load latency is covered by STAGES-1 K-steps of MFMA work and no
+// registers are spent on staging.  Lane l of a load instruction lands at
+// byte 16*l of its 1 KiB, i.e. row l/8, slot l%8, and therefore fetches
+// logical chunk (l%8) ^ key(row) -- the same XOR layout the fragment reads use.
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED>
+__global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(GemmK g) {
+#if defined(__HIP_DEVICE_COMPILE__)  // LDS-DMA builtins exist only in the device pass
+    constexpr int NW = WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int RB = BK * 2;                                 // bytes per slab row
+    constexpr int SPR = BK / 8;                                // 16-byte slots per row
+    constexpr int ROWS_PER_INST = 1024 / RB;                   // rows one wave load fills
+    constexpr int A_INST = BM / ROWS_PER_INST / NW;            // load instructions per wave per slab
+    constexpr int B_INST = BN / ROWS_PER_INST / NW;
+    constexpr int IPW = A_INST + B_INST;
+    constexpr int SLAB = (BM + BN) * RB;
+    static_assert(A_INST >= 1 && B_INST >= 1 && STAGES >= 2, "tile shape");
+    extern __shared__ __align__(16) char smem[];
+
     const int tiles_m = (g.M + BM - 1) / BM;
     const int tiles_n = (g.N + BN - 1) / BN;
     const int total = tiles_m * tiles_n;
@@ -72,50 +184,35 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_f16_nt_kernel(GemmK g) {
     const int first_m = group * kGroupM;
     const int gsize = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
     const int in_group = bid - group * per_group;
-    const int tm0 = first_m + in_group % gsize;
-    const int tn0 = in_group / gsize;
-    const int m0 = tm0 * BM, n0 = tn0 * BN;
+    const int m0 = (first_m + in_group % gsize) * BM;
+    const int n0 = (in_group / gsize) * BN;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
 
-    // ---- global -> register staging ------------------------------------------
-    u32x4g ra[A_LOADS], rb[B_LOADS];
-    auto gload = [&](int kt) {
-        const int64_t k0 = (int64_t)kt * kBK;
+    const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)g.A, 0, (int)((int64_t)g.M * g.lda * 2), kBufferConfig);
+    const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)g.B, 0, (int)((int64_t)g.N * g.ldb * 2), kBufferConfig);
+    // per-lane global byte offsets and per-wave LDS offsets of this wave's loads
+    const int lrow = lane / SPR;                      // row inside the load's row group
+    const int lslot = lane % SPR;                     // LDS slot this lane fills
+    int a_goff[A_INST], a_loff[A_INST], b_goff[B_INST], b_loff[B_INST];
 #pragma unroll
-        for (int i = 0; i < A_LOADS; ++i) {
-            const int q = tid + kGemmThreads * i;
-            const int row = q >> 3, c8 = q & 7;
-            const int gr = m0 + row;
-            ra[i] = gr < g.M ? *reinterpret_cast<const u32x4g*>(g.A + (int64_t)gr * g.lda + k0 + c8 * 8)
-                             : u32x4g{0u, 0u, 0u, 0u};
-        }
+    for (int i = 0; i < A_INST; ++i) {
+        const int row = (wave + NW * i) * ROWS_PER_INST + lrow;     // row of the A slab
+        a_goff[i] = (int)((int64_t)(m0 + row) * g.lda * 2) + ((lslot ^ swz_key<BK>(row)) << 4);
+        a_loff[i] = (wave + NW * i) * 1024;
+    }
 #pragma unroll
-        for (int i = 0; i < B_LOADS; ++i) {
-            const int q = tid + kGemmThreads * i;
-            const int row = q >> 3, c8 = q & 7;
-            const int gr = n0 + row;
-            rb[i] = gr < g.N ? *reinterpret_cast<const u32x4g*>(g.B + (int64_t)gr * g.ldb + k0 + c8 * 8)
-                             : u32x4g{0u, 0u, 0u, 0u};
-        }
-    };
-    auto sstore = [&](int buf) {
-        _Float16* as = As + buf * BM * kLDK;
-        _Float16* bs = Bs + buf * BN * kLDK;
-#pragma unroll
-        for (int i = 0; i < A_LOADS; ++i) {
-            const int q = tid + kGemmThreads * i;
-            *reinterpret_cast<u32x4g*>(as + (q >> 3) * kLDK + (q & 7) * 8) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < B_LOADS; ++i) {
-            const int q = tid + kGemmThreads * i;
-            *reinterpret_cast<u32x4g*>(bs + (q >> 3) * kLDK + (q & 7) * 8) = rb[i];
-        }
-    };
+    for (int i = 0; i < B_INST; ++i) {
+        const int row = (wave + NW * i) * ROWS_PER_INST + lrow;
+        b_goff[i] = (int)((int64_t)(n0 + row) * g.ldb * 2) + ((lslot ^ swz_key<BK>(row)) << 4);
+        b_loff[i] = BM * RB + (wave + NW * i) * 1024;
+    }
+    auto lds_ptr = [](char* p) { return (__attribute__((address_space(3))) void*)p; };
 
     f32x16 acc[TM][TN];
 #pragma unroll
@@ -125,88 +222,119 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_f16_nt_kernel(GemmK g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int KT = g.Kp / kBK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    const int frow = lane & 31;          // fragment row within a 32-block
-    const int fk = (lane >> 5) * 8;      // fragment K offset within a K=16 slice
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) gload(kt + 1);
-        const _Float16* as = As + cur * BM * kLDK + (wm * WM + frow) * kLDK + fk;
-        const _Float16* bs = Bs + cur * BN * kLDK + (wn * WN + frow) * kLDK + fk;
+    const int KT = g.Kp / BK;
+    // prologue: slabs 0 .. STAGES-2
 #pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            f16x8 af[TM], bf[TN];
+    for (int s = 0; s < STAGES - 1; ++s) {
+        if (s < KT) {
+            char* slab = smem + s * SLAB;
 #pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const f16x8*>(as + i * 32 * kLDK + kk * 16);
+            for (int i = 0; i < A_INST; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, lds_ptr(slab + a_loff[i]), 16, a_goff[i] + s * RB, 0, 0, 0);
 #pragma unroll
-            for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const f16x8*>(bs + j * 32 * kLDK + kk * 16);
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < B_INST; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, lds_ptr(slab + b_loff[i]), 16, b_goff[i] + s * RB, 0, 0, 0);
         }
-        if (kt + 1 < KT) sstore(cur ^ 1);
-        __syncthreads();
     }
 
-    // ---- epilogue -------------------------------------------------------------
+    const int fr = lane & 31;
+    const int fh = lane >> 5;
+    const int a_row0 = wm * WM + fr;
+    const int b_row0 = wn * WN + fr;
+    for (int kt = 0; kt < KT; ++kt) {
+        // slab kt has landed once at most (slabs issued after it) * IPW loads are outstanding
+        const int ahead = (KT - 1 - kt) < (STAGES - 2) ? (KT - 1 - kt) : (STAGES - 2);
+        if constexpr (STAGES >= 4) {
+            if (ahead >= 2) wait_vmcnt<2 * IPW>();
+            else if (ahead == 1) wait_vmcnt<IPW>();
+            else wait_vmcnt<0>();
+        } else if constexpr (STAGES == 3) {
+            if (ahead >= 1) wait_vmcnt<IPW>();
+            else wait_vmcnt<0>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        // a bare s_barrier: __syncthreads() would also drain every outstanding
+        // load (vmcnt(0)) and serialise the pipeline; the explicit vmcnt wait
+        // above already orders this wave's LDS fills before the barrier.
+        __builtin_amdgcn_s_barrier();
+        const int nk = kt + STAGES - 1;
+        if (nk < KT) {
+            char* slab = smem + (nk % STAGES) * SLAB;
+#pragma unroll
+            for (int i = 0; i < A_INST; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, lds_ptr(slab + a_loff[i]), 16, a_goff[i] + nk * RB, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < B_INST; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, lds_ptr(slab + b_loff[i]), 16, b_goff[i] + nk * RB, 0, 0, 0);
+        }
+        const char* slab = smem + (kt % STAGES) * SLAB;
+        mma_step<BK, TM, TN, SCHED>(acc, slab, slab + BM * RB, a_row0, b_row0, fh);
+    }
+
     const int gexp = g.glob_exp ? (*g.glob_exp == INT_MIN ? 0 : *g.glob_exp + g.glob_add) : 0;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn * WN + j * 32 + (lane & 31);
-            if (col >= g.N) continue;
-            const int cexp = (g.col_exp ? g.col_exp[col] : 0) + gexp;
-            const float bias = g.bias ? g.bias[col] : 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                if (row >= g.M) continue;
-                const int e = cexp + (g.row_exp ? g.row_exp[row] : 0);
-                const float v = __builtin_amdgcn_ldexpf(acc[i][j][r], e) + bias;
-                const int64_t o = (int64_t)row * g.ldo + col;
-                if (g.out_dtype == AXS6_F32) reinterpret_cast<float*>(g.out)[o] = v;
-                else if (g.out_dtype == AXS6_BF16) reinterpret_cast<uint16_t*>(g.out)[o] = to_bf16(v);
-                else reinterpret_cast<_Float16*>(g.out)[o] = (_Float16)v;
-            }
-        }
-    }
+        for (int j = 0; j < TN; ++j)
+            store_block(acc[i][j], g, m0 + wm * WM + i * 32 + fh * 4, n0 + wn * WN + j * 32 + fr, gexp);
+#endif
 }
 
-template <int BM, int BN>
-int run_gemm(const GemmK& k, hipStream_t st) {
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED>
+int run_gemm_lds(const GemmK& k, hipStream_t st) {
     const int tiles = ((k.M + BM - 1) / BM) * ((k.N + BN - 1) / BN);
-    const size_t lds = (size_t)2 * (BM + BN) * kLDK * sizeof(_Float16);
+    const size_t lds = (size_t)STAGES * (BM + BN) * BK * 2;
     static bool attr_set = false;
     if (!attr_set) {
-        hipFuncSetAttribute((const void*)gemm_f16_nt_kernel<BM, BN>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        (void)hipFuncSetAttribute((const void*)gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         attr_set = true;
     }
-    gemm_f16_nt_kernel<BM, BN><<<dim3((unsigned)tiles), kGemmThreads, lds, st>>>(k);
-    return check_launch("gemm_f16");
+    gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED><<<dim3((unsigned)tiles), WGM * WGN * 64, lds, st>>>(k);
+    return check_launch("gemm_f16_lds");
+}
+
+// Launch configuration; AXS6_GEMM_CFG selects one for launch-shape sweeps
+// (BMxBN tile / K-slab / LDS stages / waves / schedule variant of mma_step):
+//   0: 256x256 / 64 / 2 / 8 / 2      1: 256x256 / 32 / 4 / 8 / 2
+//   2: 256x256 / 32 / 3 / 8 / 2      3: 256x256 / 32 / 4 / 8 / 0
+//   4: 256x256 / 32 / 4 / 4 / 2      5: 256x256 / 32 / 4 / 8 / 3
+//   6: 256x256 / 64 / 2 / 8 / 0      7: 256x128 / 64 / 3 / 8 / 2
+int gemm_cfg() {
+    static int v = [] {
+        const char* s = getenv("AXS6_GEMM_CFG");
+        int n = s ? atoi(s) : -1;
+        return (n >= 0 && n <= 7) ? n : 0;
+    }();
+    return v;
 }
 
 }  // namespace
 
 int launch_gemm_f16(const GemmArgs& a, hipStream_t st) {
     if (a.M == 0 || a.N == 0) return AXS6_OK;
-    if (a.Kp % kBK != 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: Kp (%lld) must be a multiple of %d", (long long)a.Kp, kBK);
+    if (a.Kp % 64 != 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: Kp (%lld) must be a multiple of 64", (long long)a.Kp);
     if (a.lda % 8 || a.ldb % 8 || (uintptr_t)a.A % 16 || (uintptr_t)a.B % 16)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: operands must be 16-byte aligned with ld a multiple of 8");
+    if (a.Kp > a.lda || a.Kp > a.ldb) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: Kp exceeds the leading dimension");
+    // buffer offsets are 32-bit: every operand byte (plus one tile of rows) must be addressable
+    if ((a.M + 256) * a.lda * 2 >= ((int64_t)1 << 31) || (a.N + 256) * a.ldb * 2 >= ((int64_t)1 << 31))
+        return fail(AXS6_ERR_UNSUPPORTED, "gemm: operand larger than 2 GiB");
     if (a.M > INT_MAX || a.N > INT_MAX || a.Kp > INT_MAX)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: dimension exceeds int32");
     GemmK k{a.A, a.lda, a.B, a.ldb, (int)a.M, (int)a.N, (int)a.Kp, a.row_exp, a.col_exp, a.glob_exp,
             a.glob_add, a.bias, a.out, a.ldo, a.out_dtype};
-#if defined(AXS6_GEMM_BM) && defined(AXS6_GEMM_BN)
-    return run_gemm<AXS6_GEMM_BM, AXS6_GEMM_BN>(k, st);
-#else
-    return run_gemm<128, 128>(k, st);
-#endif
+    switch (gemm_cfg()) {
+        case 1: return run_gemm_lds<256, 256, 32, 4, 2, 4, 2>(k, st);
+        case 2: return run_gemm_lds<256, 256, 32, 3, 2, 4, 2>(k, st);
+        case 3: return run_gemm_lds<256, 256, 32, 4, 2, 4, 0>(k, st);
+        case 4: return run_gemm_lds<256, 256, 32, 4, 2, 2, 2>(k, st);
+        case 5: return run_gemm_lds<256, 256, 32, 4, 2, 4, 3>(k, st);
+        case 6: return run_gemm_lds<256, 256, 64, 2, 2, 4, 0>(k, st);
+        case 7: return run_gemm_lds<256, 128, 64, 3, 4, 2, 2>(k, st);
+        default: return run_gemm_lds<256, 256, 64, 2, 2, 4, 2>(k, st);
+    }
 }
 
 }  // namespace axs6

@@ -66,11 +66,21 @@ def load_traffic(name: str):
         return None
 
 
-def time_steps(fn, steps: int, warmup: int):
+def time_steps(step, launches, steps: int, warmup: int):
+    """Time `steps` eager steps after `warmup` untimed ones.
+
+    `step` is the full step through the public API (autograd included).  The
+    timed region is bracketed by device synchronisations; HIP events recorded
+    on the launch stream (torch's current stream, which the library launches
+    on) around it give the device time per step.  For reference the step's
+    kernels (`launches`) are also captured once into a HIP graph and replayed
+    -- on ROCm a replay adds a few microseconds of launch latency, so the
+    eager loop is the primary figure.
+    Returns (eager wall ms/step, device ms/step, graph-replay wall ms/step)."""
     import torch
 
     for _ in range(warmup):
-        fn()
+        step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -78,19 +88,38 @@ def time_steps(fn, steps: int, warmup: int):
     t0 = time.perf_counter()
     ev0.record(stream)
     for _ in range(steps):
-        fn()
+        step()
     ev1.record(stream)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    wall_ms = (t1 - t0) * 1e3 / steps
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     gpu_ms = ev0.elapsed_time(ev1) / steps
-    return wall_ms, gpu_ms
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            launches()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launches()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    graph_ms = (time.perf_counter() - t0) * 1e3 / steps
+    return wall_ms, gpu_ms, graph_ms
 
 
 def bench_fq(steps: int, warmup: int):
     import torch
 
     from axs.unified.functional_unified import fake_quantize_unified
+    from axs.unified.hip_kernels import hip_fused_fake_quantize
 
     g = torch.Generator(device="cuda").manual_seed(3)
     x = torch.randn(*FQ_SHAPE, device="cuda", generator=g)
@@ -101,14 +130,21 @@ def bench_fq(steps: int, warmup: int):
 
     def step():
         y = fake_quantize_unified(x, 32, "nearest")
-        # STE backward: returns `grad` itself (no kernel); autograd.grad
-        # avoids accumulating into a leaf .grad, which is not part of the path
+        # STE backward: hands back `grad` itself and launches nothing;
+        # autograd.grad avoids accumulating into a leaf .grad (not part of the path)
         (gx,) = torch.autograd.grad(y, x, grad)
-        assert gx.data_ptr() == grad.data_ptr()
+        return y, gx
 
-    wall_ms, gpu_ms = time_steps(step, steps, warmup)
+    _, gx = step()
+    assert gx.data_ptr() == grad.data_ptr(), "STE backward must hand back the incoming gradient"
+    xd = x.detach()
+
+    def launches():
+        hip_fused_fake_quantize(xd, 32, "nearest")
+
+    wall_ms, gpu_ms, graph_ms = time_steps(step, launches, steps, warmup)
     nbytes = 8 * x.numel()
-    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "bytes": nbytes}
+    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "graph_ms": graph_ms, "bytes": nbytes}
 
 
 def bench_linear(steps: int, warmup: int):
@@ -125,9 +161,10 @@ def bench_linear(steps: int, warmup: int):
     def step():
         hip_linear.linear_forward(X, W, b, 32, True)
 
-    wall_ms, gpu_ms = time_steps(step, steps, warmup)
+    wall_ms, gpu_ms, graph_ms = time_steps(step, step, steps, warmup)
     kern = hip_linear.last_forward_kernel_times(X, W, b, reps=max(steps, 10))
-    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "flops": 2.0 * M * N * K, "kernels": kern}
+    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "graph_ms": graph_ms, "flops": 2.0 * M * N * K,
+            "kernels": kern}
 
 
 def cpu_baseline_fq(budget_s: float = 12.0):
@@ -186,8 +223,8 @@ def main() -> int:
     fq = bench_fq(a.steps, a.warmup)
     gbs = fq["bytes"] / (fq["wall_ms"] * 1e-3) / 1e9
     achieved = fq["bytes"] / (fq["gpu_ms"] * 1e-3) / 1e9
-    log(f"fq 8192x4096: {fq['wall_ms']*1e3:.1f} us/step wall, {fq['gpu_ms']*1e3:.1f} us/launch, "
-        f"{achieved:.0f} GB/s")
+    log(f"fq 8192x4096: {fq['wall_ms']*1e3:.1f} us/step, {fq['gpu_ms']*1e3:.1f} us/launch (device), "
+        f"{achieved:.0f} GB/s; graph replay {fq['graph_ms']*1e3:.1f} us/step")
     traffic = load_traffic("fq_8192x4096_traffic.json")
     out = {
         "metric": "NF5 fake-quant GB/s @8192x4096 fp32; AXS-6 linear TFLOP/s @4096^3 bf16",
@@ -197,6 +234,7 @@ def main() -> int:
         "steps": a.steps,
         "warmup": a.warmup,
         "ms_per_step": round(fq["wall_ms"], 5),
+        "graph_replay_ms_per_step": round(fq["graph_ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -220,6 +258,7 @@ def main() -> int:
                 "metric": "AXS-6 linear forward TFLOP/s @4096^3",
                 "value": round(tflops, 1), "unit": "TFLOP/s",
                 "ms_per_step": round(lin["wall_ms"], 5),
+                "graph_replay_ms_per_step": round(lin["graph_ms"], 5),
                 "dtype": k.get("compute_dtype"),
                 "kernels_ms": {kk: round(v, 5) for kk, v in k.items() if kk.endswith("_ms")},
                 "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1) if gemm_tf else None,
