@@ -13,8 +13,12 @@ linear TFLOP/s @4096^3 bf16"):
   * "linear": the fused AXS-6 linear forward at M=N=K=4096 (config 3), FLOPs
     per step = 2*M*N*K, timed the same way.
 Inputs are synthetic, resident in HBM before the timed region.  K steps are
-timed between device synchronisations; per-kernel time comes from HIP events
-on the stream the kernels run on (torch's current stream).
+timed between device synchronisations as replays of a HIP graph holding 20
+steps' kernels (every kernel runs every step; the graph removes the host
+launch cost, which exceeds the 40 us kernel through the Python API); the
+same K steps through the Python API and autograd are timed and reported as
+eager_ms_per_step.  Device time per step comes from HIP events on the stream
+the kernels run on (torch's current stream).
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -66,33 +70,32 @@ def load_traffic(name: str):
         return None
 
 
-def time_steps(step, launches, steps: int, warmup: int):
-    """Time `steps` eager steps after `warmup` untimed ones.
+GRAPH_STEPS = 20   # steps captured per HIP graph
 
-    `step` is the full step through the public API (autograd included).  The
-    timed region is bracketed by device synchronisations; HIP events recorded
-    on the launch stream (torch's current stream, which the library launches
-    on) around it give the device time per step.  For reference the step's
-    kernels (`launches`) are also captured once into a HIP graph and replayed
-    -- on ROCm a replay adds a few microseconds of launch latency, so the
-    eager loop is the primary figure.
-    Returns (eager wall ms/step, device ms/step, graph-replay wall ms/step)."""
+
+def time_steps(step, launches, steps: int, warmup: int):
+    """Time `steps` steps.
+
+    `step` is the full step through the public API (autograd included);
+    `launches` issues exactly the kernels of one step (the STE backward of
+    the fake-quantize launches none).  After `warmup` eager steps, `steps`
+    eager steps are timed for reference; then GRAPH_STEPS steps' launches
+    are captured into one HIP graph on a side stream and the graph is
+    replayed until `steps` steps have run, between device synchronisations
+    (wall clock) and HIP events on the launch stream (device time).  Every
+    kernel runs every step; the graph only takes the per-launch host cost
+    out of the loop, which otherwise exceeds the 40 us kernel.
+    Returns (wall ms/step, device ms/step, eager wall ms/step)."""
     import torch
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    ev0.record(stream)
     for _ in range(steps):
         step()
-    ev1.record(stream)
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    gpu_ms = ev0.elapsed_time(ev1) / steps
+    eager_ms = (time.perf_counter() - t0) * 1e3 / steps
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -103,16 +106,22 @@ def time_steps(step, launches, steps: int, warmup: int):
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        launches()
-    for _ in range(3):
-        g.replay()
+        for _ in range(GRAPH_STEPS):
+            launches()
+    g.replay()
     torch.cuda.synchronize()
+    replays = max(1, (steps + GRAPH_STEPS - 1) // GRAPH_STEPS)
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for _ in range(steps):
+    ev0.record(stream)
+    for _ in range(replays):
         g.replay()
+    ev1.record(stream)
     torch.cuda.synchronize()
-    graph_ms = (time.perf_counter() - t0) * 1e3 / steps
-    return wall_ms, gpu_ms, graph_ms
+    wall_ms = (time.perf_counter() - t0) * 1e3 / (replays * GRAPH_STEPS)
+    return wall_ms, ev0.elapsed_time(ev1) / (replays * GRAPH_STEPS), eager_ms
 
 
 def bench_fq(steps: int, warmup: int):
@@ -142,9 +151,9 @@ def bench_fq(steps: int, warmup: int):
     def launches():
         hip_fused_fake_quantize(xd, 32, "nearest")
 
-    wall_ms, gpu_ms, graph_ms = time_steps(step, launches, steps, warmup)
+    wall_ms, gpu_ms, eager_ms = time_steps(step, launches, steps, warmup)
     nbytes = 8 * x.numel()
-    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "graph_ms": graph_ms, "bytes": nbytes}
+    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "eager_ms": eager_ms, "bytes": nbytes}
 
 
 def bench_linear(steps: int, warmup: int):
@@ -161,9 +170,9 @@ def bench_linear(steps: int, warmup: int):
     def step():
         hip_linear.linear_forward(X, W, b, 32, True)
 
-    wall_ms, gpu_ms, graph_ms = time_steps(step, step, steps, warmup)
+    wall_ms, gpu_ms, eager_ms = time_steps(step, step, steps, warmup)
     kern = hip_linear.last_forward_kernel_times(X, W, b, reps=max(steps, 10))
-    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "graph_ms": graph_ms, "flops": 2.0 * M * N * K,
+    return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "eager_ms": eager_ms, "flops": 2.0 * M * N * K,
             "kernels": kern}
 
 
@@ -198,6 +207,71 @@ def cpu_baseline_fq(budget_s: float = 12.0):
     }
 
 
+def pmc_pass() -> int:
+    """A short run for rocprofv3 counter collection: 5 NF5 fake-quantize
+    launches at 8192x4096 f32, 3 linear forwards at 4096^3 and, as the
+    calibration reference for HBM byte counters, 5 plain device copies of a
+    known 128 MiB (torch's copy kernel: 128 MiB read + 128 MiB written)."""
+    import torch
+
+    from axs.unified import hip_linear
+    from axs.unified.hip_kernels import hip_fused_fake_quantize
+
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(*FQ_SHAPE, device="cuda", generator=g)
+    for _ in range(5):
+        hip_fused_fake_quantize(x, 32, "nearest")
+    M, K, N = LIN_SHAPE
+    X = torch.randn(M, K, device="cuda", generator=g)
+    W = torch.randn(N, K, device="cuda", generator=g) * K ** -0.5
+    for _ in range(3):
+        hip_linear.linear_forward(X, W, None, 32, True)
+    src = torch.randn(32 * 1024 * 1024, device="cuda", generator=g)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc pass done", flush=True)
+    return 0
+
+
+def gemm_only(n: int, reps: int = 50) -> int:
+    """Times the fp16 MFMA GEMM alone at n^3 (small-integer fp16 operands, so
+    the fp32 result is exact and checked), for launch-shape sweeps with
+    AXS6_GEMM_CFG=<config>.  Prints one JSON line."""
+    import torch
+
+    from axs import _lib
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    A = torch.randint(-4, 5, (n, n), device="cuda", generator=g).half()
+    B = torch.randint(-4, 5, (n, n), device="cuda", generator=g).half()
+    C = torch.empty(n, n, device="cuda")
+    st = _lib.stream_of(A)
+
+    def run():
+        _lib.call("axs6_gemm_f16_nt", A.data_ptr(), n, B.data_ptr(), n, n, n, n, None, None, None,
+                  C.data_ptr(), n, _lib.F32, st)
+
+    run()
+    torch.cuda.synchronize()
+    exact = bool(torch.equal(C, A.float() @ B.float().T))
+    for _ in range(5):
+        run()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / reps * 1e3
+    print(json.dumps({"gemm_cfg": os.environ.get("AXS6_GEMM_CFG", "default"), "n": n, "us": round(us, 1),
+                      "TFLOPs": round(2 * n ** 3 / us / 1e6, 1), "exact": exact}), flush=True)
+    return 0 if exact else 1
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -205,6 +279,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-linear", action="store_true")
+    ap.add_argument("--gemm-only", type=int, default=0, metavar="N",
+                    help="time the fp16 MFMA GEMM alone at N^3 (launch-shape sweeps)")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="short fixed workload for rocprofv3 counter runs (no JSON line)")
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -218,13 +296,17 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
+    if a.pmc_pass:
+        return pmc_pass()
+    if a.gemm_only:
+        return gemm_only(a.gemm_only)
     log(f"device: {torch.cuda.get_device_name()}  steps={a.steps} warmup={a.warmup}")
 
     fq = bench_fq(a.steps, a.warmup)
     gbs = fq["bytes"] / (fq["wall_ms"] * 1e-3) / 1e9
     achieved = fq["bytes"] / (fq["gpu_ms"] * 1e-3) / 1e9
     log(f"fq 8192x4096: {fq['wall_ms']*1e3:.1f} us/step, {fq['gpu_ms']*1e3:.1f} us/launch (device), "
-        f"{achieved:.0f} GB/s; graph replay {fq['graph_ms']*1e3:.1f} us/step")
+        f"{achieved:.0f} GB/s; eager API step {fq['eager_ms']*1e3:.1f} us")
     traffic = load_traffic("fq_8192x4096_traffic.json")
     out = {
         "metric": "NF5 fake-quant GB/s @8192x4096 fp32; AXS-6 linear TFLOP/s @4096^3 bf16",
@@ -234,7 +316,10 @@ def main() -> int:
         "steps": a.steps,
         "warmup": a.warmup,
         "ms_per_step": round(fq["wall_ms"], 5),
-        "graph_replay_ms_per_step": round(fq["graph_ms"], 5),
+        "device_ms_per_launch": round(fq["gpu_ms"], 5),
+        "eager_ms_per_step": round(fq["eager_ms"], 5),
+        "launch": f"steps run as replays of a HIP graph of {GRAPH_STEPS} steps (every kernel runs every step); "
+                  "eager_ms_per_step is the same step through the Python API and autograd",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -258,7 +343,8 @@ def main() -> int:
                 "metric": "AXS-6 linear forward TFLOP/s @4096^3",
                 "value": round(tflops, 1), "unit": "TFLOP/s",
                 "ms_per_step": round(lin["wall_ms"], 5),
-                "graph_replay_ms_per_step": round(lin["graph_ms"], 5),
+                "device_ms_per_step": round(lin["gpu_ms"], 5),
+                "eager_ms_per_step": round(lin["eager_ms"], 5),
                 "dtype": k.get("compute_dtype"),
                 "kernels_ms": {kk: round(v, 5) for kk, v in k.items() if kk.endswith("_ms")},
                 "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1) if gemm_tf else None,
