@@ -216,17 +216,25 @@ def last_forward_kernel_times(X, W, b, reps: int = 20) -> dict:
 
     out = {"compute_dtype": "fp16 MFMA operands (power-of-two row scaled), fp32 accumulate"}
     for name, fn in (("pack_x_ms", pack_x), ("pack_w_ms", pack_w), ("gemm_ms", gemm)):
-        for _ in range(3):
-            fn()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        out[name] = e0.elapsed_time(e1) / reps
+        out[name] = _event_time(fn, reps)
+    # the forward packs X and W in one launch
+    out["pack_xw_ms"] = _event_time(lambda: _lib.call(
+        "axs6_nf5_linear_forward", X.data_ptr(), W.data_ptr(), _lib.ptr(b), y.data_ptr(), code, M, N, K, 32, 1,
+        xq.data_ptr(), sx.data_ptr(), wq.data_ptr(), sw.data_ptr(), st), reps) - out["gemm_ms"]
     return out
+
+
+def _event_time(fn, reps: int) -> float:
+    for _ in range(3):
+        fn()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 def clear_weight_cache() -> None:

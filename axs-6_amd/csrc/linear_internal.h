@@ -24,6 +24,9 @@ struct PackRowsArgs {
     const int32_t* rowx; int32_t* gmax;  // nullable pair
 };
 int launch_pack_rows(const PackRowsArgs& a, const DeviceTables& t, hipStream_t st);
+// Two independent row packs in one launch when they share dtype, mode and
+// row length class (the forward's X and W); otherwise two launches.
+int launch_pack_rows2(const PackRowsArgs& a, const PackRowsArgs& b, const DeviceTables& t, hipStream_t st);
 
 // Global pack: out[r, c] = fp16(FQ(x)[r, c] * 2^(rowx[r] - (*gmax - 15))),
 // zero for cols <= c < cols_pad; optional column partial sums of FQ(x):

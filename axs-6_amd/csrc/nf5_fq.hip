@@ -64,19 +64,31 @@ __global__ __launch_bounds__(kThreads) void fq_vec_kernel(const typename Elem<DT
     static_assert(G >= 1 && G <= 8, "group size");
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
-    stage_tables(lut_s, band_w, lut_g, band_g);
     const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
 
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
     u32x4* yv = reinterpret_cast<u32x4*>(y);
     const int tid = threadIdx.x;
     const int64_t step = (int64_t)gridDim.x * (kThreads * kUnroll);
-    for (int64_t base = (int64_t)blockIdx.x * (kThreads * kUnroll); base < n_vec; base += step) {
-        u32x4 raw[kUnroll];
+    // The first tile's HBM loads go out before the LUT is staged, so the two
+    // latencies overlap; later tiles are prefetched one iteration ahead.
+    int64_t base = (int64_t)blockIdx.x * (kThreads * kUnroll);
+    u32x4 raw[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            int64_t vi = base + u * kThreads + tid;
-            raw[u] = vi < n_vec ? stream_load(xv + vi) : u32x4{0u, 0u, 0u, 0u};
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t vi = base + u * kThreads + tid;
+        raw[u] = vi < n_vec ? stream_load(xv + vi) : u32x4{0u, 0u, 0u, 0u};
+    }
+    stage_tables(lut_s, band_w, lut_g, band_g);
+    for (; base < n_vec; base += step) {
+        u32x4 nxt[kUnroll];
+        const int64_t nbase = base + step;
+        if (nbase < n_vec) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int64_t vi = nbase + u * kThreads + tid;
+                nxt[u] = vi < n_vec ? stream_load(xv + vi) : u32x4{0u, 0u, 0u, 0u};
+            }
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
@@ -98,6 +110,10 @@ __global__ __launch_bounds__(kThreads) void fq_vec_kernel(const typename Elem<DT
                 o[j] = fq_value(f[j], s, lut_s, STOCH, uu);
             }
             if (vi < n_vec) stream_store(E::pack(o), yv + vi);
+        }
+        if (nbase < n_vec) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) raw[u] = nxt[u];
         }
     }
 }

@@ -3,8 +3,8 @@
 // through the C ABI of include/axs6.h.
 //
 // Forward  Y = FQ(X) FQ(W)^T + b:
-//   pack_rows(X) -> Xq16 [M, Kp], sx[M]      (FQ + row scale, one HBM pass)
-//   pack_rows(W) -> Wq16 [N, Kp], sw[N]
+//   pack_rows(X), pack_rows(W) in one launch -> Xq16 [M, Kp], sx[M] and
+//   Wq16 [N, Kp], sw[N]                       (FQ + row scale, one HBM pass)
 //   GEMM(Xq16, Wq16) with epilogue 2^(sx[m] + sw[n]) and + b
 // Xq16/sx/Wq16/sw are caller-owned and reused by the backward.
 //
@@ -113,10 +113,9 @@ extern "C" int axs6_nf5_linear_forward(const void* x, const void* w, const float
     const int64_t Kp = pad_to(K, kGemmK);
     PackRowsArgs px{x, dtype, M, K, block_size, quantize_input != 0, false, 0, 0, nullptr,
                     (_Float16*)xq_f16, Kp, Kp, x_shift, nullptr, nullptr, nullptr};
-    if ((rc = launch_pack_rows(px, t, st))) return rc;
     PackRowsArgs pw{w, dtype, N, K, block_size, true, false, 0, 0, nullptr,
                     (_Float16*)wq_f16, Kp, Kp, w_shift, nullptr, nullptr, nullptr};
-    if ((rc = launch_pack_rows(pw, t, st))) return rc;
+    if ((rc = launch_pack_rows2(px, pw, t, st))) return rc;
     GemmArgs g{(const _Float16*)xq_f16, Kp, (const _Float16*)wq_f16, Kp, M, N, Kp, x_shift, w_shift, nullptr, 0,
                bias, y, N, dtype};
     return launch_gemm_f16(g, st);

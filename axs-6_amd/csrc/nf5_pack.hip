@@ -85,7 +85,7 @@ __device__ __forceinline__ void store_f16(_Float16* p, const float* v, int sh_ba
 }
 
 struct PackRowsK {
-    const void* x; int64_t cols; int block;
+    const void* x; int64_t rows; int64_t cols; int block;
     uint64_t seed; uint64_t offset;
     const int32_t* colx;
     _Float16* out; int64_t ld_out; int64_t cols_pad;
@@ -95,31 +95,34 @@ struct PackRowsK {
 };
 
 template <int DT, int MODE, bool COLX, int NV>
-__global__ __launch_bounds__(kPackThreads) void pack_rows_kernel(PackRowsK k) {
+__global__ __launch_bounds__(kPackThreads) void pack_rows_kernel(PackRowsK k, PackRowsK k2) {
     using E = Elem<DT>;
     using S = typename E::S;
     constexpr int V = E::V;
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
     __shared__ int red[2][kPackThreads / 64];
-    stage_tables(lut_s, band_w, k.lut, k.band);
     const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
 
+    // two operands may share one launch: workgroups past k.rows take k2
+    const bool second = blockIdx.x >= k.rows;
+    const PackRowsK q = second ? k2 : k;      // by value: field-wise selects, no stack copy
     const int tid = threadIdx.x;
-    const int64_t r = blockIdx.x;
-    const int64_t nvec = k.cols / V;
-    const int g = k.block / V;
-    const S* xr = reinterpret_cast<const S*>(k.x) + r * k.cols;
+    const int64_t r = second ? blockIdx.x - k.rows : blockIdx.x;
+    const int64_t nvec = q.cols / V;
+    const int g = q.block / V;
+    const S* xr = reinterpret_cast<const S*>(q.x) + r * q.cols;
 
+    // the row's HBM loads go out before the LUT is staged
     float f[NV][V];
     int eb[NV];
     u32x4 raw[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int64_t vi = tid + (int64_t)kPackThreads * j;
-        raw[j] = vi < nvec ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr) + vi)
-                           : u32x4{0u, 0u, 0u, 0u};
+        raw[j] = vi < nvec ? *(reinterpret_cast<const u32x4*>(xr) + vi) : u32x4{0u, 0u, 0u, 0u};
     }
+    stage_tables(lut_s, band_w, q.lut, q.band);
     int tmax = INT_MIN, rmax = INT_MIN;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
@@ -137,7 +140,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_rows_kernel(PackRowsK k) {
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const float u = (MODE == kStochastic)
-                    ? dither_uniform(k.seed, k.offset + (uint64_t)(r * k.cols + vi * V + e)) : 0.0f;
+                    ? dither_uniform(q.seed, q.offset + (uint64_t)(r * q.cols + vi * V + e)) : 0.0f;
                 f[j][e] = fq_value(f[j][e], s, lut_s, MODE == kStochastic, u);
             }
         }
@@ -148,7 +151,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_rows_kernel(PackRowsK k) {
             if (eb[j] != INT_MIN) {
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
-                    const int b = eb[j] + k.colx[vi * V + e];
+                    const int b = eb[j] + q.colx[vi * V + e];
                     tmax = b > tmax ? b : tmax;
                 }
             }
@@ -169,8 +172,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_rows_kernel(PackRowsK k) {
     }
     const int S_row = (tmax == INT_MIN) ? 0 : tmax - kF16MaxExp;
 
-    if (k.out) {
-        _Float16* orow = k.out + r * k.ld_out;
+    if (q.out) {
+        _Float16* orow = q.out + r * q.ld_out;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int64_t vi = tid + (int64_t)kPackThreads * j;
@@ -178,19 +181,19 @@ __global__ __launch_bounds__(kPackThreads) void pack_rows_kernel(PackRowsK k) {
                 int colx_v[V];
                 if constexpr (COLX) {
 #pragma unroll
-                    for (int e = 0; e < V; ++e) colx_v[e] = k.colx[vi * V + e];
+                    for (int e = 0; e < V; ++e) colx_v[e] = q.colx[vi * V + e];
                 }
                 store_f16<V>(orow + vi * V, f[j], -S_row, COLX ? colx_v : nullptr);
             }
         }
-        const int64_t zvec = (k.cols_pad - k.cols) / 8;   // 8-half zero chunks
+        const int64_t zvec = (q.cols_pad - q.cols) / 8;   // 8-half zero chunks
         for (int64_t z = tid; z < zvec; z += kPackThreads)
-            *reinterpret_cast<u32x4*>(orow + k.cols + z * 8) = u32x4{0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4*>(orow + q.cols + z * 8) = u32x4{0u, 0u, 0u, 0u};
     }
     if (tid == 0) {
-        k.s_out[r] = S_row;
-        if (k.rmax_out) k.rmax_out[r] = rmax;
-        if (k.gmax && rmax != INT_MIN) atomicMax(k.gmax, rmax + (k.rowx ? k.rowx[r] : 0));
+        q.s_out[r] = S_row;
+        if (q.rmax_out) q.rmax_out[r] = rmax;
+        if (q.gmax && rmax != INT_MIN) atomicMax(q.gmax, rmax + (q.rowx ? q.rowx[r] : 0));
     }
 }
 
@@ -270,25 +273,26 @@ __global__ __launch_bounds__(256) void transpose_f16_kernel(const uint16_t* __re
 __global__ void init_gmax_kernel(int32_t* p) { *p = INT_MIN; }
 
 template <int DT, int MODE, bool COLX>
-void dispatch_rows_nv(const PackRowsK& k, int64_t rows, int nv, hipStream_t st) {
+void dispatch_rows_nv(const PackRowsK& k, const PackRowsK& k2, int64_t rows, int nv, hipStream_t st) {
     const dim3 grid((unsigned)rows);
     switch (nv) {
-        case 1: pack_rows_kernel<DT, MODE, COLX, 1><<<grid, kPackThreads, 0, st>>>(k); break;
-        case 2: pack_rows_kernel<DT, MODE, COLX, 2><<<grid, kPackThreads, 0, st>>>(k); break;
-        case 4: pack_rows_kernel<DT, MODE, COLX, 4><<<grid, kPackThreads, 0, st>>>(k); break;
-        case 8: pack_rows_kernel<DT, MODE, COLX, 8><<<grid, kPackThreads, 0, st>>>(k); break;
-        default: pack_rows_kernel<DT, MODE, COLX, 16><<<grid, kPackThreads, 0, st>>>(k); break;
+        case 1: pack_rows_kernel<DT, MODE, COLX, 1><<<grid, kPackThreads, 0, st>>>(k, k2); break;
+        case 2: pack_rows_kernel<DT, MODE, COLX, 2><<<grid, kPackThreads, 0, st>>>(k, k2); break;
+        case 4: pack_rows_kernel<DT, MODE, COLX, 4><<<grid, kPackThreads, 0, st>>>(k, k2); break;
+        case 8: pack_rows_kernel<DT, MODE, COLX, 8><<<grid, kPackThreads, 0, st>>>(k, k2); break;
+        default: pack_rows_kernel<DT, MODE, COLX, 16><<<grid, kPackThreads, 0, st>>>(k, k2); break;
     }
 }
 
 template <int DT>
-void dispatch_rows(const PackRowsK& k, int64_t rows, int mode, bool colx, int nv, hipStream_t st) {
+void dispatch_rows(const PackRowsK& k, const PackRowsK& k2, int64_t rows, int mode, bool colx, int nv,
+                   hipStream_t st) {
     if (mode == kRaw) {
-        if (colx) dispatch_rows_nv<DT, kRaw, true>(k, rows, nv, st); else dispatch_rows_nv<DT, kRaw, false>(k, rows, nv, st);
+        if (colx) dispatch_rows_nv<DT, kRaw, true>(k, k2, rows, nv, st); else dispatch_rows_nv<DT, kRaw, false>(k, k2, rows, nv, st);
     } else if (mode == kNearest) {
-        if (colx) dispatch_rows_nv<DT, kNearest, true>(k, rows, nv, st); else dispatch_rows_nv<DT, kNearest, false>(k, rows, nv, st);
+        if (colx) dispatch_rows_nv<DT, kNearest, true>(k, k2, rows, nv, st); else dispatch_rows_nv<DT, kNearest, false>(k, k2, rows, nv, st);
     } else {
-        if (colx) dispatch_rows_nv<DT, kStochastic, true>(k, rows, nv, st); else dispatch_rows_nv<DT, kStochastic, false>(k, rows, nv, st);
+        if (colx) dispatch_rows_nv<DT, kStochastic, true>(k, k2, rows, nv, st); else dispatch_rows_nv<DT, kStochastic, false>(k, k2, rows, nv, st);
     }
 }
 
@@ -305,7 +309,9 @@ constexpr int kGlobalRowsPerChunk = 64;
 
 int64_t pack_global_chunks(int64_t rows) { return (rows + kGlobalRowsPerChunk - 1) / kGlobalRowsPerChunk; }
 
-int launch_pack_rows(const PackRowsArgs& a, const DeviceTables& t, hipStream_t st) {
+namespace {
+
+int check_pack_rows(const PackRowsArgs& a, int* nv_out) {
     const int V = a.dtype == AXS6_F32 ? 4 : 8;
     if (a.cols % a.block != 0)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: cols (%lld) must be a multiple of block_size", (long long)a.cols);
@@ -317,15 +323,49 @@ int launch_pack_rows(const PackRowsArgs& a, const DeviceTables& t, hipStream_t s
     if (per > 16)
         return fail(AXS6_ERR_UNSUPPORTED, "pack_rows: rows of %lld elements exceed the register-resident limit (%d)",
                     (long long)a.cols, 16 * kPackThreads * V);
-    const int nv = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
+    *nv_out = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
+    return AXS6_OK;
+}
+
+PackRowsK to_kernel_args(const PackRowsArgs& a, const DeviceTables& t) {
+    return PackRowsK{a.x, a.rows, a.cols, a.block, a.seed, a.offset, a.colx, a.out, a.ld_out, a.cols_pad,
+                     a.s_out, a.rmax_out, a.rowx, a.gmax, t.lut, t.band};
+}
+
+int pack_mode(const PackRowsArgs& a) { return a.fake_quant ? (a.stochastic ? kStochastic : kNearest) : kRaw; }
+
+}  // namespace
+
+int launch_pack_rows(const PackRowsArgs& a, const DeviceTables& t, hipStream_t st) {
+    int nv = 0;
+    int rc = check_pack_rows(a, &nv);
+    if (rc) return rc;
     if (a.rows == 0) return AXS6_OK;
-    PackRowsK k{a.x, a.cols, a.block, a.seed, a.offset, a.colx, a.out, a.ld_out, a.cols_pad,
-                a.s_out, a.rmax_out, a.rowx, a.gmax, t.lut, t.band};
-    const int mode = a.fake_quant ? (a.stochastic ? kStochastic : kNearest) : kRaw;
+    const PackRowsK k = to_kernel_args(a, t);
     const bool colx = a.colx != nullptr;
-    if (a.dtype == AXS6_F32) dispatch_rows<AXS6_F32>(k, a.rows, mode, colx, nv, st);
-    else if (a.dtype == AXS6_BF16) dispatch_rows<AXS6_BF16>(k, a.rows, mode, colx, nv, st);
-    else dispatch_rows<AXS6_F16>(k, a.rows, mode, colx, nv, st);
+    if (a.dtype == AXS6_F32) dispatch_rows<AXS6_F32>(k, k, a.rows, pack_mode(a), colx, nv, st);
+    else if (a.dtype == AXS6_BF16) dispatch_rows<AXS6_BF16>(k, k, a.rows, pack_mode(a), colx, nv, st);
+    else dispatch_rows<AXS6_F16>(k, k, a.rows, pack_mode(a), colx, nv, st);
+    return check_launch("pack_rows");
+}
+
+int launch_pack_rows2(const PackRowsArgs& a, const PackRowsArgs& b, const DeviceTables& t, hipStream_t st) {
+    int nva = 0, nvb = 0;
+    int rc = check_pack_rows(a, &nva);
+    if (rc) return rc;
+    if ((rc = check_pack_rows(b, &nvb))) return rc;
+    const bool same = a.dtype == b.dtype && pack_mode(a) == pack_mode(b) && nva == nvb &&
+                      (a.colx != nullptr) == (b.colx != nullptr);
+    if (!same || a.rows == 0 || b.rows == 0) {
+        if ((rc = launch_pack_rows(a, t, st))) return rc;
+        return launch_pack_rows(b, t, st);
+    }
+    const PackRowsK ka = to_kernel_args(a, t), kb = to_kernel_args(b, t);
+    const bool colx = a.colx != nullptr;
+    const int64_t rows = a.rows + b.rows;
+    if (a.dtype == AXS6_F32) dispatch_rows<AXS6_F32>(ka, kb, rows, pack_mode(a), colx, nva, st);
+    else if (a.dtype == AXS6_BF16) dispatch_rows<AXS6_BF16>(ka, kb, rows, pack_mode(a), colx, nva, st);
+    else dispatch_rows<AXS6_F16>(ka, kb, rows, pack_mode(a), colx, nva, st);
     return check_launch("pack_rows");
 }
 
