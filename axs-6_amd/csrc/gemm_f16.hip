@@ -6,13 +6,11 @@
 // Tiling.  A workgroup of WGM x WGN waves owns a BM x BN tile of C; each wave
 // a (BM/WGM) x (BN/WGN) sub-tile of 32x32 MFMA blocks
 // (v_mfma_f32_32x32x16_f16: K = 16 per instruction, 16 fp32 accumulators per
-// lane).  Per K-step of 64 halves the A and B tiles are staged through LDS:
-// each 64-half row is 8 slots of 16 bytes, and chunk c of row r lives in slot
-// c ^ (r & 7), so the 16-byte fragment reads of 8 consecutive rows land in 8
-// distinct bank groups without padding.  The next K-step's tiles are fetched
-// into registers (buffer loads: rows past M/N read as zero through the
-// buffer's range check) while the current one is multiplied; two LDS buffers,
-// one barrier per step.
+// lane).  Per K-step of 64 halves the A and B tiles go from HBM straight into
+// LDS (buffer_load ... lds; rows past M/N read as zero through the buffer's
+// range check) while the previous slab is multiplied; two LDS slabs, one
+// barrier per step.  Each 64-half row is 8 slots of 16 bytes, XOR-swizzled
+// (swz_key) so the 16-byte fragment reads are bank-conflict free.
 //
 // Schedule.  Workgroup ids are dispatched round-robin over the 8 XCDs; the
 // id is remapped so that each XCD receives a contiguous range of the grouped
@@ -21,7 +19,13 @@
 //
 // Epilogue.  v = ldexp(acc, row_exp[m] + col_exp[n] + glob) + bias[n], written
 // as fp32, bf16 or fp16; the exponents undo the packing kernels' power-of-two
-// row scales exactly.
+// row scales exactly.  The accumulators leave through LDS: each wave stages
+// one 32-row block row of its sub-tile at a time and writes whole row
+// segments with 16 bytes per lane (f32) or 8 bytes (16-bit outputs), so a
+// store instruction covers full 128-byte lines.  With one tile per CU every
+// tile finishes at once; the scattered per-lane stores of the MFMA layout
+// (two 128-byte rows per instruction) cost ~8% of the 4096^3 GEMM, the staged
+// stores ~1%.
 #include <limits.h>
 #include <stdlib.h>
 
@@ -122,24 +126,32 @@ __device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const char* as, 
     }
 }
 
-// Writes one 32x32 accumulator block.  Lane layout of v_mfma_f32_32x32x16:
-// column = lane % 32, row = 8 * (r / 4) + 4 * (lane / 32) + r % 4 for
-// accumulator register r; `row0` already includes the 4 * (lane / 32) term.
-__device__ __forceinline__ void store_block(const f32x16 a, const GemmK& g, int row0, int col, int gexp) {
-    if (col >= g.N) return;
-    const int cexp = (g.col_exp ? g.col_exp[col] : 0) + gexp;
-    const float bias = g.bias ? g.bias[col] : 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int row = row0 + (r >> 2) * 8 + (r & 3);
-        if (row < g.M) {
-            const int e = cexp + (g.row_exp ? g.row_exp[row] : 0);
-            const float v = __builtin_amdgcn_ldexpf(a[r], e) + bias;
-            const int64_t o = (int64_t)row * g.ldo + col;
-            if (g.out_dtype == AXS6_F32) reinterpret_cast<float*>(g.out)[o] = v;
-            else if (g.out_dtype == AXS6_BF16) reinterpret_cast<uint16_t*>(g.out)[o] = to_bf16(v);
-            else reinterpret_cast<_Float16*>(g.out)[o] = (_Float16)v;
+// Writes 4 consecutive output values of row `row` starting at column `col`
+// (col % 4 == 0): one vector store when the 4 columns exist and the row
+// segment is aligned, else element by element up to N.
+__device__ __forceinline__ void store4(const GemmK& g, int row, int col, const float (&v)[4], bool vec) {
+    const int64_t o = (int64_t)row * g.ldo + col;
+    if (vec && col + 3 < g.N) {
+        if (g.out_dtype == AXS6_F32) {
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(g.out) + o) = make_float4(v[0], v[1], v[2], v[3]);
+        } else if (g.out_dtype == AXS6_BF16) {
+            uint2 w;
+            w.x = (uint32_t)to_bf16(v[0]) | ((uint32_t)to_bf16(v[1]) << 16);
+            w.y = (uint32_t)to_bf16(v[2]) | ((uint32_t)to_bf16(v[3]) << 16);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(g.out) + o) = w;
+        } else {
+            typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+            f16x4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+            *reinterpret_cast<f16x4*>(reinterpret_cast<_Float16*>(g.out) + o) = h;
         }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        if (col + t >= g.N) break;
+        if (g.out_dtype == AXS6_F32) reinterpret_cast<float*>(g.out)[o + t] = v[t];
+        else if (g.out_dtype == AXS6_BF16) reinterpret_cast<uint16_t*>(g.out)[o + t] = to_bf16(v[t]);
+        else reinterpret_cast<_Float16*>(g.out)[o + t] = (_Float16)v[t];
     }
 }
 
@@ -272,12 +284,57 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
         mma_step<BK, TM, TN, SCHED>(acc, slab, slab + BM * RB, a_row0, b_row0, fh);
     }
 
+    // ---- epilogue through LDS ------------------------------------------------
+    // Accumulator r of block (i, j) holds row 8*(r/4) + 4*(lane/32) + r%4,
+    // column lane%32 of that 32x32 block.  Each wave stages its block row i
+    // (32 x WN floats, row stride WN+4 to spread banks) in its own LDS region,
+    // then reads it back as 4 consecutive columns per lane.  The slabs are
+    // dead once every wave has left the K loop (barrier); after that a wave
+    // touches only its own region, and LDS operations of one wave complete in
+    // order, so no further barrier is needed.
+    constexpr int LDW = WN + 4;
+    constexpr int LANES_PER_ROW = WN / 4;
+    constexpr int ROWS_PER_PASS = 64 / LANES_PER_ROW;
+    static_assert(NW * 32 * LDW * 4 <= STAGES * SLAB, "epilogue staging must fit in the slab LDS");
+    static_assert(64 % LANES_PER_ROW == 0, "wave tile width");
+    wait_vmcnt<0>();
+    __syncthreads();
+    float* ws = reinterpret_cast<float*>(smem) + wave * (32 * LDW);
     const int gexp = g.glob_exp ? (*g.glob_exp == INT_MIN ? 0 : *g.glob_exp + g.glob_add) : 0;
+    const int c4 = (lane % LANES_PER_ROW) * 4;
+    const int rsub = lane / LANES_PER_ROW;
+    const int gcol = n0 + wn * WN + c4;
+    int cexp[4];
+    float cbias[4];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int t = 0; t < 4; ++t) {
+        const bool in = gcol + t < g.N;
+        cexp[t] = gexp + ((g.col_exp && in) ? g.col_exp[gcol + t] : 0);
+        cbias[t] = (g.bias && in) ? g.bias[gcol + t] : 0.0f;
+    }
+    const int esize = g.out_dtype == AXS6_F32 ? 4 : 2;
+    const bool vec = (g.ldo % 4 == 0) && ((uintptr_t)g.out % (4 * esize) == 0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-            store_block(acc[i][j], g, m0 + wm * WM + i * 32 + fh * 4, n0 + wn * WN + j * 32 + fr, gexp);
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                ws[((r >> 2) * 8 + (r & 3) + fh * 4) * LDW + j * 32 + fr] = acc[i][j][r];
+#pragma unroll
+        for (int rr = 0; rr < 32; rr += ROWS_PER_PASS) {
+            const int lr = rr + rsub;
+            const int grow = m0 + wm * WM + i * 32 + lr;
+            const float* src = ws + lr * LDW + c4;
+            float v[4] = {src[0], src[1], src[2], src[3]};
+            if (grow < g.M && gcol < g.N) {
+                const int rexp = g.row_exp ? g.row_exp[grow] : 0;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) v[t] = __builtin_amdgcn_ldexpf(v[t], rexp + cexp[t]) + cbias[t];
+                store4(g, grow, gcol, v, vec);
+            }
+        }
+    }
 #endif
 }
 

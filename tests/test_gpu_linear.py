@@ -62,6 +62,37 @@ def test_gemm_epilogue_exponents_bias_and_dtypes():
         assert torch.equal(got, want.to(dt)), dt
 
 
+@pytest.mark.parametrize("N,ldo,offset", [(161, 161, 0), (250, 256, 0), (256, 260, 1), (37, 40, 2)],
+                         ids=["ragged_n", "strided", "misaligned_base", "narrow"])
+def test_gemm_epilogue_ragged_and_strided_output(N, ldo, offset):
+    # the staged epilogue writes 4 columns per lane: vector stores only where the
+    # row segment is whole and aligned, element stores elsewhere; nothing may be
+    # written outside [row, 0:N) of each output row
+    from axs import _lib
+
+    M, Kp = 300, 192
+    g = torch.Generator().manual_seed(N + ldo)
+    A = torch.randint(-4, 5, (M, Kp), generator=g).to(torch.float16)
+    B = torch.randint(-4, 5, (N, Kp), generator=g).to(torch.float16)
+    re = torch.randint(-10, 10, (M,), generator=g, dtype=torch.int32)
+    ce = torch.randint(-10, 10, (N,), generator=g, dtype=torch.int32)
+    bias = torch.randn(N, generator=g)
+    acc = A.double() @ B.double().T
+    want = (acc * torch.exp2((re[:, None] + ce[None, :]).double())).float() + bias
+    # device copies held in names: the call is asynchronous and must not see freed temporaries
+    Ad, Bd, red, ced, biasd = (t.to(DEV) for t in (A, B, re, ce, bias))
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        buf = torch.full((offset + M * ldo + 8,), 7.0, dtype=dt, device=DEV)
+        _lib.call("axs6_gemm_f16_nt", Ad.data_ptr(), Kp, Bd.data_ptr(), Kp, M, N, Kp,
+                  _lib.ptr(red), _lib.ptr(ced), _lib.ptr(biasd),
+                  buf.data_ptr() + offset * buf.element_size(), ldo, _lib.DTYPE_CODE[dt], _lib.stream_of(buf))
+        host = buf.cpu()
+        out = host[offset:offset + M * ldo].view(M, ldo)
+        assert torch.equal(out[:, :N], want.to(dt)), dt
+        untouched = torch.cat([host[:offset], out[:, N:].reshape(-1), host[offset + M * ldo:]])
+        assert bool((untouched == 7.0).all()), f"{dt}: wrote outside the output rows"
+
+
 def _oracle_linear(x, w, b):
     xq = oracle.fake_quantize(x.numpy(), 32)
     wq = oracle.fake_quantize(w.numpy(), 32)
