@@ -28,18 +28,42 @@ int launch_pack_rows(const PackRowsArgs& a, const DeviceTables& t, hipStream_t s
 // row length class (the forward's X and W); otherwise two launches.
 int launch_pack_rows2(const PackRowsArgs& a, const PackRowsArgs& b, const DeviceTables& t, hipStream_t st);
 
-// Global pack: out[r, c] = fp16(FQ(x)[r, c] * 2^(rowx[r] - (*gmax - 15))),
-// zero for cols <= c < cols_pad; optional column partial sums of FQ(x):
-// partial[chunk, c] = sum over rows of chunk (fixed order).
-struct PackGlobalArgs {
+// Transposed global pack: out[c, r] = fp16(FQ(x)[r, c] * 2^(rowx[r] - (*gmax - 15)))
+// for c < cols, r < rows; zero for rows <= r < pad_to(rows, 64) (ld_out >= that).
+// FQ uses the same dither counters as pack_rows on the same x, seed and offset.
+// Optional column partial sums of FQ(x): partial[chunk, c] over the 64 rows of
+// chunk, in a fixed order.  gmax may be null (shift 0).
+// Also, with out_r: the row-major operand out_r[r, c] = fp16(FQ(x)[r, c] *
+// 2^(colx_r[c] - shift_r[r])) for r < rows, zero for cols <= c < pad_to(cols, 64)
+// -- what pack_rows writes, with the row shifts taken from a statistics-only
+// pack_rows pass (mode raw, no output).
+struct PackTArgs {
     const void* x; int dtype; int64_t rows; int64_t cols; int block;
     bool fake_quant; bool stochastic; uint64_t seed; uint64_t offset;
     const int32_t* rowx;            // nullable (0)
-    const int32_t* gmax;            // device scalar
-    _Float16* out; int64_t ld_out; int64_t cols_pad;   // out nullable
-    float* partial; int rows_per_chunk;                 // nullable
+    const int32_t* gmax;            // device scalar, nullable
+    _Float16* out; int64_t ld_out;  // out nullable
+    _Float16* out_r; int64_t ld_r;  // out_r nullable
+    const int32_t* colx_r;          // nullable (0)
+    const int32_t* shift_r;         // required with out_r
+    float* partial;                 // nullable
 };
-int launch_pack_global(const PackGlobalArgs& a, const DeviceTables& t, hipStream_t st);
+int launch_pack_t(const PackTArgs& a, const DeviceTables& t, hipStream_t st);
+
+// Row statistics of x (block exponents only): shift[r] = max over the row's
+// finite nonzero blocks of (e1 + max colx over the block) - 15 (0 if none),
+// and gmax = max over rows of (max block e1 + rowx[r]) (INT_MIN if none) --
+// the shifts pack_rows derives.  scratch: 2 * rows int32 of device memory.
+struct RowStatsArgs {
+    const void* x; int dtype; int64_t rows; int64_t cols; int block;
+    const int32_t* colx;            // nullable (0)
+    int32_t* shift;                 // nullable
+    const int32_t* rowx;            // nullable (0)
+    int32_t* gmax;                  // nullable
+    int32_t* scratch;               // [2 * rows]
+};
+int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t st);
+
 int64_t pack_global_chunks(int64_t rows);
 
 // db[c] = sum_k partial[k, c], k in order.

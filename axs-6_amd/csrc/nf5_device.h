@@ -181,14 +181,9 @@ __device__ __forceinline__ float normalise(uint32_t abits, const FqScale& s) {
     return __builtin_amdgcn_ldexpf(__uint_as_float(abits), -s.e1);
 }
 
-__device__ __forceinline__ int lut_index(float n, bool stochastic, float u) {
-    float t;
-    if (stochastic) {
-        float d = (u - 0.5f) / 1023.0f;   // IEEE division, as torch
-        t = (n + d) * 1023.0f;
-    } else {
-        t = n * 1023.0f;
-    }
+// `d` is the dither (U - 0.5) / 1023 of the stochastic mode (0 for nearest).
+__device__ __forceinline__ int lut_index(float n, bool stochastic, float d) {
+    float t = stochastic ? (n + d) * 1023.0f : n * 1023.0f;
     t = (t == t) ? t : 0.0f;              // NaN -> INT_MIN -> clamped to 0 in torch
     int i = (int)t;                       // truncation toward zero
     return i < 0 ? 0 : (i > kLutMax ? kLutMax : i);
@@ -198,28 +193,107 @@ __device__ __forceinline__ float torch_sign(float x) {
     return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
 }
 
-__device__ __forceinline__ float fq_value(float x, const FqScale& s, const float* lut, bool stochastic, float u) {
+__device__ __forceinline__ float fq_value(float x, const FqScale& s, const float* lut, bool stochastic, float d) {
     uint32_t ab = __float_as_uint(x) & 0x7fffffffu;
     float n = normalise(ab, s);
-    float rec = lut[lut_index(n, stochastic, u)];
+    float rec = lut[lut_index(n, stochastic, d)];
     float r = (torch_sign(x) * rec) * s.scale;
     return s.nan_block ? __uint_as_float(kNanBits) : r;
 }
 
-// splitmix64 mix of (seed + i * golden); top 24 bits -> U[0,1).
-__device__ __forceinline__ float dither_uniform(uint64_t seed, uint64_t i) {
-    uint64_t z = seed + i * 0x9E3779B97F4A7C15ull;
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    z ^= z >> 31;
-    return (float)(uint32_t)(z >> 40) * (1.0f / 16777216.0f);
+// fused_fake_quantize of the V elements of one 16-byte vector whose block
+// scale is s; d[e] is element e's dither (U - 0.5) / 1023 (unused in nearest
+// mode).  Blocks with a NaN or an infinite scale take the per-element general
+// path (fq_value).  When no lane of the wave holds such a block -- the normal
+// case, tested with one ballot so the branch is uniform -- a shorter sequence
+// gives the same bits: the scale 2^e1 exceeds every |x| of the block, so
+// n = |x| 2^-e1 < 1 is finite, (n + d) * 1023 lies in (-0.51, 1023.5) and
+// truncates into [0, 1023], and (sign(x) * lut) * scale equals lut * scale
+// with x's sign bit (rounding to nearest is symmetric), or +0 where x is +-0
+// (torch.sign(-0.0) is +0).
+template <int V>
+__device__ __forceinline__ void fq_vector(float (&f)[V], const FqScale& s, const float* lut, bool stochastic,
+                                          const float (&d)[V]) {
+    const bool special = s.nan_block || s.inf_scale;
+    if (__builtin_amdgcn_ballot_w64(special) != 0) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) f[e] = fq_value(f[e], s, lut, stochastic, d[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const uint32_t xb = __float_as_uint(f[e]);
+            const uint32_t ab = xb & 0x7fffffffu;
+            const float n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -s.e1);
+            const float t = stochastic ? (n + d[e]) * 1023.0f : n * 1023.0f;
+            int i = (int)t;
+            i = i < 0 ? 0 : (i > kLutMax ? kLutMax : i);   // in range already; keeps the LDS index bounded
+            const float mag = lut[i] * s.scale;
+            f[e] = __uint_as_float(ab == 0u ? 0u : (__float_as_uint(mag) ^ (xb & 0x80000000u)));
+        }
+    }
 }
 
-// Stages the LUT (and the band table) in LDS; needs kThreads == 256.
+// Dither stream of the stochastic mode.  A call's 64-bit seed is turned into
+// a key once (the splitmix64 finaliser); the draw for element counter i is a
+// 32-bit multiply-xorshift hash (the "lowbias32" constants published by
+// C. Wellons) of i's low word mixed with the key and i's high word, and its
+// top 24 bits scaled by 2^-24 give U in [0, 1) -- the resolution of
+// torch.rand's float32 draws.  Three 32-bit multiplies per element instead of
+// splitmix64's 64-bit ones, which made the dY packing kernels VALU-bound.
+__host__ __device__ __forceinline__ uint64_t dither_key(uint64_t seed) {
+    uint64_t z = seed + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint32_t dither_mix(uint32_t h) {
+    h ^= h >> 16;
+    h *= 0x7feb352du;
+    h ^= h >> 15;
+    h *= 0x846ca68bu;
+    h ^= h >> 16;
+    return h;
+}
+
+// (U - 0.5) / 1023 for the draw U = (h >> 8) * 2^-24, bit-identical to the
+// IEEE float division torch performs: J = U * 2^24 - 2^23 is an exact
+// integer, J / 1023 is rounded by a reciprocal product and one FMA residual
+// correction (identical to the correctly rounded quotient for every one of
+// the 2^24 possible J), and the rescale by 2^-24 is exact.
+__device__ __forceinline__ float dither_from_hash(uint32_t h) {
+    const float fj = (float)((int)(h >> 8) - (1 << 23));
+    float q = fj * (1.0f / 1023.0f);
+    const float r = __builtin_fmaf(-q, 1023.0f, fj);
+    q = __builtin_fmaf(r, 1.0f / 1023.0f, q);
+    return q * (1.0f / 16777216.0f);
+}
+
+// The dither (U - 0.5) / 1023 of element counter i.
+__device__ __forceinline__ float dither_step(uint64_t key, uint64_t i) {
+    const uint32_t hg = (uint32_t)(i >> 32) * 0x9E3779B9u + (uint32_t)(key >> 32);
+    return dither_from_hash(dither_mix((uint32_t)i ^ (uint32_t)key ^ hg));
+}
+
+// The same for the elements base, base + 1, ... of one vector: the high-word
+// term is computed once and carried across a 2^32 boundary inside the vector.
+struct DitherVec {
+    uint32_t klo, hg, lo0;
+};
+__device__ __forceinline__ DitherVec dither_vec(uint64_t key, uint64_t base) {
+    return DitherVec{(uint32_t)key, (uint32_t)(base >> 32) * 0x9E3779B9u + (uint32_t)(key >> 32), (uint32_t)base};
+}
+__device__ __forceinline__ float dither_step(const DitherVec& v, int e) {
+    const uint32_t lo = v.lo0 + (uint32_t)e;
+    const uint32_t hg = lo < v.lo0 ? v.hg + 0x9E3779B9u : v.hg;
+    return dither_from_hash(dither_mix(lo ^ v.klo ^ hg));
+}
+
+// Stages the LUT (and the band table) in LDS; needs at least 256 threads.
 __device__ __forceinline__ void stage_tables(float* lut_s, uint32_t* band_w, const float* lut_g,
                                              const uint8_t* band_g) {
     const int tid = threadIdx.x;
-    reinterpret_cast<float4*>(lut_s)[tid] = reinterpret_cast<const float4*>(lut_g)[tid];
+    if (tid < kLutSize / 4) reinterpret_cast<float4*>(lut_s)[tid] = reinterpret_cast<const float4*>(lut_g)[tid];
     if (tid < kBandSize / 4) band_w[tid] = reinterpret_cast<const uint32_t*>(band_g)[tid];
     __syncthreads();
 }

@@ -57,7 +57,7 @@ __global__ __launch_bounds__(kThreads) void fq_vec_kernel(const typename Elem<DT
                                                           typename Elem<DT>::S* y, int64_t n_vec,
                                                           const float* __restrict__ lut_g,
                                                           const uint8_t* __restrict__ band_g,
-                                                          uint64_t seed, uint64_t offset) {
+                                                          uint64_t key, uint64_t offset) {
     using E = Elem<DT>;
     constexpr int V = E::V;
     constexpr int G = BS / V;
@@ -103,13 +103,12 @@ __global__ __launch_bounds__(kThreads) void fq_vec_kernel(const typename Elem<DT
             }
             m = group_umax<G>(m);
             FqScale s = fq_scale(m, band_s);
-            float o[V];
+            float d[V];
+            const DitherVec dv = dither_vec(key, offset + (uint64_t)(vi * V));
 #pragma unroll
-            for (int j = 0; j < V; ++j) {
-                float uu = STOCH ? dither_uniform(seed, offset + (uint64_t)(vi * V + j)) : 0.0f;
-                o[j] = fq_value(f[j], s, lut_s, STOCH, uu);
-            }
-            if (vi < n_vec) stream_store(E::pack(o), yv + vi);
+            for (int j = 0; j < V; ++j) d[j] = STOCH ? dither_step(dv, j) : 0.0f;
+            fq_vector<V>(f, s, lut_s, STOCH, d);
+            if (vi < n_vec) stream_store(E::pack(f), yv + vi);
         }
         if (nbase < n_vec) {
 #pragma unroll
@@ -124,7 +123,7 @@ __global__ __launch_bounds__(kThreads) void fq_scalar_kernel(const typename Elem
                                                              int64_t cols, int64_t nblk,
                                                              const float* __restrict__ lut_g,
                                                              const uint8_t* __restrict__ band_g,
-                                                             uint64_t seed, uint64_t offset) {
+                                                             uint64_t key, uint64_t offset) {
     using E = Elem<DT>;
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
@@ -147,8 +146,8 @@ __global__ __launch_bounds__(kThreads) void fq_scalar_kernel(const typename Elem
         float f = valid ? E::to_f(x[gi]) : 0.0f;
         uint32_t m = group_umax_shfl<BS>(__float_as_uint(f) & 0x7fffffffu);
         FqScale s = fq_scale(m, band_s);
-        float uu = STOCH ? dither_uniform(seed, offset + (uint64_t)gi) : 0.0f;
-        float o = fq_value(f, s, lut_s, STOCH, uu);
+        const float d = STOCH ? dither_step(key, offset + (uint64_t)gi) : 0.0f;
+        float o = fq_value(f, s, lut_s, STOCH, d);
         if (valid) y[gi] = E::from_f(o);
     }
 }
@@ -164,7 +163,7 @@ template <int DT, int BS, bool STOCH>
 __global__ __launch_bounds__(kThreads) void quantize_kernel(
     const typename Elem<DT>::S* x, int64_t rows, int64_t cols, int64_t nblk,
     const float* __restrict__ lut_g, const uint8_t* __restrict__ band_g,
-    const uint8_t* __restrict__ rev_g, uint64_t seed, uint64_t offset, uint8_t* __restrict__ exps,
+    const uint8_t* __restrict__ rev_g, uint64_t key, uint64_t offset, uint8_t* __restrict__ exps,
     uint8_t* __restrict__ codes, uint8_t* __restrict__ signs, typename Elem<DT>::S* fq) {
     using E = Elem<DT>;
     __shared__ float lut_s[kLutSize];
@@ -190,7 +189,7 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(
         float f = valid ? E::to_f(x[gi]) : 0.0f;
         uint32_t ab = __float_as_uint(f) & 0x7fffffffu;
         uint32_t m = group_umax_shfl<BS>(ab);
-        float uu = STOCH ? dither_uniform(seed, offset + (uint64_t)gi) : 0.0f;
+        const float d = STOCH ? dither_step(key, offset + (uint64_t)gi) : 0.0f;
 
         // shared exponent
         int e = (m == 0u || m >= kInfBits) ? 0 : floor_log2_torch(m, band_s) + 1 + kExpBias;
@@ -200,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(
         if (se >= 128) n = ab >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;   // x / inf
         else n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -se);
         n = (n > 1.0f) ? 1.0f : n;                 // clamp(0, 1); NaN passes through
-        const int idx = lut_index(n, STOCH, uu);
+        const int idx = lut_index(n, STOCH, d);
         if (vb) {
             const int64_t o = blk * BS + j;
             codes[o] = rev_s[idx];
@@ -209,7 +208,7 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(
         }
         if (fq) {
             FqScale s = fq_scale(m, band_s);
-            float v = fq_value(f, s, lut_s, STOCH, uu);
+            float v = fq_value(f, s, lut_s, STOCH, d);
             if (valid) fq[gi] = E::from_f(v);
         }
     }
@@ -281,16 +280,16 @@ void launch_fq_typed(const void* x, void* y, int64_t rows, int64_t cols, bool st
         const int64_t n_vec = rows * cols / V;
         const dim3 grid((unsigned)capped_grid(n_vec, (int64_t)kThreads * kUnroll));
         if (stochastic)
-            fq_vec_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, seed, offset);
+            fq_vec_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, dither_key(seed), offset);
         else
-            fq_vec_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, seed, offset);
+            fq_vec_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, dither_key(seed), offset);
     } else {
         const int64_t nblk = (cols + BS - 1) / BS;
         const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));
         if (stochastic)
-            fq_scalar_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, seed, offset);
+            fq_scalar_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, dither_key(seed), offset);
         else
-            fq_scalar_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, seed, offset);
+            fq_scalar_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, dither_key(seed), offset);
     }
 }
 
@@ -310,9 +309,9 @@ void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochast
     const int64_t nblk = (cols + BS - 1) / BS;
     const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));
     if (stochastic)
-        quantize_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, seed, offset, exps, codes, signs, (S*)fq);
+        quantize_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, dither_key(seed), offset, exps, codes, signs, (S*)fq);
     else
-        quantize_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, seed, offset, exps, codes, signs, (S*)fq);
+        quantize_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, dither_key(seed), offset, exps, codes, signs, (S*)fq);
 }
 
 template <int DT>

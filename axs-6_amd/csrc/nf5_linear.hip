@@ -9,13 +9,18 @@
 // Xq16/sx/Wq16/sw are caller-owned and reused by the backward.
 //
 // Backward (dYq = stochastic FQ(dY) when quantize_grad, else dY):
-//   dX = dYq FQ(W):   pack_rows(dY, colx = sw) -> A1 [M, Np] (row shift t[m]),
-//                     transpose Wq16 -> [Kp, Np], GEMM, epilogue 2^t[m];
-//   dW = dYq^T FQ(X): pack_global(dY, rowx = sx) -> A2 [M, Np] with one
-//                     tensor-wide shift G (max over rows of the row maxima,
-//                     gathered by the first pack), transposes A2 -> [N, Mp]
-//                     and Xq16 -> [Kp, Mp], GEMM, epilogue 2^G;
-//   db = column sums of dYq, in a fixed order (partials + reduce).
+//   row_stats(dY):    the row shifts t[m] of the dX operand (with the weight's
+//                     row exponents sw folded in per column) and the
+//                     tensor-wide shift G of the dW operand (max over rows of
+//                     the row maxima + sx[m]) -- block exponents only, no FQ
+//                     values, streamed over tiles with per-row atomicMax;
+//   pack_t(dY):       one pass over 64x64 tiles computes dYq once and writes
+//                     A1 [M, Np] = dYq * 2^(sw[n] - t[m]) (row-major, for dX),
+//                     A2T [N, Mp] = (dYq * 2^(sx[m] - G))^T (for dW, transposed
+//                     through LDS) and the fixed-order column partials for db;
+//   dX = dYq FQ(W):   transpose Wq16 -> [Kp, Np], GEMM(A1, WqT), epilogue 2^t[m];
+//   dW = dYq^T FQ(X): transpose Xq16 -> [Kp, Mp], GEMM(A2T, XqT), epilogue 2^G;
+//   db = reduce of the partials (fixed order).
 #include <string.h>
 
 #include "linear_internal.h"
@@ -27,7 +32,7 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct BwdLayout {
-    size_t gmax, t, a1, wqt, a2, a2t, xqt, partial, total;
+    size_t gmax, t, stats, a1, wqt, a2t, xqt, partial, total;
 };
 
 BwdLayout bwd_layout(int64_t M, int64_t N, int64_t K, bool dx, bool dw, bool db) {
@@ -37,9 +42,9 @@ BwdLayout bwd_layout(int64_t M, int64_t N, int64_t K, bool dx, bool dw, bool db)
     auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
     L.gmax = take(sizeof(int32_t));
     L.t = take(sizeof(int32_t) * (size_t)M);
+    L.stats = take(2 * sizeof(int32_t) * (size_t)M);
     L.a1 = dx ? take(2 * (size_t)M * Np) : 0;
     L.wqt = dx ? take(2 * (size_t)Kp * Np) : 0;
-    L.a2 = dw ? take(2 * (size_t)M * Np) : 0;
     L.a2t = dw ? take(2 * (size_t)N * Mp) : 0;
     L.xqt = dw ? take(2 * (size_t)Kp * Mp) : 0;
     L.partial = db ? take(sizeof(float) * (size_t)pack_global_chunks(M) * N) : 0;
@@ -153,12 +158,17 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
     int32_t* tshift = (int32_t*)(ws + L.t);
     const bool fq = quantize_grad != 0;
 
-    if (need_dw && (rc = launch_init_gmax(gmax, st))) return rc;
     if (need_dx || need_dw) {
-        PackRowsArgs p{dy, dtype, M, N, block_size, fq, fq, seed, offset, need_dx ? w_shift : nullptr,
-                       need_dx ? (_Float16*)(ws + L.a1) : nullptr, Np, Np, tshift, nullptr,
-                       need_dw ? x_shift : nullptr, need_dw ? gmax : nullptr};
-        if ((rc = launch_pack_rows(p, t, st))) return rc;
+        RowStatsArgs s{dy, dtype, M, N, block_size, need_dx ? w_shift : nullptr, tshift,
+                       need_dw ? x_shift : nullptr, need_dw ? gmax : nullptr, (int32_t*)(ws + L.stats)};
+        if ((rc = launch_row_stats(s, t, st))) return rc;
+    }
+    if (need_dx || need_dw || need_db) {
+        PackTArgs p{dy, dtype, M, N, block_size, fq, fq, seed, offset, x_shift, need_dw ? gmax : nullptr,
+                    need_dw ? (_Float16*)(ws + L.a2t) : nullptr, Mp,
+                    need_dx ? (_Float16*)(ws + L.a1) : nullptr, Np, w_shift, tshift,
+                    need_db ? (float*)(ws + L.partial) : nullptr};
+        if ((rc = launch_pack_t(p, t, st))) return rc;
     }
     if (need_dx) {
         _Float16* wqt = (_Float16*)(ws + L.wqt);
@@ -167,17 +177,9 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
                    dx, K, dtype};
         if ((rc = launch_gemm_f16(g, st))) return rc;
     }
-    if (need_dw || need_db) {
-        if (!need_dw && (rc = launch_init_gmax(gmax, st))) return rc;
-        PackGlobalArgs p{dy, dtype, M, N, block_size, fq, fq, seed, offset, x_shift, gmax,
-                         need_dw ? (_Float16*)(ws + L.a2) : nullptr, Np, Np,
-                         need_db ? (float*)(ws + L.partial) : nullptr, 0};
-        if ((rc = launch_pack_global(p, t, st))) return rc;
-    }
     if (need_dw) {
         _Float16* a2t = (_Float16*)(ws + L.a2t);
         _Float16* xqt = (_Float16*)(ws + L.xqt);
-        if ((rc = launch_transpose_f16((const _Float16*)(ws + L.a2), M, Np, Np, a2t, N, Mp, Mp, st))) return rc;
         if ((rc = launch_transpose_f16((const _Float16*)xq_f16, M, Kp, Kp, xqt, Kp, Mp, Mp, st))) return rc;
         GemmArgs g{a2t, Mp, xqt, Mp, N, K, Mp, nullptr, nullptr, gmax, -15, nullptr, dw, K, AXS6_F32};
         if ((rc = launch_gemm_f16(g, st))) return rc;

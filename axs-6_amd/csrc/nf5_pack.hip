@@ -14,8 +14,9 @@
 //                       FQ + row scale in a single HBM pass (forward X, W;
 //                       backward dY for dX with the weight's row exponents
 //                       folded in per column).
-//   pack_global_kernel  column strips, one tensor-wide scale (read from a
-//                       device scalar): backward dY for dW, plus fixed-order
+//   pack_t_kernel       64 x 64 tiles, one tensor-wide scale (read from a
+//                       device scalar), written transposed: backward dY ->
+//                       the dW operand [N, Mp] directly, plus fixed-order
 //                       column partial sums for the bias gradient.
 //   transpose_f16_kernel / reduce_partials_kernel / init_gmax_kernel.
 #include <limits.h>
@@ -86,7 +87,7 @@ __device__ __forceinline__ void store_f16(_Float16* p, const float* v, int sh_ba
 
 struct PackRowsK {
     const void* x; int64_t rows; int64_t cols; int block;
-    uint64_t seed; uint64_t offset;
+    uint64_t key; uint64_t offset;      // dither key (dither_key of the call's seed)
     const int32_t* colx;
     _Float16* out; int64_t ld_out; int64_t cols_pad;
     int32_t* s_out; int32_t* rmax_out;
@@ -94,216 +95,502 @@ struct PackRowsK {
     const float* lut; const uint8_t* band;
 };
 
-template <int DT, int MODE, bool COLX, int NV>
-__global__ __launch_bounds__(kPackThreads) void pack_rows_kernel(PackRowsK k, PackRowsK k2) {
+// Row pack, persistent: workgroup w handles rows w, w + gridDim.x, ... of the
+// concatenation of k's rows and k2's (two operands in one launch; k2 == k and
+// total == k.rows for one).  NT threads hold a row in registers, NV 16-byte
+// vectors each (NT grows with the row length so that NV <= 4 and occupancy
+// stays high); the LUT and band table are staged once per workgroup.
+template <int DT, int MODE, bool COLX, int NV, int NT>
+__global__ __launch_bounds__(NT) void pack_rows_kernel(PackRowsK k, PackRowsK k2, int64_t total) {
     using E = Elem<DT>;
     using S = typename E::S;
     constexpr int V = E::V;
+    constexpr int NW = NT / 64;
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
-    __shared__ int red[2][kPackThreads / 64];
+    __shared__ int red[2][2][NW];         // [row parity][tmax, rmax][wave]
     const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
-
-    // two operands may share one launch: workgroups past k.rows take k2
-    const bool second = blockIdx.x >= k.rows;
-    const PackRowsK q = second ? k2 : k;      // by value: field-wise selects, no stack copy
     const int tid = threadIdx.x;
-    const int64_t r = second ? blockIdx.x - k.rows : blockIdx.x;
-    const int64_t nvec = q.cols / V;
-    const int g = q.block / V;
-    const S* xr = reinterpret_cast<const S*>(q.x) + r * q.cols;
+    stage_tables(lut_s, band_w, k.lut, k.band);
 
-    // the row's HBM loads go out before the LUT is staged
-    float f[NV][V];
-    int eb[NV];
-    u32x4 raw[NV];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int64_t vi = tid + (int64_t)kPackThreads * j;
-        raw[j] = vi < nvec ? *(reinterpret_cast<const u32x4*>(xr) + vi) : u32x4{0u, 0u, 0u, 0u};
-    }
-    stage_tables(lut_s, band_w, q.lut, q.band);
-    int tmax = INT_MIN, rmax = INT_MIN;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int64_t vi = tid + (int64_t)kPackThreads * j;
-        E::unpack(raw[j], f[j]);
-        uint32_t m = 0;
-#pragma unroll
-        for (int e = 0; e < V; ++e) {
-            uint32_t a = __float_as_uint(f[j][e]) & 0x7fffffffu;
-            m = m > a ? m : a;
-        }
-        m = group_umax_rt(m, g);
-        const FqScale s = fq_scale(m, band_s);
-        if constexpr (MODE != kRaw) {
-#pragma unroll
-            for (int e = 0; e < V; ++e) {
-                const float u = (MODE == kStochastic)
-                    ? dither_uniform(q.seed, q.offset + (uint64_t)(r * q.cols + vi * V + e)) : 0.0f;
-                f[j][e] = fq_value(f[j][e], s, lut_s, MODE == kStochastic, u);
-            }
-        }
-        const bool finite_block = !(s.nan_block || s.inf_scale || m == 0u);
-        eb[j] = (vi < nvec && finite_block) ? s.e1 : INT_MIN;
-        rmax = eb[j] > rmax ? eb[j] : rmax;
-        if constexpr (COLX) {
-            if (eb[j] != INT_MIN) {
-#pragma unroll
-                for (int e = 0; e < V; ++e) {
-                    const int b = eb[j] + q.colx[vi * V + e];
-                    tmax = b > tmax ? b : tmax;
-                }
-            }
-        }
-    }
-    if constexpr (!COLX) tmax = rmax;
+    int parity = 0;
+    for (int64_t R = blockIdx.x; R < total; R += gridDim.x, parity ^= 1) {
+        const bool second = R >= k.rows;
+        const PackRowsK q = second ? k2 : k;      // by value: field-wise selects, no stack copy
+        const int64_t r = second ? R - k.rows : R;
+        const int64_t nvec = q.cols / V;
+        const int g = q.block / V;
+        const S* xr = reinterpret_cast<const S*>(q.x) + r * q.cols;
 
-    // workgroup max of (tmax, rmax)
-    tmax = wave_max_i32(tmax);
-    rmax = wave_max_i32(rmax);
-    if ((tid & 63) == 0) { red[0][tid >> 6] = tmax; red[1][tid >> 6] = rmax; }
-    __syncthreads();
-    tmax = red[0][0]; rmax = red[1][0];
-#pragma unroll
-    for (int w = 1; w < kPackThreads / 64; ++w) {
-        tmax = red[0][w] > tmax ? red[0][w] : tmax;
-        rmax = red[1][w] > rmax ? red[1][w] : rmax;
-    }
-    const int S_row = (tmax == INT_MIN) ? 0 : tmax - kF16MaxExp;
-
-    if (q.out) {
-        _Float16* orow = q.out + r * q.ld_out;
+        float f[NV][V];
+        int cx[NV][V];
+        u32x4 raw[NV];
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const int64_t vi = tid + (int64_t)kPackThreads * j;
-            if (vi < nvec) {
-                int colx_v[V];
-                if constexpr (COLX) {
+            const int64_t vi = tid + (int64_t)NT * j;
+            raw[j] = vi < nvec ? *(reinterpret_cast<const u32x4*>(xr) + vi) : u32x4{0u, 0u, 0u, 0u};
+            if constexpr (COLX) {
+                // V consecutive column exponents: one or two 16-byte loads
 #pragma unroll
-                    for (int e = 0; e < V; ++e) colx_v[e] = q.colx[vi * V + e];
+                for (int h = 0; h < V / 4; ++h) {
+                    const u32x4 c4 = vi < nvec ? *(reinterpret_cast<const u32x4*>(q.colx + vi * V) + h)
+                                               : u32x4{0u, 0u, 0u, 0u};
+                    cx[j][4 * h] = (int)c4.x; cx[j][4 * h + 1] = (int)c4.y;
+                    cx[j][4 * h + 2] = (int)c4.z; cx[j][4 * h + 3] = (int)c4.w;
                 }
-                store_f16<V>(orow + vi * V, f[j], -S_row, COLX ? colx_v : nullptr);
             }
         }
-        const int64_t zvec = (q.cols_pad - q.cols) / 8;   // 8-half zero chunks
-        for (int64_t z = tid; z < zvec; z += kPackThreads)
-            *reinterpret_cast<u32x4*>(orow + q.cols + z * 8) = u32x4{0u, 0u, 0u, 0u};
-    }
-    if (tid == 0) {
-        q.s_out[r] = S_row;
-        if (q.rmax_out) q.rmax_out[r] = rmax;
-        if (q.gmax && rmax != INT_MIN) atomicMax(q.gmax, rmax + (q.rowx ? q.rowx[r] : 0));
+        int tmax = INT_MIN, rmax = INT_MIN;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int64_t vi = tid + (int64_t)NT * j;
+            E::unpack(raw[j], f[j]);
+            uint32_t m = 0;
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                uint32_t a = __float_as_uint(f[j][e]) & 0x7fffffffu;
+                m = m > a ? m : a;
+            }
+            m = group_umax_rt(m, g);
+            const FqScale s = fq_scale(m, band_s);
+            if constexpr (MODE != kRaw) {
+                const DitherVec dv = dither_vec(q.key, q.offset + (uint64_t)(r * q.cols + vi * V));
+                float d[V];
+#pragma unroll
+                for (int e = 0; e < V; ++e) d[e] = (MODE == kStochastic) ? dither_step(dv, e) : 0.0f;
+                fq_vector<V>(f[j], s, lut_s, MODE == kStochastic, d);
+            }
+            const bool finite_block = !(s.nan_block || s.inf_scale || m == 0u);
+            const int eb = (vi < nvec && finite_block) ? s.e1 : INT_MIN;
+            rmax = eb > rmax ? eb : rmax;
+            if constexpr (COLX) {
+                if (eb != INT_MIN) {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) {
+                        const int b = eb + cx[j][e];
+                        tmax = b > tmax ? b : tmax;
+                    }
+                }
+            }
+        }
+        if constexpr (!COLX) tmax = rmax;
+
+        // workgroup max of (tmax, rmax); the parity buffer lets the next row's
+        // writes proceed while slower waves still read this row's values
+        tmax = wave_max_i32(tmax);
+        rmax = wave_max_i32(rmax);
+        if ((tid & 63) == 0) { red[parity][0][tid >> 6] = tmax; red[parity][1][tid >> 6] = rmax; }
+        __syncthreads();
+        tmax = red[parity][0][0]; rmax = red[parity][1][0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            tmax = red[parity][0][w] > tmax ? red[parity][0][w] : tmax;
+            rmax = red[parity][1][w] > rmax ? red[parity][1][w] : rmax;
+        }
+        const int S_row = (tmax == INT_MIN) ? 0 : tmax - kF16MaxExp;
+
+        if (q.out) {
+            _Float16* orow = q.out + r * q.ld_out;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int64_t vi = tid + (int64_t)NT * j;
+                if (vi < nvec) store_f16<V>(orow + vi * V, f[j], -S_row, COLX ? cx[j] : nullptr);
+            }
+            const int64_t zvec = (q.cols_pad - q.cols) / 8;   // 8-half zero chunks
+            for (int64_t z = tid; z < zvec; z += NT)
+                *reinterpret_cast<u32x4*>(orow + q.cols + z * 8) = u32x4{0u, 0u, 0u, 0u};
+        }
+        if (tid == 0) {
+            q.s_out[r] = S_row;
+            if (q.rmax_out) q.rmax_out[r] = rmax;
+            if (q.gmax && rmax != INT_MIN) atomicMax(q.gmax, rmax + (q.rowx ? q.rowx[r] : 0));
+        }
     }
 }
 
-struct PackGlobalK {
+// Transposed global pack: one workgroup per 64 x 64 tile of x (rows r, columns
+// c).  Loads are 16-byte vectors along the rows, so an NF5 block is G = block/V
+// neighbouring lanes and its amax is a DPP reduction; the value of element
+// (r, c) is FQ(x)[r, c] with the same dither counter as the row pack, scaled
+// by 2^(rowx[r] - G) (G = *gmax - 15) and written transposed through LDS:
+// out[c, r] (ld_out halves per row, r up to the tile end: zeros past rows).
+// With `partial`, the tile's column sums of FQ(x) go to partial[tile_row, c],
+// summed in a fixed order (each thread over its rows in order, then the
+// row groups in order), so the bias gradient is deterministic.
+struct PackTK {
     const void* x; int64_t rows; int64_t cols; int block;
-    uint64_t seed; uint64_t offset;
+    uint64_t key; uint64_t offset;
     const int32_t* rowx; const int32_t* gmax;
-    _Float16* out; int64_t ld_out; int64_t cols_pad;
-    float* partial; int rows_per_chunk;
+    _Float16* out; int64_t ld_out;
+    _Float16* out_r; int64_t ld_r; const int32_t* colx_r; const int32_t* shift_r;
+    float* partial;
     const float* lut; const uint8_t* band;
 };
 
-template <int DT, int MODE>
-__global__ __launch_bounds__(kPackThreads) void pack_global_kernel(PackGlobalK k) {
+constexpr int kTile = 64;          // rows and columns of a transpose tile
+constexpr int kTileLd = kTile + 8; // LDS row stride (halves) of the transposed tile
+
+template <int DT, int MODE, int BS>
+__global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t ntx, int64_t ntiles) {
     using E = Elem<DT>;
     using S = typename E::S;
+    constexpr int V = E::V;
+    constexpr int GL = BS / V > 0 ? BS / V : 1;     // lanes per NF5 block
+    constexpr int TPR = kTile / V;                  // threads per tile row
+    constexpr int RPP = kPackThreads / TPR;         // tile rows per pass
+    constexpr int PASSES = kTile / RPP;
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
-    stage_tables(lut_s, band_w, k.lut, k.band);
+    __shared__ uint16_t tile[kTile * kTileLd];      // transposed: tile[c * kTileLd + r]
+    __shared__ float csum[RPP][kTile + 1];
     const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
 
-    const int64_t c = (int64_t)blockIdx.x * kPackThreads + threadIdx.x;
-    const bool vc = c < k.cols;
-    const int64_t r0 = (int64_t)blockIdx.y * k.rows_per_chunk;
-    const int64_t r1 = r0 + k.rows_per_chunk < k.rows ? r0 + k.rows_per_chunk : k.rows;
-    const int gm = *k.gmax;
-    const int G = (gm == INT_MIN) ? 0 : gm - kF16MaxExp;
+    const int tid = threadIdx.x;
+    const int tc = tid % TPR, tr = tid / TPR;
     const S* xs = reinterpret_cast<const S*>(k.x);
-    float colsum = 0.0f;
-#pragma unroll 4
-    for (int64_t r = r0; r < r1; ++r) {
-        const int64_t gi = r * k.cols + c;
-        float f = vc ? E::to_f(xs[gi]) : 0.0f;
-        const uint32_t m = group_umax_shfl_rt(__float_as_uint(f) & 0x7fffffffu, k.block);
-        if constexpr (MODE != kRaw) {
-            const FqScale s = fq_scale(m, band_s);
-            const float u = (MODE == kStochastic) ? dither_uniform(k.seed, k.offset + (uint64_t)gi) : 0.0f;
-            f = fq_value(f, s, lut_s, MODE == kStochastic, u);
+    stage_tables(lut_s, band_w, k.lut, k.band);
+    const int gm = k.gmax ? *k.gmax : INT_MIN;
+    const int G = (gm == INT_MIN) ? 0 : gm - kF16MaxExp;
+
+    // persistent over tiles; consecutive workgroups take neighbouring column
+    // tiles of one 64-row band, so a band of x streams through once
+    for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+        const int64_t ty = t / ntx, tx = t - ty * ntx;
+        const int64_t c0 = tx * kTile, r0 = ty * kTile;
+        const int64_t c = c0 + tc * V;
+        const bool cin = c < k.cols;                // cols % block == 0: vectors are whole
+
+        u32x4 raw[PASSES];
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int64_t r = r0 + tr + RPP * p;
+            raw[p] = (cin && r < k.rows) ? *reinterpret_cast<const u32x4*>(xs + r * k.cols + c)
+                                         : u32x4{0u, 0u, 0u, 0u};
         }
-        if (k.out && c < k.cols_pad) {
-            const int sh = (k.rowx ? k.rowx[r] : 0) - G;
-            k.out[r * k.ld_out + c] = vc ? (_Float16)__builtin_amdgcn_ldexpf(f, sh) : (_Float16)0.0f;
+        float colsum[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) colsum[e] = 0.0f;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int lr = tr + RPP * p;
+            const int64_t r = r0 + lr;
+            float f[V];
+            E::unpack(raw[p], f);
+            uint32_t m = 0;
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const uint32_t a = __float_as_uint(f[e]) & 0x7fffffffu;
+                m = m > a ? m : a;
+            }
+            m = group_umax<GL>(m);
+            if constexpr (MODE != kRaw) {
+                const FqScale s = fq_scale(m, band_s);
+                const DitherVec dv = dither_vec(k.key, k.offset + (uint64_t)(r * k.cols + c));
+                float d[V];
+#pragma unroll
+                for (int e = 0; e < V; ++e) d[e] = (MODE == kStochastic) ? dither_step(dv, e) : 0.0f;
+                fq_vector<V>(f, s, lut_s, MODE == kStochastic, d);
+            }
+            const bool live = cin && r < k.rows;
+            if (k.partial) {
+#pragma unroll
+                for (int e = 0; e < V; ++e) colsum[e] += live ? f[e] : 0.0f;
+            }
+            if (k.out_r && r < k.rows) {
+                // row-major operand: fp16(v * 2^(colx[c] - shift[r])), zeros in the
+                // padding columns cols <= c < 64 * ceil(cols / 64)
+                int cx[V];
+#pragma unroll
+                for (int h = 0; h < V / 4; ++h) {
+                    const u32x4 c4 = (cin && k.colx_r) ? *(reinterpret_cast<const u32x4*>(k.colx_r + c) + h)
+                                                       : u32x4{0u, 0u, 0u, 0u};
+                    cx[4 * h] = (int)c4.x; cx[4 * h + 1] = (int)c4.y; cx[4 * h + 2] = (int)c4.z; cx[4 * h + 3] = (int)c4.w;
+                }
+                float z[V];
+#pragma unroll
+                for (int e = 0; e < V; ++e) z[e] = cin ? f[e] : 0.0f;
+                store_f16<V>(k.out_r + r * k.ld_r + c, z, -k.shift_r[r], cx);
+            }
+            if (k.out) {
+                const int sh = (live && k.rowx) ? k.rowx[r] - G : -G;
+#pragma unroll
+                for (int e = 0; e < V; ++e) {
+                    const _Float16 h = live ? (_Float16)__builtin_amdgcn_ldexpf(f[e], sh) : (_Float16)0.0f;
+                    tile[(tc * V + e) * kTileLd + lr] = __builtin_bit_cast(uint16_t, h);
+                }
+            }
         }
-        colsum += f;
+        if (k.partial) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) csum[tr][tc * V + e] = colsum[e];
+        }
+        __syncthreads();
+        if (k.partial && tid < kTile && c0 + tid < k.cols) {
+            float s = 0.0f;
+            for (int q = 0; q < RPP; ++q) s += csum[q][tid];
+            k.partial[ty * k.cols + c0 + tid] = s;
+        }
+        if (k.out) {
+            // 64 output rows (columns c of x) of 64 halves = 8 chunks of 16 bytes each
+#pragma unroll
+            for (int q = tid; q < kTile * 8; q += kPackThreads) {
+                const int oc = q >> 3, j = q & 7;
+                if (c0 + oc < k.cols)
+                    *reinterpret_cast<u32x4*>(k.out + (c0 + oc) * k.ld_out + r0 + j * 8) =
+                        *reinterpret_cast<const u32x4*>(&tile[oc * kTileLd + j * 8]);
+            }
+        }
+        __syncthreads();   // tile and csum are rewritten by the next iteration
     }
-    if (k.partial && vc) k.partial[(int64_t)blockIdx.y * k.cols + c] = colsum;
 }
 
+// Row statistics of x for the packing shifts (block exponents only, no FQ
+// values), streamed over tiles of 64 rows x 256 columns.  For the blocks with
+// a finite nonzero scale 2^e1 (every FQ value of the block is at most 2^e1 in
+// magnitude) each workgroup folds into
+//   tmax[r] = max over blocks of (e1 + max colx over the block's columns)
+//   rmax[r] = max over blocks of e1
+// with atomicMax (both start at INT_MIN); stats_finalize_kernel then writes
+//   shift[r] = tmax[r] - 15 (0 if INT_MIN) and atomicMax(gmax, rmax[r] + rowx[r]).
+// These are the quantities pack_rows derives for a whole row in one workgroup;
+// a row-per-workgroup pass over long rows is latency-bound, this one streams.
+struct StatsK {
+    const void* x; int64_t rows; int64_t cols;
+    const int32_t* colx; int32_t* tmax; int32_t* rmax;
+    const uint8_t* band;
+};
+
+constexpr int kStatsCols = 256;   // columns of a statistics tile
+
+template <int DT, int BS>
+__global__ __launch_bounds__(256) void stats_tile_kernel(StatsK k, int64_t ntx) {
+    using E = Elem<DT>;
+    using S = typename E::S;
+    constexpr int V = E::V;
+    constexpr int G = BS / V > 0 ? BS / V : 1;
+    constexpr int TPR = kTile / V;                  // threads per 64-column chunk of a row
+    constexpr int RPP = 256 / TPR;                  // rows per pass
+    constexpr int PASSES = kTile / RPP;
+    constexpr int CH = kStatsCols / kTile;          // 64-column chunks per tile
+    __shared__ uint32_t band_w[kBandSize / 4];
+    const int tid = threadIdx.x;
+    if (tid < kBandSize / 4) band_w[tid] = reinterpret_cast<const uint32_t*>(k.band)[tid];
+    const int tc = tid % TPR, tr = tid / TPR;
+    const int64_t ty = blockIdx.x / ntx, tx = blockIdx.x - ty * ntx;
+    const int64_t r0 = ty * kTile, c0 = tx * kStatsCols;
+    const S* xs = reinterpret_cast<const S*>(k.x);
+
+    u32x4 raw[PASSES][CH];
+    int cm[CH];
+#pragma unroll
+    for (int h = 0; h < CH; ++h) {
+        const int64_t c = c0 + h * kTile + tc * V;
+        const bool cin = c < k.cols;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int64_t r = r0 + tr + RPP * p;
+            raw[p][h] = (cin && r < k.rows) ? *reinterpret_cast<const u32x4*>(xs + r * k.cols + c)
+                                            : u32x4{0u, 0u, 0u, 0u};
+        }
+        int m = INT_MIN;
+        if (cin && k.colx) {
+#pragma unroll
+            for (int q = 0; q < V / 4; ++q) {
+                const u32x4 c4 = *(reinterpret_cast<const u32x4*>(k.colx + c) + q);
+                const int a = (int)c4.x > (int)c4.y ? (int)c4.x : (int)c4.y;
+                const int b = (int)c4.z > (int)c4.w ? (int)c4.z : (int)c4.w;
+                const int ab = a > b ? a : b;
+                m = ab > m ? ab : m;
+            }
+        } else if (cin) {
+            m = 0;
+        }
+        cm[h] = m;
+    }
+    __syncthreads();
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int64_t r = r0 + tr + RPP * p;
+        int tm = INT_MIN, rm = INT_MIN;
+#pragma unroll
+        for (int h = 0; h < CH; ++h) {
+            float f[V];
+            E::unpack(raw[p][h], f);
+            uint32_t a = 0;
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const uint32_t b = __float_as_uint(f[e]) & 0x7fffffffu;
+                a = a > b ? a : b;
+            }
+            a = group_umax<G>(a);
+            const FqScale s = fq_scale(a, band_s);
+            if (!(s.nan_block || s.inf_scale || a == 0u) && cm[h] != INT_MIN) {
+                rm = s.e1 > rm ? s.e1 : rm;
+                const int t = s.e1 + cm[h];
+                tm = t > tm ? t : tm;
+            }
+        }
+        // max over the TPR lanes of this row (consecutive lanes)
+#pragma unroll
+        for (int off = 1; off < TPR; off <<= 1) {
+            const int o1 = __shfl_xor(tm, off, 64), o2 = __shfl_xor(rm, off, 64);
+            tm = o1 > tm ? o1 : tm;
+            rm = o2 > rm ? o2 : rm;
+        }
+        if (tc == 0 && r < k.rows && rm != INT_MIN) {
+            atomicMax(k.tmax + r, tm);
+            atomicMax(k.rmax + r, rm);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void stats_init_kernel(int32_t* a, int64_t n, int32_t* gmax) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) a[i] = INT_MIN;
+    if (i == 0 && gmax) *gmax = INT_MIN;
+}
+
+__global__ __launch_bounds__(256) void stats_finalize_kernel(const int32_t* __restrict__ tmax,
+                                                             const int32_t* __restrict__ rmax, int64_t rows,
+                                                             int32_t* shift, const int32_t* rowx, int32_t* gmax) {
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    int g = INT_MIN;
+    if (r < rows) {
+        const int t = tmax[r];
+        if (shift) shift[r] = t == INT_MIN ? 0 : t - kF16MaxExp;
+        const int rm = rmax[r];
+        if (rm != INT_MIN) g = rm + (rowx ? rowx[r] : 0);
+    }
+    if (gmax) {
+        g = wave_max_i32(g);
+        if ((threadIdx.x & 63) == 0 && g != INT_MIN) atomicMax(gmax, g);
+    }
+}
+
+// out[c] = sum over chunks k of partial[k, c], in the order k = 0, 1, ...
+// split into 4 consecutive ranges combined in order: deterministic.
 __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ partial, int64_t chunks,
                                                               int64_t cols, float* __restrict__ out) {
-    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (c >= cols) return;
+    __shared__ float part[4][64];
+    const int lc = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int64_t c = (int64_t)blockIdx.x * 64 + lc;
+    const int64_t per = (chunks + 3) / 4;
+    const int64_t k0 = q * per, k1 = (k0 + per) < chunks ? k0 + per : chunks;
     float s = 0.0f;
-    for (int64_t k = 0; k < chunks; ++k) s += partial[k * cols + c];
-    out[c] = s;
+    if (c < cols)
+        for (int64_t kk = k0; kk < k1; ++kk) s += partial[kk * cols + c];
+    part[q][lc] = s;
+    __syncthreads();
+    if (q == 0 && c < cols) out[c] = ((part[0][lc] + part[1][lc]) + part[2][lc]) + part[3][lc];
 }
 
+// out[c, r] = in[r, c] for r < rows, c < out_rows; zero for rows <= r < rows_pad.
+// 64 x 64 tiles; 16-byte loads along input rows, 16-byte stores along output
+// rows, the transpose done through LDS with 2-byte accesses.
 __global__ __launch_bounds__(256) void transpose_f16_kernel(const uint16_t* __restrict__ in, int64_t rows,
                                                             int64_t cols, int64_t ld_in, uint16_t* __restrict__ out,
                                                             int64_t out_rows, int64_t rows_pad, int64_t ld_out) {
-    __shared__ uint16_t tile[64][66];
-    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    const int64_t c0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 64;
+    __shared__ uint16_t tile[kTile * kTileLd];   // tile[c * kTileLd + r]
+    const int tid = threadIdx.x;
+    const int64_t c0 = (int64_t)blockIdx.x * kTile, r0 = (int64_t)blockIdx.y * kTile;
+    const bool vec_in = (ld_in % 8 == 0) && ((uintptr_t)in % 16 == 0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int64_t r = r0 + ty + 4 * i, c = c0 + tx;
-        tile[ty + 4 * i][tx] = (r < rows && c < cols) ? in[r * ld_in + c] : (uint16_t)0;
+    for (int q = tid; q < kTile * 8; q += 256) {
+        const int lr = q >> 3, j = q & 7;
+        const int64_t r = r0 + lr, cb = c0 + j * 8;
+        uint16_t h[8];
+        if (r < rows && vec_in && cb + 8 <= cols) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(in + r * ld_in + cb);
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { h[2 * e] = (uint16_t)(ww[e] & 0xffffu); h[2 * e + 1] = (uint16_t)(ww[e] >> 16); }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = (r < rows && cb + e < cols) ? in[r * ld_in + cb + e] : (uint16_t)0;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tile[(j * 8 + e) * kTileLd + lr] = h[e];
     }
     __syncthreads();
+    const bool vec_out = (ld_out % 8 == 0) && ((uintptr_t)out % 16 == 0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int64_t oc = c0 + ty + 4 * i, orr = r0 + tx;
-        if (oc < out_rows && orr < rows_pad) out[oc * ld_out + orr] = tile[tx][ty + 4 * i];
+    for (int q = tid; q < kTile * 8; q += 256) {
+        const int oc = q >> 3, j = q & 7;
+        const int64_t orow = c0 + oc, ocol = r0 + j * 8;
+        if (orow >= out_rows) continue;
+        const uint16_t* src = &tile[oc * kTileLd + j * 8];
+        if (vec_out && ocol + 8 <= rows_pad) {
+            *reinterpret_cast<u32x4*>(out + orow * ld_out + ocol) = *reinterpret_cast<const u32x4*>(src);
+        } else {
+            for (int e = 0; e < 8; ++e)
+                if (ocol + e < rows_pad) out[orow * ld_out + ocol + e] = src[e];
+        }
     }
 }
 
 __global__ void init_gmax_kernel(int32_t* p) { *p = INT_MIN; }
 
+// Launch shape of the row pack for a row of nvec 16-byte vectors: NT threads,
+// NV vectors each.
+struct RowsShape { int nt; int nv; };
+inline RowsShape rows_shape(int64_t nvec) {
+    if (nvec <= 256) return {256, 1};
+    if (nvec <= 512) return {256, 2};
+    if (nvec <= 1024) return {256, 4};
+    if (nvec <= 2048) return {512, 4};
+    return {1024, 4};
+}
+constexpr int64_t kRowsMaxVec = 4096;   // 1024 threads x 4 vectors
+
 template <int DT, int MODE, bool COLX>
-void dispatch_rows_nv(const PackRowsK& k, const PackRowsK& k2, int64_t rows, int nv, hipStream_t st) {
+void dispatch_rows_nv(const PackRowsK& k, const PackRowsK& k2, int64_t rows, RowsShape sh, hipStream_t st) {
+    // one row per workgroup (the loop in the kernel runs once): independent
+    // workgroups overlap better than a persistent loop (measured)
     const dim3 grid((unsigned)rows);
-    switch (nv) {
-        case 1: pack_rows_kernel<DT, MODE, COLX, 1><<<grid, kPackThreads, 0, st>>>(k, k2); break;
-        case 2: pack_rows_kernel<DT, MODE, COLX, 2><<<grid, kPackThreads, 0, st>>>(k, k2); break;
-        case 4: pack_rows_kernel<DT, MODE, COLX, 4><<<grid, kPackThreads, 0, st>>>(k, k2); break;
-        case 8: pack_rows_kernel<DT, MODE, COLX, 8><<<grid, kPackThreads, 0, st>>>(k, k2); break;
-        default: pack_rows_kernel<DT, MODE, COLX, 16><<<grid, kPackThreads, 0, st>>>(k, k2); break;
+    if (sh.nt == 1024) {
+        pack_rows_kernel<DT, MODE, COLX, 4, 1024><<<grid, 1024, 0, st>>>(k, k2, rows);
+    } else if (sh.nt == 512) {
+        pack_rows_kernel<DT, MODE, COLX, 4, 512><<<grid, 512, 0, st>>>(k, k2, rows);
+    } else if (sh.nv == 1) {
+        pack_rows_kernel<DT, MODE, COLX, 1, 256><<<grid, 256, 0, st>>>(k, k2, rows);
+    } else if (sh.nv == 2) {
+        pack_rows_kernel<DT, MODE, COLX, 2, 256><<<grid, 256, 0, st>>>(k, k2, rows);
+    } else {
+        pack_rows_kernel<DT, MODE, COLX, 4, 256><<<grid, 256, 0, st>>>(k, k2, rows);
     }
 }
 
 template <int DT>
-void dispatch_rows(const PackRowsK& k, const PackRowsK& k2, int64_t rows, int mode, bool colx, int nv,
+void dispatch_rows(const PackRowsK& k, const PackRowsK& k2, int64_t rows, int mode, bool colx, RowsShape sh,
                    hipStream_t st) {
     if (mode == kRaw) {
-        if (colx) dispatch_rows_nv<DT, kRaw, true>(k, k2, rows, nv, st); else dispatch_rows_nv<DT, kRaw, false>(k, k2, rows, nv, st);
+        if (colx) dispatch_rows_nv<DT, kRaw, true>(k, k2, rows, sh, st); else dispatch_rows_nv<DT, kRaw, false>(k, k2, rows, sh, st);
     } else if (mode == kNearest) {
-        if (colx) dispatch_rows_nv<DT, kNearest, true>(k, k2, rows, nv, st); else dispatch_rows_nv<DT, kNearest, false>(k, k2, rows, nv, st);
+        if (colx) dispatch_rows_nv<DT, kNearest, true>(k, k2, rows, sh, st); else dispatch_rows_nv<DT, kNearest, false>(k, k2, rows, sh, st);
     } else {
-        if (colx) dispatch_rows_nv<DT, kStochastic, true>(k, k2, rows, nv, st); else dispatch_rows_nv<DT, kStochastic, false>(k, k2, rows, nv, st);
+        if (colx) dispatch_rows_nv<DT, kStochastic, true>(k, k2, rows, sh, st); else dispatch_rows_nv<DT, kStochastic, false>(k, k2, rows, sh, st);
     }
 }
 
-template <int DT>
-void dispatch_global(const PackGlobalK& k, int mode, dim3 grid, hipStream_t st) {
-    if (mode == kRaw) pack_global_kernel<DT, kRaw><<<grid, kPackThreads, 0, st>>>(k);
-    else if (mode == kNearest) pack_global_kernel<DT, kNearest><<<grid, kPackThreads, 0, st>>>(k);
-    else pack_global_kernel<DT, kStochastic><<<grid, kPackThreads, 0, st>>>(k);
+template <int DT, int BS>
+void dispatch_t_bs(const PackTK& k, int mode, int64_t ntx, int64_t ntiles, hipStream_t st) {
+    // one tile per workgroup: independent workgroups overlap their load,
+    // compute and store phases better than a persistent loop (measured)
+    const dim3 grid((unsigned)ntiles);
+    if (mode == kRaw) pack_t_kernel<DT, kRaw, BS><<<grid, kPackThreads, 0, st>>>(k, ntx, ntiles);
+    else if (mode == kNearest) pack_t_kernel<DT, kNearest, BS><<<grid, kPackThreads, 0, st>>>(k, ntx, ntiles);
+    else pack_t_kernel<DT, kStochastic, BS><<<grid, kPackThreads, 0, st>>>(k, ntx, ntiles);
 }
 
-constexpr int kGlobalRowsPerChunk = 64;
+template <int DT>
+void dispatch_t(const PackTK& k, int mode, int64_t ntx, int64_t ntiles, hipStream_t st) {
+    if (k.block == 8) dispatch_t_bs<DT, 8>(k, mode, ntx, ntiles, st);
+    else if (k.block == 16) dispatch_t_bs<DT, 16>(k, mode, ntx, ntiles, st);
+    else dispatch_t_bs<DT, 32>(k, mode, ntx, ntiles, st);
+}
+
+constexpr int kGlobalRowsPerChunk = kTile;
 
 }  // namespace
 
@@ -311,24 +598,25 @@ int64_t pack_global_chunks(int64_t rows) { return (rows + kGlobalRowsPerChunk - 
 
 namespace {
 
-int check_pack_rows(const PackRowsArgs& a, int* nv_out) {
+int check_pack_rows(const PackRowsArgs& a, RowsShape* sh_out) {
     const int V = a.dtype == AXS6_F32 ? 4 : 8;
     if (a.cols % a.block != 0)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: cols (%lld) must be a multiple of block_size", (long long)a.cols);
     if ((uintptr_t)a.x % 16 != 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: input not 16-byte aligned");
+    if (a.colx && (uintptr_t)a.colx % 16 != 0)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: column exponents not 16-byte aligned");
     if (a.out && (a.ld_out % 8 != 0 || (uintptr_t)a.out % 16 != 0 || a.cols_pad % 8 != 0 || a.cols_pad < a.cols))
         return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: output must be 16-byte aligned with padded width >= cols");
     const int64_t nvec = a.cols / V;
-    const int64_t per = (nvec + kPackThreads - 1) / kPackThreads;
-    if (per > 16)
-        return fail(AXS6_ERR_UNSUPPORTED, "pack_rows: rows of %lld elements exceed the register-resident limit (%d)",
-                    (long long)a.cols, 16 * kPackThreads * V);
-    *nv_out = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
+    if (nvec > kRowsMaxVec)
+        return fail(AXS6_ERR_UNSUPPORTED, "pack_rows: rows of %lld elements exceed the register-resident limit (%lld)",
+                    (long long)a.cols, (long long)(kRowsMaxVec * V));
+    *sh_out = rows_shape(nvec);
     return AXS6_OK;
 }
 
 PackRowsK to_kernel_args(const PackRowsArgs& a, const DeviceTables& t) {
-    return PackRowsK{a.x, a.rows, a.cols, a.block, a.seed, a.offset, a.colx, a.out, a.ld_out, a.cols_pad,
+    return PackRowsK{a.x, a.rows, a.cols, a.block, dither_key(a.seed), a.offset, a.colx, a.out, a.ld_out, a.cols_pad,
                      a.s_out, a.rmax_out, a.rowx, a.gmax, t.lut, t.band};
 }
 
@@ -337,24 +625,24 @@ int pack_mode(const PackRowsArgs& a) { return a.fake_quant ? (a.stochastic ? kSt
 }  // namespace
 
 int launch_pack_rows(const PackRowsArgs& a, const DeviceTables& t, hipStream_t st) {
-    int nv = 0;
-    int rc = check_pack_rows(a, &nv);
+    RowsShape sh{};
+    int rc = check_pack_rows(a, &sh);
     if (rc) return rc;
     if (a.rows == 0) return AXS6_OK;
     const PackRowsK k = to_kernel_args(a, t);
     const bool colx = a.colx != nullptr;
-    if (a.dtype == AXS6_F32) dispatch_rows<AXS6_F32>(k, k, a.rows, pack_mode(a), colx, nv, st);
-    else if (a.dtype == AXS6_BF16) dispatch_rows<AXS6_BF16>(k, k, a.rows, pack_mode(a), colx, nv, st);
-    else dispatch_rows<AXS6_F16>(k, k, a.rows, pack_mode(a), colx, nv, st);
+    if (a.dtype == AXS6_F32) dispatch_rows<AXS6_F32>(k, k, a.rows, pack_mode(a), colx, sh, st);
+    else if (a.dtype == AXS6_BF16) dispatch_rows<AXS6_BF16>(k, k, a.rows, pack_mode(a), colx, sh, st);
+    else dispatch_rows<AXS6_F16>(k, k, a.rows, pack_mode(a), colx, sh, st);
     return check_launch("pack_rows");
 }
 
 int launch_pack_rows2(const PackRowsArgs& a, const PackRowsArgs& b, const DeviceTables& t, hipStream_t st) {
-    int nva = 0, nvb = 0;
-    int rc = check_pack_rows(a, &nva);
+    RowsShape sa{}, sb{};
+    int rc = check_pack_rows(a, &sa);
     if (rc) return rc;
-    if ((rc = check_pack_rows(b, &nvb))) return rc;
-    const bool same = a.dtype == b.dtype && pack_mode(a) == pack_mode(b) && nva == nvb &&
+    if ((rc = check_pack_rows(b, &sb))) return rc;
+    const bool same = a.dtype == b.dtype && pack_mode(a) == pack_mode(b) && sa.nt == sb.nt && sa.nv == sb.nv &&
                       (a.colx != nullptr) == (b.colx != nullptr);
     if (!same || a.rows == 0 || b.rows == 0) {
         if ((rc = launch_pack_rows(a, t, st))) return rc;
@@ -363,30 +651,64 @@ int launch_pack_rows2(const PackRowsArgs& a, const PackRowsArgs& b, const Device
     const PackRowsK ka = to_kernel_args(a, t), kb = to_kernel_args(b, t);
     const bool colx = a.colx != nullptr;
     const int64_t rows = a.rows + b.rows;
-    if (a.dtype == AXS6_F32) dispatch_rows<AXS6_F32>(ka, kb, rows, pack_mode(a), colx, nva, st);
-    else if (a.dtype == AXS6_BF16) dispatch_rows<AXS6_BF16>(ka, kb, rows, pack_mode(a), colx, nva, st);
-    else dispatch_rows<AXS6_F16>(ka, kb, rows, pack_mode(a), colx, nva, st);
+    if (a.dtype == AXS6_F32) dispatch_rows<AXS6_F32>(ka, kb, rows, pack_mode(a), colx, sa, st);
+    else if (a.dtype == AXS6_BF16) dispatch_rows<AXS6_BF16>(ka, kb, rows, pack_mode(a), colx, sa, st);
+    else dispatch_rows<AXS6_F16>(ka, kb, rows, pack_mode(a), colx, sa, st);
     return check_launch("pack_rows");
 }
 
-int launch_pack_global(const PackGlobalArgs& a, const DeviceTables& t, hipStream_t st) {
+int launch_pack_t(const PackTArgs& a, const DeviceTables& t, hipStream_t st) {
     if (a.cols % a.block != 0)
-        return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_global: cols must be a multiple of block_size");
-    if (a.rows == 0) return AXS6_OK;
-    PackGlobalK k{a.x, a.rows, a.cols, a.block, a.seed, a.offset, a.rowx, a.gmax, a.out, a.ld_out,
-                  a.out ? a.cols_pad : a.cols, a.partial, kGlobalRowsPerChunk, t.lut, t.band};
-    const int64_t width = a.out ? a.cols_pad : a.cols;
-    const dim3 grid((unsigned)((width + kPackThreads - 1) / kPackThreads), (unsigned)pack_global_chunks(a.rows));
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_t: cols must be a multiple of block_size");
+    if ((uintptr_t)a.x % 16 != 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_t: input not 16-byte aligned");
+    if (a.out && (a.ld_out % 8 != 0 || (uintptr_t)a.out % 16 != 0 || a.ld_out < pad_to(a.rows, kTile)))
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_t: output rows must be 16-byte aligned and hold the padded rows");
+    if (a.rows == 0 || a.cols == 0) return AXS6_OK;
+    if (a.out_r && (a.ld_r % 8 != 0 || (uintptr_t)a.out_r % 16 != 0 || a.ld_r < pad_to(a.cols, kTile) ||
+                    !a.shift_r || (a.colx_r && (uintptr_t)a.colx_r % 16 != 0)))
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_t: row-major output must be 16-byte aligned and hold the padded columns");
+    PackTK k{a.x, a.rows, a.cols, a.block, dither_key(a.seed), a.offset, a.rowx, a.gmax, a.out, a.ld_out,
+             a.out_r, a.ld_r, a.colx_r, a.shift_r, a.partial, t.lut, t.band};
+    const int64_t ntx = (a.cols + kTile - 1) / kTile, ntiles = ntx * pack_global_chunks(a.rows);
     const int mode = a.fake_quant ? (a.stochastic ? kStochastic : kNearest) : kRaw;
-    if (a.dtype == AXS6_F32) dispatch_global<AXS6_F32>(k, mode, grid, st);
-    else if (a.dtype == AXS6_BF16) dispatch_global<AXS6_BF16>(k, mode, grid, st);
-    else dispatch_global<AXS6_F16>(k, mode, grid, st);
-    return check_launch("pack_global");
+    if (a.dtype == AXS6_F32) dispatch_t<AXS6_F32>(k, mode, ntx, ntiles, st);
+    else if (a.dtype == AXS6_BF16) dispatch_t<AXS6_BF16>(k, mode, ntx, ntiles, st);
+    else dispatch_t<AXS6_F16>(k, mode, ntx, ntiles, st);
+    return check_launch("pack_t");
+}
+
+int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t st) {
+    if (a.cols % a.block != 0)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "row_stats: cols must be a multiple of block_size");
+    if ((uintptr_t)a.x % 16 != 0 || (a.colx && (uintptr_t)a.colx % 16 != 0))
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "row_stats: input and column exponents must be 16-byte aligned");
+    if (a.rows == 0) return AXS6_OK;
+    const int64_t n = 2 * a.rows;
+    stats_init_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, st>>>(a.scratch, n, a.gmax);
+    int rc = check_launch("row_stats");
+    if (rc) return rc;
+    StatsK k{a.x, a.rows, a.cols, a.colx, a.scratch, a.scratch + a.rows, t.band};
+    const int64_t ntx = (a.cols + kStatsCols - 1) / kStatsCols, nty = (a.rows + kTile - 1) / kTile;
+    const dim3 grid((unsigned)(ntx * nty));
+#define AXS6_STATS(DT_)                                                                              \
+    do {                                                                                             \
+        if (a.block == 8) stats_tile_kernel<DT_, 8><<<grid, 256, 0, st>>>(k, ntx);                   \
+        else if (a.block == 16) stats_tile_kernel<DT_, 16><<<grid, 256, 0, st>>>(k, ntx);            \
+        else stats_tile_kernel<DT_, 32><<<grid, 256, 0, st>>>(k, ntx);                               \
+    } while (0)
+    if (a.dtype == AXS6_F32) AXS6_STATS(AXS6_F32);
+    else if (a.dtype == AXS6_BF16) AXS6_STATS(AXS6_BF16);
+    else AXS6_STATS(AXS6_F16);
+#undef AXS6_STATS
+    if ((rc = check_launch("row_stats"))) return rc;
+    stats_finalize_kernel<<<dim3((unsigned)((a.rows + 255) / 256)), 256, 0, st>>>(
+        a.scratch, a.scratch + a.rows, a.rows, a.shift, a.rowx, a.gmax);
+    return check_launch("row_stats");
 }
 
 int launch_reduce_partials(const float* partial, int64_t chunks, int64_t cols, float* out, hipStream_t st) {
     if (cols == 0) return AXS6_OK;
-    reduce_partials_kernel<<<dim3((unsigned)((cols + 255) / 256)), 256, 0, st>>>(partial, chunks, cols, out);
+    reduce_partials_kernel<<<dim3((unsigned)((cols + 63) / 64)), 256, 0, st>>>(partial, chunks, cols, out);
     return check_launch("reduce_partials");
 }
 

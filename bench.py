@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the AXS-6 NF5 hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-linear]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-linear] [--no-minigpt]
 
 Workload (BASELINE.json metric "NF5 fake-quant GB/s @8192x4096 fp32; AXS-6
 linear TFLOP/s @4096^3 bf16"):
@@ -12,6 +12,10 @@ linear TFLOP/s @4096^3 bf16"):
     (4 read + 4 written) = 268,435,456 B.
   * "linear": the fused AXS-6 linear forward at M=N=K=4096 (config 3), FLOPs
     per step = 2*M*N*K, timed the same way.
+  * "linear_train": config 4, forward + backward at its four shapes
+    (6*M*N*K FLOPs per step).
+  * "minigpt": config 5, the MiniGPT training step with every nn.Linear
+    converted (ms/step and the loss curve, beside the fp32 model).
 Inputs are synthetic, resident in HBM before the timed region.  K steps are
 timed between device synchronisations as replays of a HIP graph holding 20
 steps' kernels (every kernel runs every step; the graph removes the host
@@ -176,6 +180,96 @@ def bench_linear(steps: int, warmup: int):
             "kernels": kern}
 
 
+LIN_TRAIN_SHAPES = [(8192, 4096, 11008), (8192, 11008, 4096), (2048, 768, 3072), (2048, 3072, 768)]
+
+
+def bench_linear_train(reps: int = 5, warmup: int = 2):
+    """quantized linear forward + backward (stochastic FQ of
+    dY, dX, dW and db) at each [M, K, N]; FLOPs per step = 6*M*N*K.  Device
+    time per step from HIP events on torch's current stream around `reps`
+    steps through hip_linear (the kernels run ~0.1-3 ms per step, so the host
+    launch cost is hidden)."""
+    import torch
+
+    from axs.unified import hip_linear
+
+    rows = []
+    for (M, K, N) in LIN_TRAIN_SHAPES:
+        g = torch.Generator(device="cuda").manual_seed(7)
+        X = torch.randn(M, K, device="cuda", generator=g)
+        W = torch.randn(N, K, device="cuda", generator=g) * K ** -0.5
+        b = torch.zeros(N, device="cuda")
+        dY = torch.randn(M, N, device="cuda", generator=g)
+
+        def fwd():
+            return hip_linear.forward_train(X, W, b, 32, True)
+
+        def step():
+            _, saved = fwd()
+            hip_linear.backward(dY, saved, 32, True, True, True, True)
+
+        def timed(fn):
+            for _ in range(warmup):
+                fn()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / reps
+
+        ms_step = timed(step)
+        ms_fwd = timed(fwd)
+        flops = 6.0 * M * N * K
+        rows.append({"shape_mkn": [M, K, N], "ms_per_step": round(ms_step, 4), "fwd_ms": round(ms_fwd, 4),
+                     "bwd_ms": round(ms_step - ms_fwd, 4),
+                     "tflops": round(flops / (ms_step * 1e-3) / 1e12, 1),
+                     "frac_of_peak": round(flops / (ms_step * 1e-3) / 1e12 / BF16_DENSE_PEAK_TFLOPS, 4)})
+        log(f"linear fwd+bwd {M}x{K}x{N}: {ms_step:.3f} ms/step ({rows[-1]['tflops']} TFLOP/s)")
+        del X, W, b, dY
+    return {"metric": "AXS-6 linear fwd+bwd TFLOP/s (config 4, 6*M*N*K per step)", "shapes": rows}
+
+
+def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
+    """MiniGPT (4 layers, d 256, FFN 1024, vocab 256, ctx 128,
+    batch 64) with every nn.Linear converted to the AXS-6 linear, AdamW lr 3e-4,
+    fp32 master weights, one fixed synthetic batch (tests/minigpt.py).  A step
+    is forward + cross-entropy + backward + AdamW through the Python API.
+    Reported: ms/step over the steps after `warmup`, the loss curve at a few
+    points, the same for the unquantized fp32 model, and the CPU reference
+    restatement's ms/step over `ref_steps` steps (host cores)."""
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import minigpt
+
+    x, y = minigpt.batch(1)
+    torch.manual_seed(5)
+    model = minigpt.build_axs(0, "cuda")
+    losses, ms = minigpt.train(model, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize)
+    fp32 = minigpt.base_model(0).cuda()
+    fp_losses, fp_ms = minigpt.train(fp32, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize)
+    pts = [0, steps // 4, steps // 2, 3 * steps // 4, steps - 1]
+    out = {
+        "metric": "MiniGPT AXS-6 training ms/step (config 5)",
+        "ms_per_step": round(ms, 3), "steps": steps, "warmup": warmup,
+        "loss": {str(i): round(losses[i], 4) for i in pts},
+        "fp32_model": {"ms_per_step": round(fp_ms, 3), "loss": {str(i): round(fp_losses[i], 4) for i in pts}},
+    }
+    if ref_steps:
+        from oracle import eager_torch  # noqa: F401  (the CPU reference restatement)
+
+        torch.manual_seed(6)
+        ref = minigpt.build_reference(0)
+        ref_losses, ref_ms = minigpt.train(ref, x, y, ref_steps + 1, warmup=1)
+        out["cpu_reference"] = {"ms_per_step": round(ref_ms, 1), "threads": torch.get_num_threads(),
+                                "steps_timed": ref_steps, "kind": "port",
+                                "loss": {str(i): round(v, 4) for i, v in enumerate(ref_losses)}}
+    return out
+
+
 def cpu_baseline_fq(budget_s: float = 12.0):
     import torch
 
@@ -279,6 +373,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-linear", action="store_true")
+    ap.add_argument("--no-minigpt", action="store_true")
     ap.add_argument("--gemm-only", type=int, default=0, metavar="N",
                     help="time the fp16 MFMA GEMM alone at N^3 (launch-shape sweeps)")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -355,6 +450,15 @@ def main() -> int:
             }
         except NotImplementedError as e:
             log(f"linear: skipped ({e})")
+
+    if not a.no_linear:
+        log("linear fwd+bwd (config 4) ...")
+        out["linear_train"] = bench_linear_train()
+
+    if not a.no_minigpt:
+        log("minigpt (config 5) ...")
+        out["minigpt"] = bench_minigpt(ref_steps=0 if a.no_cpu_baseline else 3)
+        log(f"minigpt: {out['minigpt']['ms_per_step']} ms/step, loss {out['minigpt']['loss']}")
 
     if not a.no_cpu_baseline:
         log("cpu baseline ...")

@@ -15,8 +15,10 @@
  *   - dtype codes: AXS6_F32, AXS6_BF16, AXS6_F16 select the element type of
  *     the input and of the same-typed output; arithmetic is float32;
  *   - stochastic rounding (dither of +-0.5 LUT steps) draws U[0,1) for the
- *     element at flat index i from splitmix64(seed + (offset + i) * golden),
- *     so a (seed, offset) pair reproduces a draw exactly.
+ *     element at flat index i from a keyed hash of the counter offset + i
+ *     (key = splitmix64 finaliser of seed; a 32-bit multiply-xorshift hash
+ *     per element; top 24 bits), so a (seed, offset) pair reproduces a draw
+ *     exactly.
  *
  * Python binding: axs-6_amd/axs/_lib.py (ctypes).  The reference entry
  * point each call replaces is cited on its declaration.

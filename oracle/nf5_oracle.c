@@ -15,8 +15,9 @@
  *   oracle_fake_quantize  fused_fake_quantize                     quantize_unified.py:121-204
  *   oracle_quantize       quantize_unified                        quantize_unified.py:211-282
  *   oracle_dequantize     dequantize_unified                      quantize_unified.py:285-308
- *   oracle_uniform        the HIP library's own dither stream (splitmix64), so
- *                         the stochastic kernels can be checked bit-for-bit.
+ *   oracle_uniform        the HIP library's own dither stream (keyed 32-bit
+ *                         hash), so the stochastic kernels can be checked
+ *                         bit-for-bit.
  *
  * How each piece is pinned (tests/test_oracle.py):
  *   - codebook / LUT: SHA-256 of the float32 bytes against the values the
@@ -298,15 +299,31 @@ void oracle_dequantize(const uint8_t* exps, const uint8_t* codes,
     }
 }
 
-/* The HIP library's dither stream: U = top 24 bits of splitmix64's output
- * mix of (seed + (offset + i) * golden), scaled by 2^-24.  Restated here so
- * the stochastic kernels can be compared bit-for-bit with the oracle. */
+/* The HIP library's dither stream (its own design; the reference draws
+ * torch.rand_like, whose stream cannot be reproduced, so stochastic parity
+ * with the reference is distributional).  key = splitmix64 finaliser of the
+ * seed; the draw for element counter c = offset + i is Wellons' "lowbias32"
+ * multiply-xorshift hash of (low word of c) ^ key_lo ^ (high word of c *
+ * 0x9E3779B9 + key_hi), whose top 24 bits times 2^-24 give U in [0, 1).
+ * Restated here so the stochastic kernels can be compared bit-for-bit. */
+static uint64_t dither_key(uint64_t seed) {
+    uint64_t z = seed + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
 void oracle_uniform(uint64_t seed, uint64_t offset, int64_t n, float* u) {
+    const uint64_t key = dither_key(seed);
     for (int64_t i = 0; i < n; ++i) {
-        uint64_t z = seed + (offset + (uint64_t)i) * 0x9E3779B97F4A7C15ull;
-        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-        z = z ^ (z >> 31);
-        u[i] = (float)(uint32_t)(z >> 40) * (1.0f / 16777216.0f);
+        const uint64_t c = offset + (uint64_t)i;
+        uint32_t h = (uint32_t)c ^ (uint32_t)key ^
+                     ((uint32_t)(c >> 32) * 0x9E3779B9u + (uint32_t)(key >> 32));
+        h ^= h >> 16;
+        h *= 0x7feb352du;
+        h ^= h >> 15;
+        h *= 0x846ca68bu;
+        h ^= h >> 16;
+        u[i] = (float)(h >> 8) * (1.0f / 16777216.0f);
     }
 }
