@@ -1,0 +1,274 @@
+// NF5 wire format (gfx950): the reference's 6.25-bit gradient encoding,
+// produced and consumed on the device in one pass each way.
+//
+// Record of one block of `bs` values (bs in {8, 16, 32}), blocks in row-major
+// order, a row's last block zero-padded virtually:
+//   byte 0                 shared exponent e (uint8, quantize_unified's rule)
+//   bytes 1 .. 3*bs/4      6-bit codes q = (sign << 5) | code, four per three
+//                          bytes:  b0 = q0 | q1<<6,  b1 = q1>>2 | q2<<4,
+//                                  b2 = q2>>4 | q3<<2   (low bits first)
+// so a 32-value block takes 25 bytes.  Layout of _pack_to_flat_buffer
+// (axs/unified/distributed.py:147-198); the codes are those of
+// _pack_gradient (:70-115), i.e. quantize_unified with nearest rounding.
+//
+// One thread handles one group of four values (three bytes); a block is
+// bs/4 neighbouring lanes, whose amax is a DPP reduction.  Byte traffic is
+// small next to the 4 B/value read, so the stores stay byte-granular.
+#include "nf5_device.h"
+
+namespace axs6 {
+namespace {
+
+__device__ __forceinline__ void pack3(const int (&q)[4], uint8_t* out) {
+    out[0] = (uint8_t)((q[0] & 0x3F) | ((q[1] & 0x03) << 6));
+    out[1] = (uint8_t)(((q[1] >> 2) & 0x0F) | ((q[2] & 0x0F) << 4));
+    out[2] = (uint8_t)(((q[2] >> 4) & 0x03) | ((q[3] & 0x3F) << 2));
+}
+
+__device__ __forceinline__ void unpack3(const uint8_t* in, int (&q)[4]) {
+    const int b0 = in[0], b1 = in[1], b2 = in[2];
+    q[0] = b0 & 0x3F;
+    q[1] = ((b0 >> 6) & 0x03) | ((b1 & 0x0F) << 2);
+    q[2] = ((b1 >> 4) & 0x0F) | ((b2 & 0x03) << 4);
+    q[3] = (b2 >> 2) & 0x3F;
+}
+
+struct WireGeom {
+    int64_t rows, cols, nblk, groups;   // groups = rows * nblk * bs / 4
+};
+
+// x [rows, cols] -> records.  Exponent: e = clamp(floor(log2(max(amax,
+// 1e-45))) + 1 + 127, 0, 255), 0 for an all-zero block (and for NaN/inf
+// amax, whose int cast is INT_MIN); index = trunc(clamp(|x| / 2^(e-127), 0, 1)
+// * 1023); code = reverse_lut[index]; sign = x < 0.
+template <int DT, int BS>
+__global__ __launch_bounds__(kThreads) void wire_pack_kernel(const typename Elem<DT>::S* __restrict__ x, WireGeom g,
+                                                             const uint8_t* __restrict__ band_g,
+                                                             const uint8_t* __restrict__ rev_g,
+                                                             uint8_t* __restrict__ buf) {
+    using E = Elem<DT>;
+    constexpr int GPB = BS / 4;                 // groups (lanes) per block
+    constexpr int REC = 1 + BS * 3 / 4;         // bytes per block record
+    __shared__ uint32_t band_w[kBandSize / 4];
+    __shared__ uint8_t rev_s[kLutSize];
+    const int tid = threadIdx.x;
+    reinterpret_cast<uint32_t*>(rev_s)[tid] = reinterpret_cast<const uint32_t*>(rev_g)[tid];
+    if (tid < kBandSize / 4) band_w[tid] = reinterpret_cast<const uint32_t*>(band_g)[tid];
+    __syncthreads();
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+
+    const int64_t step = (int64_t)gridDim.x * kThreads;
+    // the loop bound is rounded up to whole waves so every lane of a block's
+    // DPP group runs every iteration
+    const int64_t span = (g.groups + 63) / 64 * 64;
+    for (int64_t q = (int64_t)blockIdx.x * kThreads + tid; q < span; q += step) {
+        const bool vq = q < g.groups;
+        const int64_t blk = vq ? q / GPB : 0;
+        const int j4 = (int)(q % GPB);
+        const int64_t r = blk / g.nblk;
+        const int64_t c0 = (blk - r * g.nblk) * BS + j4 * 4;
+        float f[4];
+        uint32_t m = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t c = c0 + e;
+            f[e] = (vq && c < g.cols) ? E::to_f(x[r * g.cols + c]) : 0.0f;
+            const uint32_t a = __float_as_uint(f[e]) & 0x7fffffffu;
+            m = m > a ? m : a;
+        }
+        m = group_umax<GPB>(m);
+        int e8 = (m == 0u || m >= kInfBits) ? 0 : floor_log2_torch(m, band_s) + 1 + kExpBias;
+        e8 = e8 < 0 ? 0 : (e8 > 255 ? 255 : e8);
+        const int se = e8 - kExpBias;           // scale 2^se, se in [-127, 128]
+        int qv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t ab = __float_as_uint(f[e]) & 0x7fffffffu;
+            float n;
+            if (se >= 128) n = ab >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;
+            else n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -se);
+            n = n > 1.0f ? 1.0f : n;            // clamp(0, 1); NaN passes to the index rule
+            const int idx = lut_index(n, false, 0.0f);
+            qv[e] = (int)rev_s[idx] | ((f[e] < 0.0f ? 1 : 0) << 5);
+        }
+        if (vq) {
+            uint8_t* rec = buf + blk * REC;
+            if (j4 == 0) rec[0] = (uint8_t)e8;
+            pack3(qv, rec + 1 + 3 * j4);
+        }
+    }
+}
+
+// records -> y [rows, cols] f32: codebook[code] * 2^(e-127), negated where the
+// sign bit is set (_unpack_from_flat_buffer + _unpack_gradient, :118-144,201-232).
+template <int BS>
+__global__ __launch_bounds__(kThreads) void wire_unpack_kernel(const uint8_t* __restrict__ buf, WireGeom g,
+                                                               const float* __restrict__ cb_g, float* __restrict__ y) {
+    constexpr int GPB = BS / 4;
+    constexpr int REC = 1 + BS * 3 / 4;
+    __shared__ float cb[kLevels];
+    if (threadIdx.x < kLevels) cb[threadIdx.x] = cb_g[threadIdx.x];
+    __syncthreads();
+    const int64_t step = (int64_t)gridDim.x * kThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < g.groups; q += step) {
+        const int64_t blk = q / GPB;
+        const int j4 = (int)(q % GPB);
+        const int64_t r = blk / g.nblk;
+        const int64_t c0 = (blk - r * g.nblk) * BS + j4 * 4;
+        const uint8_t* rec = buf + blk * REC;
+        const float scale = pow2_float((int)rec[0] - kExpBias);
+        int qv[4];
+        unpack3(rec + 1 + 3 * j4, qv);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t c = c0 + e;
+            if (c < g.cols) {
+                const float v = cb[qv[e] & 0x1F] * scale;
+                y[r * g.cols + c] = (qv[e] & 0x20) ? -v : v;
+            }
+        }
+    }
+}
+
+// AXSTensor components (exponents [rows, nblk], codes and signs [rows, nblk, bs])
+// <-> records, for the component-level API (_pack_to_flat_buffer /
+// _unpack_from_flat_buffer).
+__global__ __launch_bounds__(kThreads) void wire_from_codes_kernel(const uint8_t* __restrict__ exps,
+                                                                   const uint8_t* __restrict__ codes,
+                                                                   const uint8_t* __restrict__ signs, int bs,
+                                                                   int64_t groups, uint8_t* __restrict__ buf) {
+    const int gpb = bs / 4, rec_bytes = 1 + bs * 3 / 4;
+    const int64_t step = (int64_t)gridDim.x * kThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < groups; q += step) {
+        const int64_t blk = q / gpb;
+        const int j4 = (int)(q % gpb);
+        int qv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t o = q * 4 + e;
+            qv[e] = (codes[o] & 0x1F) | ((signs && signs[o]) ? 0x20 : 0);
+        }
+        uint8_t* rec = buf + blk * rec_bytes;
+        if (j4 == 0) rec[0] = exps[blk];
+        pack3(qv, rec + 1 + 3 * j4);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void wire_to_codes_kernel(const uint8_t* __restrict__ buf, int bs,
+                                                                 int64_t groups, uint8_t* __restrict__ exps,
+                                                                 uint8_t* __restrict__ codes,
+                                                                 uint8_t* __restrict__ signs) {
+    const int gpb = bs / 4, rec_bytes = 1 + bs * 3 / 4;
+    const int64_t step = (int64_t)gridDim.x * kThreads;
+    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < groups; q += step) {
+        const int64_t blk = q / gpb;
+        const int j4 = (int)(q % gpb);
+        const uint8_t* rec = buf + blk * rec_bytes;
+        int qv[4];
+        unpack3(rec + 1 + 3 * j4, qv);
+        if (j4 == 0) exps[blk] = rec[0];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t o = q * 4 + e;
+            codes[o] = (uint8_t)(qv[e] & 0x1F);
+            if (signs) signs[o] = (uint8_t)((qv[e] >> 5) & 1);
+        }
+    }
+}
+
+unsigned wire_grid(int64_t groups) {
+    const int64_t wgs = (groups + kThreads - 1) / kThreads;
+    return (unsigned)(wgs < 65536 ? (wgs > 0 ? wgs : 1) : 65536);
+}
+
+int check_wire(const char* fn, int64_t rows, int64_t cols, int bs) {
+    if (!valid_block(bs)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: block_size must be 8, 16 or 32 (got %d)", fn, bs);
+    if (rows < 0 || cols < 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: negative shape", fn);
+    if (rows > ((int64_t)1 << 40) / (cols + 1)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: tensor too large", fn);
+    return AXS6_OK;
+}
+
+}  // namespace
+}  // namespace axs6
+
+using namespace axs6;
+
+extern "C" int64_t axs6_nf5_wire_bytes(int64_t rows, int64_t cols, int32_t block_size) {
+    if (rows < 0 || cols < 0 || !valid_block(block_size)) return -1;
+    const int64_t nblk = (cols + block_size - 1) / block_size;
+    return rows * nblk * (1 + block_size * 3 / 4);
+}
+
+extern "C" int axs6_nf5_pack_wire(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
+                                  uint8_t* buffer, void* stream) {
+    const char* fn = "axs6_nf5_pack_wire";
+    if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
+    int rc = check_wire(fn, rows, cols, block_size);
+    if (rc) return rc;
+    if (rows == 0 || cols == 0) return AXS6_OK;
+    if (!x || !buffer) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    DeviceTables t;
+    if ((rc = device_tables(&t))) return rc;
+    const int64_t nblk = (cols + block_size - 1) / block_size;
+    const WireGeom g{rows, cols, nblk, rows * nblk * (block_size / 4)};
+    const dim3 grid(wire_grid(g.groups));
+    hipStream_t st = (hipStream_t)stream;
+#define AXS6_WIRE(DT_)                                                                                         \
+    do {                                                                                                       \
+        using S_ = typename Elem<DT_>::S;                                                                      \
+        if (block_size == 8) wire_pack_kernel<DT_, 8><<<grid, kThreads, 0, st>>>((const S_*)x, g, t.band, t.rev, buffer);   \
+        else if (block_size == 16) wire_pack_kernel<DT_, 16><<<grid, kThreads, 0, st>>>((const S_*)x, g, t.band, t.rev, buffer); \
+        else wire_pack_kernel<DT_, 32><<<grid, kThreads, 0, st>>>((const S_*)x, g, t.band, t.rev, buffer);     \
+    } while (0)
+    if (dtype == AXS6_F32) AXS6_WIRE(AXS6_F32);
+    else if (dtype == AXS6_BF16) AXS6_WIRE(AXS6_BF16);
+    else AXS6_WIRE(AXS6_F16);
+#undef AXS6_WIRE
+    return check_launch(fn);
+}
+
+extern "C" int axs6_nf5_unpack_wire(const uint8_t* buffer, int64_t rows, int64_t cols, int32_t block_size, float* y,
+                                    void* stream) {
+    const char* fn = "axs6_nf5_unpack_wire";
+    int rc = check_wire(fn, rows, cols, block_size);
+    if (rc) return rc;
+    if (rows == 0 || cols == 0) return AXS6_OK;
+    if (!buffer || !y) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    DeviceTables t;
+    if ((rc = device_tables(&t))) return rc;
+    const int64_t nblk = (cols + block_size - 1) / block_size;
+    const WireGeom g{rows, cols, nblk, rows * nblk * (block_size / 4)};
+    const dim3 grid(wire_grid(g.groups));
+    hipStream_t st = (hipStream_t)stream;
+    if (block_size == 8) wire_unpack_kernel<8><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);
+    else if (block_size == 16) wire_unpack_kernel<16><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);
+    else wire_unpack_kernel<32><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);
+    return check_launch(fn);
+}
+
+extern "C" int axs6_nf5_wire_from_codes(const uint8_t* exponents, const uint8_t* codes, const uint8_t* signs,
+                                        int64_t rows, int64_t nblk, int32_t block_size, uint8_t* buffer,
+                                        void* stream) {
+    const char* fn = "axs6_nf5_wire_from_codes";
+    int rc = check_wire(fn, rows, nblk * (int64_t)block_size, block_size);
+    if (rc) return rc;
+    if (rows == 0 || nblk == 0) return AXS6_OK;
+    if (!exponents || !codes || !buffer) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    const int64_t groups = rows * nblk * (block_size / 4);
+    wire_from_codes_kernel<<<dim3(wire_grid(groups)), kThreads, 0, (hipStream_t)stream>>>(exponents, codes, signs,
+                                                                                          block_size, groups, buffer);
+    return check_launch(fn);
+}
+
+extern "C" int axs6_nf5_wire_to_codes(const uint8_t* buffer, int64_t rows, int64_t nblk, int32_t block_size,
+                                      uint8_t* exponents, uint8_t* codes, uint8_t* signs, void* stream) {
+    const char* fn = "axs6_nf5_wire_to_codes";
+    int rc = check_wire(fn, rows, nblk * (int64_t)block_size, block_size);
+    if (rc) return rc;
+    if (rows == 0 || nblk == 0) return AXS6_OK;
+    if (!buffer || !exponents || !codes) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    const int64_t groups = rows * nblk * (block_size / 4);
+    wire_to_codes_kernel<<<dim3(wire_grid(groups)), kThreads, 0, (hipStream_t)stream>>>(buffer, block_size, groups,
+                                                                                        exponents, codes, signs);
+    return check_launch(fn);
+}

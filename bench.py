@@ -14,6 +14,8 @@ linear TFLOP/s @4096^3 bf16"):
     per step = 2*M*N*K, timed the same way.
   * "linear_train": config 4, forward + backward at its four shapes
     (6*M*N*K FLOPs per step).
+  * "wire": the 6.25-bit gradient wire format (quantize+pack, unpack) at
+    8192x4096, GB/s.
   * "minigpt": config 5, the MiniGPT training step with every nn.Linear
     converted (ms/step and the loss curve, beside the fp32 model).
 Inputs are synthetic, resident in HBM before the timed region.  K steps are
@@ -178,6 +180,41 @@ def bench_linear(steps: int, warmup: int):
     kern = hip_linear.last_forward_kernel_times(X, W, b, reps=max(steps, 10))
     return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "eager_ms": eager_ms, "flops": 2.0 * M * N * K,
             "kernels": kern}
+
+
+def bench_wire(reps: int = 20, warmup: int = 3):
+    """NF5 wire format (the reference's 6.25-bit gradient buffer) of one
+    8192x4096 f32 tensor: quantize+pack and unpack+dequantize, one kernel each.
+    Algorithmic bytes: pack 4 B read + 25/32 B written per value; unpack the
+    reverse.  HIP-event device time per call."""
+    import torch
+
+    from axs.unified import distributed as d
+
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(*FQ_SHAPE, device="cuda", generator=g)
+    buf = d.pack_gradient_to_buffer(x, 32)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    pack_ms = timed(lambda: d.pack_gradient_to_buffer(x, 32))
+    unpack_ms = timed(lambda: d.unpack_buffer_to_gradient(buf, x.shape, 32))
+    nbytes = x.numel() * 4 + buf.numel()
+    return {"metric": "NF5 wire format GB/s @8192x4096 fp32 (quantize+pack, unpack+dequantize)",
+            "buffer_bytes": buf.numel(), "bits_per_value": round(buf.numel() * 8 / x.numel(), 4),
+            "pack_ms": round(pack_ms, 5), "unpack_ms": round(unpack_ms, 5),
+            "pack_gbs": round(nbytes / (pack_ms * 1e-3) / 1e9, 1),
+            "unpack_gbs": round(nbytes / (unpack_ms * 1e-3) / 1e9, 1)}
 
 
 LIN_TRAIN_SHAPES = [(8192, 4096, 11008), (8192, 11008, 4096), (2048, 768, 3072), (2048, 3072, 768)]
@@ -450,6 +487,9 @@ def main() -> int:
             }
         except NotImplementedError as e:
             log(f"linear: skipped ({e})")
+
+    out["wire"] = bench_wire()
+    log(f"wire 8192x4096: pack {out['wire']['pack_gbs']} GB/s, unpack {out['wire']['unpack_gbs']} GB/s")
 
     if not a.no_linear:
         log("linear fwd+bwd (config 4) ...")

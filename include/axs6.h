@@ -86,6 +86,41 @@ int axs6_nf5_quantize(const void* x, int32_t dtype, int64_t rows, int64_t cols,
 int axs6_nf5_dequantize(const uint8_t* exponents, const uint8_t* codes, const uint8_t* signs,
                         float* y, int64_t rows, int64_t cols, int32_t block_size, void* stream);
 
+/* ---- NF5 wire format ---------------------------------------------------------
+ * The 6.25-bit encoding of a gradient: per block of block_size values (blocks
+ * in row-major order, the last block of a row zero-padded), one record of
+ * 1 + block_size*3/4 bytes: byte 0 the shared exponent (quantize's rule),
+ * then 6-bit codes q = (sign << 5) | code, four per three bytes, low bits
+ * first (b0 = q0 | q1<<6, b1 = q1>>2 | q2<<4, b2 = q2>>4 | q3<<2).  A 32-value
+ * block takes 25 bytes.  Codes use nearest rounding.
+ */
+
+/* Bytes of the wire buffer for a rows x cols tensor (-1 on bad arguments). */
+int64_t axs6_nf5_wire_bytes(int64_t rows, int64_t cols, int32_t block_size);
+
+/* Quantize x [rows, cols] (`dtype`) straight into the wire buffer.
+ * Replaces: _pack_gradient + _pack_to_flat_buffer
+ *           (axs/unified/distributed.py:70-115,147-198). */
+int axs6_nf5_pack_wire(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
+                       uint8_t* buffer, void* stream);
+
+/* Decode a wire buffer to y [rows, cols] f32: +-codebook[code] * 2^(e-127).
+ * Replaces: _unpack_from_flat_buffer + _unpack_gradient
+ *           (axs/unified/distributed.py:201-232,118-144). */
+int axs6_nf5_unpack_wire(const uint8_t* buffer, int64_t rows, int64_t cols, int32_t block_size, float* y,
+                         void* stream);
+
+/* AXSTensor components (exponents u8 [rows, nblk], codes and signs u8
+ * [rows, nblk, block_size]; signs may be NULL) -> wire buffer.
+ * Replaces: _pack_to_flat_buffer (axs/unified/distributed.py:147-198). */
+int axs6_nf5_wire_from_codes(const uint8_t* exponents, const uint8_t* codes, const uint8_t* signs,
+                             int64_t rows, int64_t nblk, int32_t block_size, uint8_t* buffer, void* stream);
+
+/* Wire buffer -> AXSTensor components (signs may be NULL).
+ * Replaces: _unpack_from_flat_buffer (axs/unified/distributed.py:201-232). */
+int axs6_nf5_wire_to_codes(const uint8_t* buffer, int64_t rows, int64_t nblk, int32_t block_size,
+                           uint8_t* exponents, uint8_t* codes, uint8_t* signs, void* stream);
+
 /* ---- quantized linear ------------------------------------------------------
  * The linear contracts NF5 fake-quantized operands on fp16 MFMA.  Operands are
  * packed as fp16 rows scaled by an exact power of two (2^-shift per row, so

@@ -9,6 +9,8 @@ Contents:
   * ``liboracle.so`` (built from ``nf5_oracle.c`` by ``make -C oracle``): a
     scalar C restatement of the reference's eager NF5 operations
     (``axs/unified/quantize_unified.py:50-308``), wrapped below for numpy.
+  * :func:`wire_pack` / :func:`wire_unpack`: the reference's 6.25-bit gradient
+    buffer layout (``axs/unified/distributed.py:147-232``).
   * :func:`linear_reference`: the fp64 product of fake-quantized operands
     that the quantized-linear kernels are compared to
     (``axs/unified/functional_unified.py:107-170``).
@@ -137,6 +139,39 @@ def dequantize(exps: np.ndarray, codes: np.ndarray, signs: np.ndarray, cols: int
     lib().oracle_dequantize(_p(exps, _u8p), _p(codes, _u8p), _p(s, _u8p), _p(y, _f32p),
                             R, cols, block_size)
     return y
+
+
+def wire_pack(exps: np.ndarray, codes: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """_pack_to_flat_buffer (axs/unified/distributed.py:147-198): per block, the
+    exponent byte then the 6-bit codes (sign << 5 | code) packed four per three
+    bytes with the reference's shifts and masks (:178-183).  uint8 [R*nblk*rec]."""
+    R, nblk, bs = codes.shape
+    assert bs % 4 == 0
+    q = codes.astype(np.int32) | (np.asarray(signs).astype(np.int32) << 5)
+    q = q.reshape(R, nblk, bs // 4, 4)
+    c0, c1, c2, c3 = q[..., 0], q[..., 1], q[..., 2], q[..., 3]
+    b0 = (c0 & 0x3F) | ((c1 & 0x03) << 6)
+    b1 = ((c1 >> 2) & 0x0F) | ((c2 & 0x0F) << 4)
+    b2 = ((c2 >> 4) & 0x03) | ((c3 & 0x3F) << 2)
+    vals = np.stack([b0, b1, b2], axis=-1).reshape(R, nblk, bs * 3 // 4).astype(np.uint8)
+    out = np.zeros((R, nblk, 1 + bs * 3 // 4), np.uint8)
+    out[:, :, 0] = exps
+    out[:, :, 1:] = vals
+    return out.reshape(-1)
+
+
+def wire_unpack(buf: np.ndarray, rows: int, nblk: int, bs: int):
+    """_unpack_from_flat_buffer (distributed.py:201-232): (exps, codes, signs)."""
+    b = np.asarray(buf).view(np.uint8).reshape(rows, nblk, 1 + bs * 3 // 4)
+    exps = b[:, :, 0].copy()
+    v = b[:, :, 1:].reshape(rows, nblk, bs // 4, 3).astype(np.int32)
+    b0, b1, b2 = v[..., 0], v[..., 1], v[..., 2]
+    c0 = b0 & 0x3F
+    c1 = ((b0 >> 6) & 0x03) | ((b1 & 0x0F) << 2)
+    c2 = ((b1 >> 4) & 0x0F) | ((b2 & 0x03) << 4)
+    c3 = (b2 >> 2) & 0x3F
+    q = np.stack([c0, c1, c2, c3], axis=-1).reshape(rows, nblk, bs)
+    return exps, (q & 0x1F).astype(np.uint8), ((q >> 5) & 1).astype(bool)
 
 
 def linear_reference(xq: np.ndarray, wq: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
