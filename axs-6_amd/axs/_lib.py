@@ -35,11 +35,11 @@ _f32p = ctypes.POINTER(ctypes.c_float)
 _SIGNATURES: dict[str, list] = {
     "axs6_init": [],
     "axs6_get_tables": [_f32p, _f32p, _u8p, _u8p],
-    "axs6_nf5_fake_quantize": [_vp, _vp, _i32, _i64, _i64, _i32, _i32, _u64, _u64, _vp],
-    "axs6_nf5_quantize": [_vp, _i32, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _vp, _vp, _vp],
+    "axs6_nf5_fake_quantize": [_vp, _vp, _i32, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp],
+    "axs6_nf5_quantize": [_vp, _i32, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _vp, _vp, _vp, _vp],
     "axs6_nf5_dequantize": [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
     "axs6_linear_padded_k": [_i64],
-    "axs6_nf5_pack_rows": [_vp, _i32, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _i64, _i64, _vp, _vp],
+    "axs6_nf5_pack_rows": [_vp, _i32, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _i64, _i64, _vp, _vp, _vp],
     "axs6_gemm_f16_nt": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i32, _vp],
     "axs6_nf5_linear_forward": [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp,
                                 _vp, _vp],
@@ -50,7 +50,7 @@ _SIGNATURES: dict[str, list] = {
     "axs6_nf5_wire_from_codes": [_vp, _vp, _vp, _i64, _i64, _i32, _vp, _vp],
     "axs6_nf5_wire_to_codes": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp],
     "axs6_nf5_linear_backward": [_vp, _i32, _i64, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _vp, _vp,
-                                 _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp],
+                                 _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp, _vp],
 }
 # entry points that return a value rather than an axs6_status
 _RESTYPES = {"axs6_linear_padded_k": _i64, "axs6_nf5_linear_backward_workspace": ctypes.c_size_t,

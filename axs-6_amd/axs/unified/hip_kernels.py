@@ -72,6 +72,51 @@ def next_seed() -> int:
     return int(torch.randint(0, 2**62, (1,)).item())
 
 
+# Per-device uint64 counters for stochastic calls recorded in a HIP graph.
+# A recorded call keeps the seed drawn at capture time; the library adds the
+# counter's value, read when the kernel runs, and a recorded increment after
+# the call advances it -- so every replay draws fresh dither values.
+_graph_counters: dict[int, torch.Tensor] = {}
+
+
+def _graph_counter(device: torch.device) -> torch.Tensor:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ctr = _graph_counters.get(idx)
+    if ctr is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                "a stochastic AXS-6 call is being recorded in a HIP graph before any stochastic call ran "
+                "eagerly on this device; run one warm-up step before capture (or call "
+                "axs.unified.hip_kernels.prepare_graph_capture())")
+        ctr = torch.zeros(1, dtype=torch.int64, device=torch.device("cuda", idx))
+        _graph_counters[idx] = ctr
+    return ctr
+
+
+def prepare_graph_capture(device: torch.device | int | None = None) -> None:
+    """Creates the device's dither counter outside capture (optional: the
+    first eager stochastic call does it)."""
+    d = torch.device("cuda", torch.cuda.current_device() if device is None else
+                     (device if isinstance(device, int) else device.index))
+    _graph_counter(d)
+
+
+def stochastic_seed(device: torch.device, seed: int | None = None) -> tuple[int, int | None, torch.Tensor | None]:
+    """(seed, seed_dev pointer or None, counter to advance after the call or None).
+
+    Eagerly, a fresh host draw (or ``seed``) and no device term.  While the
+    current stream is capturing a graph and no explicit ``seed`` is given, the
+    draw is fixed at capture time and the per-device counter is added on the
+    device; the caller advances the counter after its launch."""
+    s = next_seed() if seed is None else int(seed)
+    if seed is None and torch.cuda.is_current_stream_capturing():
+        ctr = _graph_counter(device)
+        return s, ctr.data_ptr(), ctr
+    if seed is None:
+        _graph_counter(device)   # created eagerly, ready for a later capture
+    return s, None, None
+
+
 def as_rows(tensor: torch.Tensor) -> tuple[torch.Tensor, int, int]:
     """Contiguous view of ``tensor`` as (rows, cols) over its last dim, in a
     dtype the kernels take (f32 / bf16 / f16; anything else is computed in
@@ -111,10 +156,12 @@ def hip_fused_fake_quantize(
     x, rows, cols = as_rows(tensor)
     y = torch.empty_like(x)
     if rows and cols:
-        s = (next_seed() if seed is None else int(seed)) if stochastic else 0
+        s, sdev, ctr = stochastic_seed(x.device, seed) if stochastic else (0, None, None)
         with _on_device(x):
             _lib.call("axs6_nf5_fake_quantize", x.data_ptr(), y.data_ptr(), _lib.DTYPE_CODE[x.dtype],
-                      rows, cols, block_size, int(stochastic), s, 0, _lib.stream_of(x))
+                      rows, cols, block_size, int(stochastic), s, 0, sdev, _lib.stream_of(x))
+            if ctr is not None:
+                ctr.add_(1)
     y = y.reshape(tensor.shape)
     return y if y.dtype == orig_dtype else y.to(orig_dtype)
 
@@ -141,11 +188,13 @@ def hip_quantize(
     signs = torch.empty((rows, nblk, block_size), dtype=torch.uint8, device=dev)
     fq = torch.empty_like(x) if with_fake_quantized else None
     if rows and cols:
-        s = (next_seed() if seed is None else int(seed)) if stochastic else 0
+        s, sdev, ctr = stochastic_seed(x.device, seed) if stochastic else (0, None, None)
         with _on_device(x):
             _lib.call("axs6_nf5_quantize", x.data_ptr(), _lib.DTYPE_CODE[x.dtype], rows, cols,
                       block_size, int(stochastic), s, 0, exps.data_ptr(), codes.data_ptr(),
-                      signs.data_ptr(), _lib.ptr(fq), _lib.stream_of(x))
+                      signs.data_ptr(), _lib.ptr(fq), sdev, _lib.stream_of(x))
+            if ctr is not None:
+                ctr.add_(1)
     if fq is not None:
         fq = fq.reshape(tensor.shape)
         if fq.dtype != tensor.dtype:

@@ -18,7 +18,7 @@ import torch.nn.functional as F
 
 from axs import _lib
 from axs.core import VALID_BLOCK_SIZES
-from axs.unified.hip_kernels import _on_device, _require_device, next_seed
+from axs.unified.hip_kernels import _on_device, _require_device, stochastic_seed
 
 _SUPPORTED = (torch.float32, torch.bfloat16, torch.float16)
 
@@ -131,13 +131,15 @@ def backward(grad_output, saved: Saved, block_size: int, quantize_grad: bool,
         L = _lib_sigs()
         ws_bytes = int(L.axs6_nf5_linear_backward_workspace(M, N, K, int(need_x), int(need_w), int(need_b)))
         ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
-        seed = (next_seed() if seed is None else int(seed)) if quantize_grad else 0
+        s, sdev, ctr = stochastic_seed(dev, seed) if quantize_grad else (0, None, None)
         with _on_device(dy):
             _lib.call("axs6_nf5_linear_backward", dy.data_ptr(), _lib.DTYPE_CODE[saved.dtype], M, N, K,
-                      block_size, int(bool(quantize_grad)), seed, 0,
+                      block_size, int(bool(quantize_grad)), s, 0,
                       saved.xq.data_ptr(), saved.sx.data_ptr(), saved.wq.data_ptr(), saved.sw.data_ptr(),
-                      _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), ws.data_ptr(), ws_bytes,
+                      _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), ws.data_ptr(), ws_bytes, sdev,
                       _lib.stream_of(dy))
+            if ctr is not None:
+                ctr.add_(1)
     elif need_w:
         dw.zero_()
     if dx is not None:
@@ -179,9 +181,9 @@ def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         st = _lib.stream_of(a2)
         with _on_device(a2):
             _lib.call("axs6_nf5_pack_rows", a2.data_ptr(), _lib.F32, M, Kb, 32, 0, 0, 0, None,
-                      aq.data_ptr(), Kp, Kp, sa.data_ptr(), st)
+                      aq.data_ptr(), Kp, Kp, sa.data_ptr(), None, st)
             _lib.call("axs6_nf5_pack_rows", bt.data_ptr(), _lib.F32, N, Kb, 32, 0, 0, 0, None,
-                      bq.data_ptr(), Kp, Kp, sb.data_ptr(), st)
+                      bq.data_ptr(), Kp, Kp, sb.data_ptr(), None, st)
             _lib.call("axs6_gemm_f16_nt", aq.data_ptr(), Kp, bq.data_ptr(), Kp, M, N, Kp,
                       sa.data_ptr(), sb.data_ptr(), None, out.data_ptr(), N, _lib.F32, st)
     return out.reshape(*a.shape[:-1], N)
@@ -204,11 +206,11 @@ def last_forward_kernel_times(X, W, b, reps: int = 20) -> dict:
 
     def pack_x():
         _lib.call("axs6_nf5_pack_rows", X.data_ptr(), code, M, K, 32, 1, 0, 0, None, xq.data_ptr(), Kp, Kp,
-                  sx.data_ptr(), st)
+                  sx.data_ptr(), None, st)
 
     def pack_w():
         _lib.call("axs6_nf5_pack_rows", W.data_ptr(), code, N, K, 32, 1, 0, 0, None, wq.data_ptr(), Kp, Kp,
-                  sw.data_ptr(), st)
+                  sw.data_ptr(), None, st)
 
     def gemm():
         _lib.call("axs6_gemm_f16_nt", xq.data_ptr(), Kp, wq.data_ptr(), Kp, M, N, Kp, sx.data_ptr(),

@@ -48,6 +48,8 @@ struct GemmK {
     int M; int N; int Kp;
     const int32_t* row_exp; const int32_t* col_exp; const int32_t* glob_exp; int glob_add;
     const float* bias; void* out; int64_t ldo; int out_dtype;
+    int k_iters;            // 64-half K-steps per blockIdx.y (all of them without split-K)
+    int64_t split_stride;   // elements between the split outputs (0 without split-K)
 };
 
 __device__ __forceinline__ uint16_t to_bf16(float f) {
@@ -129,29 +131,106 @@ __device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const char* as, 
 // Writes 4 consecutive output values of row `row` starting at column `col`
 // (col % 4 == 0): one vector store when the 4 columns exist and the row
 // segment is aligned, else element by element up to N.
-__device__ __forceinline__ void store4(const GemmK& g, int row, int col, const float (&v)[4], bool vec) {
-    const int64_t o = (int64_t)row * g.ldo + col;
-    if (vec && col + 3 < g.N) {
-        if (g.out_dtype == AXS6_F32) {
-            *reinterpret_cast<float4*>(reinterpret_cast<float*>(g.out) + o) = make_float4(v[0], v[1], v[2], v[3]);
-        } else if (g.out_dtype == AXS6_BF16) {
+__device__ __forceinline__ void store4(void* out, int64_t ldo, int N, int out_dtype, int row, int col,
+                                       const float (&v)[4], bool vec) {
+    const int64_t o = (int64_t)row * ldo + col;
+    if (vec && col + 3 < N) {
+        if (out_dtype == AXS6_F32) {
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + o) = make_float4(v[0], v[1], v[2], v[3]);
+        } else if (out_dtype == AXS6_BF16) {
             uint2 w;
             w.x = (uint32_t)to_bf16(v[0]) | ((uint32_t)to_bf16(v[1]) << 16);
             w.y = (uint32_t)to_bf16(v[2]) | ((uint32_t)to_bf16(v[3]) << 16);
-            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(g.out) + o) = w;
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + o) = w;
         } else {
             typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
             f16x4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-            *reinterpret_cast<f16x4*>(reinterpret_cast<_Float16*>(g.out) + o) = h;
+            *reinterpret_cast<f16x4*>(reinterpret_cast<_Float16*>(out) + o) = h;
         }
         return;
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        if (col + t >= g.N) break;
-        if (g.out_dtype == AXS6_F32) reinterpret_cast<float*>(g.out)[o + t] = v[t];
-        else if (g.out_dtype == AXS6_BF16) reinterpret_cast<uint16_t*>(g.out)[o + t] = to_bf16(v[t]);
-        else reinterpret_cast<_Float16*>(g.out)[o + t] = (_Float16)v[t];
+        if (col + t >= N) break;
+        if (out_dtype == AXS6_F32) reinterpret_cast<float*>(out)[o + t] = v[t];
+        else if (out_dtype == AXS6_BF16) reinterpret_cast<uint16_t*>(out)[o + t] = to_bf16(v[t]);
+        else reinterpret_cast<_Float16*>(out)[o + t] = (_Float16)v[t];
+    }
+}
+
+// store4 with the output type fixed at compile time; `full` = the 4 columns
+// exist and the row segment is aligned for one vector store.
+template <int OUT>
+__device__ __forceinline__ void store4t(void* out, int64_t ldo, int N, int row, int col, const float (&v)[4],
+                                        bool full) {
+    const int64_t o = (int64_t)row * ldo + col;
+    if (full) {
+        if constexpr (OUT == AXS6_F32) {
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + o) = make_float4(v[0], v[1], v[2], v[3]);
+        } else if constexpr (OUT == AXS6_BF16) {
+            uint2 w;
+            w.x = (uint32_t)to_bf16(v[0]) | ((uint32_t)to_bf16(v[1]) << 16);
+            w.y = (uint32_t)to_bf16(v[2]) | ((uint32_t)to_bf16(v[3]) << 16);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + o) = w;
+        } else {
+            typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+            f16x4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+            *reinterpret_cast<f16x4*>(reinterpret_cast<_Float16*>(out) + o) = h;
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        if (col + t >= N) break;
+        if constexpr (OUT == AXS6_F32) reinterpret_cast<float*>(out)[o + t] = v[t];
+        else if constexpr (OUT == AXS6_BF16) reinterpret_cast<uint16_t*>(out)[o + t] = to_bf16(v[t]);
+        else reinterpret_cast<_Float16*>(out)[o + t] = (_Float16)v[t];
+    }
+}
+
+// The wave's share of the epilogue: per 32-row block row i of its sub-tile,
+// stage the accumulators in LDS (row stride LDW floats), then read back
+// 4 consecutive columns per lane for all PASSES row groups and their row
+// exponents at once -- one LDS wait per block row instead of two per row
+// group -- and write them with the output type fixed at compile time.
+template <int OUT, int TM, int TN, int WM, int WN, int LDW>
+__device__ __forceinline__ void epilogue_store(const f32x16 (&acc)[TM][TN], float* ws, const int (&rexp_l)[WM / 64],
+                                               const int (&cexp)[4], const float (&cbias)[4], void* out, int64_t ldo,
+                                               int M, int N, int row0, int gcol, bool vec, int lane) {
+    constexpr int LANES_PER_ROW = WN / 4;
+    constexpr int ROWS_PER_PASS = 64 / LANES_PER_ROW;
+    constexpr int PASSES = 32 / ROWS_PER_PASS;
+    const int fr = lane & 31, fh = lane >> 5;
+    const int c4 = (lane % LANES_PER_ROW) * 4;
+    const int rsub = lane / LANES_PER_ROW;
+    const bool full = vec && gcol + 3 < N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                ws[((r >> 2) * 8 + (r & 3) + fh * 4) * LDW + j * 32 + fr] = acc[i][j][r];
+        float4 q[PASSES];
+        int rx[PASSES];
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int lr = p * ROWS_PER_PASS + rsub;
+            q[p] = *reinterpret_cast<const float4*>(ws + lr * LDW + c4);
+            // row i*32 + lr of the wave tile: register i/2 of lane (i%2)*32 + lr
+            rx[p] = __shfl(rexp_l[i / 2], (i % 2) * 32 + lr, 64);
+        }
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int grow = row0 + i * 32 + p * ROWS_PER_PASS + rsub;
+            if (grow < M && gcol < N) {
+                float v[4] = {__builtin_amdgcn_ldexpf(q[p].x, rx[p] + cexp[0]) + cbias[0],
+                              __builtin_amdgcn_ldexpf(q[p].y, rx[p] + cexp[1]) + cbias[1],
+                              __builtin_amdgcn_ldexpf(q[p].z, rx[p] + cexp[2]) + cbias[2],
+                              __builtin_amdgcn_ldexpf(q[p].w, rx[p] + cexp[3]) + cbias[3]};
+                store4t<OUT>(out, ldo, N, grow, gcol, v, full);
+            }
+        }
     }
 }
 
@@ -224,6 +303,15 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
         b_goff[i] = (int)((int64_t)(n0 + row) * g.ldb * 2) + ((lslot ^ swz_key<BK>(row)) << 4);
         b_loff[i] = BM * RB + (wave + NW * i) * 1024;
     }
+    // split-K: this workgroup's range of K-steps (k_iters counts 64-half steps)
+    static_assert(kGemmK % BK == 0, "K-slab must divide the padding unit");
+    const int per = g.k_iters * (kGemmK / BK);
+    const int kbeg = blockIdx.y * per;
+    const int KT = min(per, g.Kp / BK - kbeg);
+#pragma unroll
+    for (int i = 0; i < A_INST; ++i) a_goff[i] += kbeg * RB;
+#pragma unroll
+    for (int i = 0; i < B_INST; ++i) b_goff[i] += kbeg * RB;
     auto lds_ptr = [](char* p) { return (__attribute__((address_space(3))) void*)p; };
 
     f32x16 acc[TM][TN];
@@ -234,7 +322,6 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int KT = g.Kp / BK;
     // prologue: slabs 0 .. STAGES-2
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s) {
@@ -294,16 +381,13 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     // order, so no further barrier is needed.
     constexpr int LDW = WN + 4;
     constexpr int LANES_PER_ROW = WN / 4;
-    constexpr int ROWS_PER_PASS = 64 / LANES_PER_ROW;
     static_assert(NW * 32 * LDW * 4 <= STAGES * SLAB, "epilogue staging must fit in the slab LDS");
-    static_assert(64 % LANES_PER_ROW == 0, "wave tile width");
+    static_assert(64 % LANES_PER_ROW == 0 && 32 % (64 / LANES_PER_ROW) == 0, "wave tile width");
     wait_vmcnt<0>();
     __syncthreads();
     float* ws = reinterpret_cast<float*>(smem) + wave * (32 * LDW);
     const int gexp = g.glob_exp ? (*g.glob_exp == INT_MIN ? 0 : *g.glob_exp + g.glob_add) : 0;
-    const int c4 = (lane % LANES_PER_ROW) * 4;
-    const int rsub = lane / LANES_PER_ROW;
-    const int gcol = n0 + wn * WN + c4;
+    const int gcol = n0 + wn * WN + (lane % LANES_PER_ROW) * 4;
     int cexp[4];
     float cbias[4];
 #pragma unroll
@@ -312,34 +396,36 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
         cexp[t] = gexp + ((g.col_exp && in) ? g.col_exp[gcol + t] : 0);
         cbias[t] = (g.bias && in) ? g.bias[gcol + t] : 0.0f;
     }
-    const int esize = g.out_dtype == AXS6_F32 ? 4 : 2;
-    const bool vec = (g.ldo % 4 == 0) && ((uintptr_t)g.out % (4 * esize) == 0);
+    // Row exponents of the wave's WM rows, WM/64 per lane, loaded once: a load
+    // per store pass would sit behind the previous pass's stores (the output
+    // may alias row_exp as far as the compiler knows) and pay a full memory
+    // latency each time -- ~15 us per launch, all of a small GEMM's runtime.
+    constexpr int RPL = WM / 64;                      // row exponents held per lane
+    static_assert(WM % 64 == 0, "wave tile height");
+    int rexp_l[RPL];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                ws[((r >> 2) * 8 + (r & 3) + fh * 4) * LDW + j * 32 + fr] = acc[i][j][r];
-#pragma unroll
-        for (int rr = 0; rr < 32; rr += ROWS_PER_PASS) {
-            const int lr = rr + rsub;
-            const int grow = m0 + wm * WM + i * 32 + lr;
-            const float* src = ws + lr * LDW + c4;
-            float v[4] = {src[0], src[1], src[2], src[3]};
-            if (grow < g.M && gcol < g.N) {
-                const int rexp = g.row_exp ? g.row_exp[grow] : 0;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) v[t] = __builtin_amdgcn_ldexpf(v[t], rexp + cexp[t]) + cbias[t];
-                store4(g, grow, gcol, v, vec);
-            }
-        }
+    for (int q = 0; q < RPL; ++q) {
+        const int grow = m0 + wm * WM + q * 64 + lane;
+        rexp_l[q] = (g.row_exp && grow < g.M) ? g.row_exp[grow] : 0;
     }
+    const int esize = g.out_dtype == AXS6_F32 ? 4 : 2;
+    void* const out = reinterpret_cast<char*>(g.out) + (int64_t)blockIdx.y * g.split_stride * esize;
+    const bool vec = (g.ldo % 4 == 0) && ((uintptr_t)out % (4 * esize) == 0);
+    const int row0 = m0 + wm * WM;
+    if (g.out_dtype == AXS6_F32)
+        epilogue_store<AXS6_F32, TM, TN, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+                                                      vec, lane);
+    else if (g.out_dtype == AXS6_BF16)
+        epilogue_store<AXS6_BF16, TM, TN, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+                                                       vec, lane);
+    else
+        epilogue_store<AXS6_F16, TM, TN, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+                                                      vec, lane);
 #endif
 }
 
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED>
-int run_gemm_lds(const GemmK& k, hipStream_t st) {
+int run_gemm_lds(const GemmK& k, int splits, hipStream_t st) {
     const int tiles = ((k.M + BM - 1) / BM) * ((k.N + BN - 1) / BN);
     const size_t lds = (size_t)STAGES * (BM + BN) * BK * 2;
     static bool attr_set = false;
@@ -348,26 +434,116 @@ int run_gemm_lds(const GemmK& k, hipStream_t st) {
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         attr_set = true;
     }
-    gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED><<<dim3((unsigned)tiles), WGM * WGN * 64, lds, st>>>(k);
+    gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED>
+        <<<dim3((unsigned)tiles, (unsigned)splits), WGM * WGN * 64, lds, st>>>(k);
     return check_launch("gemm_f16_lds");
 }
 
-// Launch configuration; AXS6_GEMM_CFG selects one for launch-shape sweeps
-// (BMxBN tile / K-slab / LDS stages / waves / schedule variant of mma_step):
+// Split-K finish: out[m, n] = ldexp(sum_z partial[z, m, n], row_exp[m] +
+// col_exp[n] + glob) + bias[n], the splits summed in order z = 0, 1, ... (the
+// result depends on the split count, never on scheduling).  Four columns per
+// thread; partial rows are N floats long.
+struct SplitReduceK {
+    const float* partial; int splits; int64_t stride; int M; int N;
+    const int32_t* row_exp; const int32_t* col_exp; const int32_t* glob_exp; int glob_add;
+    const float* bias; void* out; int64_t ldo; int out_dtype;
+};
+
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(SplitReduceK k) {
+    const int n4 = (k.N + 3) / 4;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)k.M * n4) return;
+    const int row = (int)(idx / n4);
+    const int col = (int)(idx - (int64_t)row * n4) * 4;
+    const bool full = col + 3 < k.N && k.N % 4 == 0;
+    const int64_t o = (int64_t)row * k.N + col;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (full) {
+        // 8 loads in flight per thread; the additions stay in split order
+        int z = 0;
+        for (; z + 8 <= k.splits; z += 8) {
+            float4 q[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) q[u] = *reinterpret_cast<const float4*>(k.partial + (z + u) * k.stride + o);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) { v[0] += q[u].x; v[1] += q[u].y; v[2] += q[u].z; v[3] += q[u].w; }
+        }
+        for (; z < k.splits; ++z) {
+            const float4 q = *reinterpret_cast<const float4*>(k.partial + z * k.stride + o);
+            v[0] += q.x; v[1] += q.y; v[2] += q.z; v[3] += q.w;
+        }
+    } else {
+        for (int z = 0; z < k.splits; ++z)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                if (col + t < k.N) v[t] += k.partial[z * k.stride + o + t];
+    }
+    const int gexp = k.glob_exp ? (*k.glob_exp == INT_MIN ? 0 : *k.glob_exp + k.glob_add) : 0;
+    const int rexp = gexp + (k.row_exp ? k.row_exp[row] : 0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        if (col + t >= k.N) break;
+        v[t] = __builtin_amdgcn_ldexpf(v[t], rexp + (k.col_exp ? k.col_exp[col + t] : 0)) +
+               (k.bias ? k.bias[col + t] : 0.0f);
+    }
+    const int esize = k.out_dtype == AXS6_F32 ? 4 : 2;
+    const bool vec = (k.ldo % 4 == 0) && ((uintptr_t)k.out % (4 * esize) == 0);
+    store4(k.out, k.ldo, k.N, k.out_dtype, row, col, v, vec);
+}
+
+// Launch configurations (BMxBN tile / K-slab / LDS stages / waves /
+// schedule variant of mma_step):
 //   0: 256x256 / 64 / 2 / 8 / 2      1: 256x256 / 32 / 4 / 8 / 2
 //   2: 256x256 / 32 / 3 / 8 / 2      3: 256x256 / 32 / 4 / 8 / 0
 //   4: 256x256 / 32 / 4 / 4 / 2      5: 256x256 / 32 / 4 / 8 / 3
 //   6: 256x256 / 64 / 2 / 8 / 0      7: 256x128 / 64 / 3 / 8 / 2
-int gemm_cfg() {
+//   8: 128x128 / 64 / 2 / 4 / 2
+// Default: 0, or 8 when the 256x256 tiles do not cover the 256 CUs once.
+// The epilogue of a tile (LDS staging, exponent scaling, stores) costs a
+// fixed ~7 us per 256x256 f32 tile and CU, all of a short-K GEMM's runtime
+// when 32 CUs carry it; 128x128 tiles spread it over 4x the CUs, two
+// workgroups sharing a CU.  AXS6_GEMM_CFG=<n> forces a configuration for
+// launch-shape sweeps.
+constexpr int kCfgSmall = 8;
+
+int gemm_cfg_env() {
     static int v = [] {
         const char* s = getenv("AXS6_GEMM_CFG");
         int n = s ? atoi(s) : -1;
-        return (n >= 0 && n <= 7) ? n : 0;
+        return (n >= 0 && n <= 8) ? n : -1;
     }();
     return v;
 }
 
+int64_t tiles_of(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+
+int pick_cfg(int64_t M, int64_t N) {
+    const int env = gemm_cfg_env();
+    if (env >= 0) return env;
+    return tiles_of(M, N, 256, 256) < 256 ? kCfgSmall : 0;
+}
+
 }  // namespace
+
+int gemm_split_count(int64_t M, int64_t N, int64_t Kp) {
+    // split launches use configuration 0 or kCfgSmall (both 64-half K-slabs)
+    const bool small = pick_cfg(M, N) == kCfgSmall;
+    const int64_t tiles = small ? tiles_of(M, N, 128, 128) : tiles_of(M, N, 256, 256);
+    const int64_t iters = Kp / kGemmK;
+    if (tiles >= 64 || iters < 8) return 1;
+    int64_t s = iters / 4;                                   // at least 4 K-steps per split
+    s = s < 256 / tiles ? s : 256 / tiles;                   // about one workgroup per CU
+    const int64_t cap = ((int64_t)4 << 20) / (M * N);       // partials <= 16 MiB
+    s = s < cap ? s : cap;
+    if (s < 2) return 1;
+    const int64_t per = (iters + s - 1) / s;       // no empty split
+    return (int)((iters + per - 1) / per);
+}
+
+size_t gemm_split_bytes(int64_t M, int64_t N, int64_t Kp) {
+    const int s = gemm_split_count(M, N, Kp);
+    return s > 1 ? (size_t)s * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
 
 int launch_gemm_f16(const GemmArgs& a, hipStream_t st) {
     if (a.M == 0 || a.N == 0) return AXS6_OK;
@@ -380,18 +556,39 @@ int launch_gemm_f16(const GemmArgs& a, hipStream_t st) {
         return fail(AXS6_ERR_UNSUPPORTED, "gemm: operand larger than 2 GiB");
     if (a.M > INT_MAX || a.N > INT_MAX || a.Kp > INT_MAX)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: dimension exceeds int32");
-    GemmK k{a.A, a.lda, a.B, a.ldb, (int)a.M, (int)a.N, (int)a.Kp, a.row_exp, a.col_exp, a.glob_exp,
-            a.glob_add, a.bias, a.out, a.ldo, a.out_dtype};
-    switch (gemm_cfg()) {
-        case 1: return run_gemm_lds<256, 256, 32, 4, 2, 4, 2>(k, st);
-        case 2: return run_gemm_lds<256, 256, 32, 3, 2, 4, 2>(k, st);
-        case 3: return run_gemm_lds<256, 256, 32, 4, 2, 4, 0>(k, st);
-        case 4: return run_gemm_lds<256, 256, 32, 4, 2, 2, 2>(k, st);
-        case 5: return run_gemm_lds<256, 256, 32, 4, 2, 4, 3>(k, st);
-        case 6: return run_gemm_lds<256, 256, 64, 2, 2, 4, 0>(k, st);
-        case 7: return run_gemm_lds<256, 128, 64, 3, 4, 2, 2>(k, st);
-        default: return run_gemm_lds<256, 256, 64, 2, 2, 4, 2>(k, st);
+    const int iters = (int)(a.Kp / kGemmK);
+    int splits = 1, per = iters;
+    if (a.split_partial) {
+        splits = gemm_split_count(a.M, a.N, a.Kp);
+        per = (iters + splits - 1) / splits;
+        if (a.split_bytes < gemm_split_bytes(a.M, a.N, a.Kp))
+            return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: split-K buffer of %zu bytes, need %zu", a.split_bytes,
+                        gemm_split_bytes(a.M, a.N, a.Kp));
     }
+    const bool split = splits > 1;
+    GemmK k{a.A, a.lda, a.B, a.ldb, (int)a.M, (int)a.N, (int)a.Kp,
+            split ? nullptr : a.row_exp, split ? nullptr : a.col_exp, split ? nullptr : a.glob_exp, a.glob_add,
+            split ? nullptr : a.bias, split ? (void*)a.split_partial : a.out, split ? a.N : a.ldo,
+            split ? (int)AXS6_F32 : a.out_dtype, per, split ? a.M * a.N : 0};
+    int rc;
+    const int cfg = pick_cfg(a.M, a.N);
+    switch (split ? (cfg == kCfgSmall ? kCfgSmall : 0) : cfg) {
+        case 1: rc = run_gemm_lds<256, 256, 32, 4, 2, 4, 2>(k, splits, st); break;
+        case 2: rc = run_gemm_lds<256, 256, 32, 3, 2, 4, 2>(k, splits, st); break;
+        case 3: rc = run_gemm_lds<256, 256, 32, 4, 2, 4, 0>(k, splits, st); break;
+        case 4: rc = run_gemm_lds<256, 256, 32, 4, 2, 2, 2>(k, splits, st); break;
+        case 5: rc = run_gemm_lds<256, 256, 32, 4, 2, 4, 3>(k, splits, st); break;
+        case 6: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 0>(k, splits, st); break;
+        case 7: rc = run_gemm_lds<256, 128, 64, 3, 4, 2, 2>(k, splits, st); break;
+        case kCfgSmall: rc = run_gemm_lds<128, 128, 64, 2, 2, 2, 2>(k, splits, st); break;
+        default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2>(k, splits, st); break;
+    }
+    if (rc || !split) return rc;
+    SplitReduceK r{a.split_partial, splits, a.M * a.N, (int)a.M, (int)a.N, a.row_exp, a.col_exp, a.glob_exp,
+                   a.glob_add, a.bias, a.out, a.ldo, a.out_dtype};
+    const int64_t threads = a.M * ((a.N + 3) / 4);
+    splitk_reduce_kernel<<<dim3((unsigned)((threads + 255) / 256)), 256, 0, st>>>(r);
+    return check_launch("gemm_splitk_reduce");
 }
 
 }  // namespace axs6

@@ -17,6 +17,7 @@ namespace axs6 {
 struct PackRowsArgs {
     const void* x; int dtype; int64_t rows; int64_t cols; int block;
     bool fake_quant; bool stochastic; uint64_t seed; uint64_t offset;
+    const uint64_t* seed_dev;       // nullable: added to seed when the kernel runs
     const int32_t* colx;            // nullable
     _Float16* out; int64_t ld_out; int64_t cols_pad;
     int32_t* s_out;                 // [rows]
@@ -40,6 +41,7 @@ int launch_pack_rows2(const PackRowsArgs& a, const PackRowsArgs& b, const Device
 struct PackTArgs {
     const void* x; int dtype; int64_t rows; int64_t cols; int block;
     bool fake_quant; bool stochastic; uint64_t seed; uint64_t offset;
+    const uint64_t* seed_dev;       // nullable
     const int32_t* rowx;            // nullable (0)
     const int32_t* gmax;            // device scalar, nullable
     _Float16* out; int64_t ld_out;  // out nullable
@@ -79,6 +81,10 @@ int launch_init_gmax(int32_t* p, hipStream_t st);
 
 // C[M, N] = epilogue(A[M, Kp] . B[N, Kp]^T); fp16 operands, fp32 accumulate.
 // Epilogue: v = ldexp(acc, row_exp[m] + col_exp[n] + (glob ? *glob + glob_add : 0)) + bias[n].
+// With split_partial (device memory of split_bytes >= gemm_split_bytes(M, N,
+// Kp)), a GEMM with few output tiles and a long contraction splits K over
+// gemm_split_count(M, N, Kp) workgroups per tile, writing fp32 partial tiles
+// that a second kernel sums in a fixed order before the epilogue.
 struct GemmArgs {
     const _Float16* A; int64_t lda; const _Float16* B; int64_t ldb;
     int64_t M; int64_t N; int64_t Kp;
@@ -86,8 +92,11 @@ struct GemmArgs {
     const int32_t* glob_exp; int32_t glob_add;
     const float* bias;
     void* out; int64_t ldo; int out_dtype;
+    float* split_partial = nullptr; size_t split_bytes = 0;
 };
 int launch_gemm_f16(const GemmArgs& g, hipStream_t st);
+int gemm_split_count(int64_t M, int64_t N, int64_t Kp);
+size_t gemm_split_bytes(int64_t M, int64_t N, int64_t Kp);
 
 constexpr int64_t kGemmK = 64;   // contraction padding unit
 inline int64_t pad_to(int64_t v, int64_t m) { return (v + m - 1) / m * m; }

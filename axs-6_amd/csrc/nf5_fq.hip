@@ -57,8 +57,9 @@ __global__ __launch_bounds__(kThreads) void fq_vec_kernel(const typename Elem<DT
                                                           typename Elem<DT>::S* y, int64_t n_vec,
                                                           const float* __restrict__ lut_g,
                                                           const uint8_t* __restrict__ band_g,
-                                                          uint64_t key, uint64_t offset) {
+                                                          uint64_t seed, const uint64_t* __restrict__ seed_dev, uint64_t offset) {
     using E = Elem<DT>;
+    const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
     constexpr int V = E::V;
     constexpr int G = BS / V;
     static_assert(G >= 1 && G <= 8, "group size");
@@ -123,8 +124,9 @@ __global__ __launch_bounds__(kThreads) void fq_scalar_kernel(const typename Elem
                                                              int64_t cols, int64_t nblk,
                                                              const float* __restrict__ lut_g,
                                                              const uint8_t* __restrict__ band_g,
-                                                             uint64_t key, uint64_t offset) {
+                                                             uint64_t seed, const uint64_t* __restrict__ seed_dev, uint64_t offset) {
     using E = Elem<DT>;
+    const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
     stage_tables(lut_s, band_w, lut_g, band_g);
@@ -163,9 +165,10 @@ template <int DT, int BS, bool STOCH>
 __global__ __launch_bounds__(kThreads) void quantize_kernel(
     const typename Elem<DT>::S* x, int64_t rows, int64_t cols, int64_t nblk,
     const float* __restrict__ lut_g, const uint8_t* __restrict__ band_g,
-    const uint8_t* __restrict__ rev_g, uint64_t key, uint64_t offset, uint8_t* __restrict__ exps,
+    const uint8_t* __restrict__ rev_g, uint64_t seed, const uint64_t* __restrict__ seed_dev, uint64_t offset, uint8_t* __restrict__ exps,
     uint8_t* __restrict__ codes, uint8_t* __restrict__ signs, typename Elem<DT>::S* fq) {
     using E = Elem<DT>;
+    const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
     __shared__ uint8_t rev_s[kLutSize];
@@ -271,7 +274,7 @@ int64_t capped_grid(int64_t work_items, int64_t per_wg) {
 }
 
 template <int DT, int BS>
-void launch_fq_typed(const void* x, void* y, int64_t rows, int64_t cols, bool stochastic, uint64_t seed,
+void launch_fq_typed(const void* x, void* y, int64_t rows, int64_t cols, bool stochastic, uint64_t seed, const uint64_t* seed_dev,
                      uint64_t offset, const DeviceTables& t, hipStream_t st) {
     using S = typename Elem<DT>::S;
     constexpr int V = Elem<DT>::V;
@@ -280,47 +283,47 @@ void launch_fq_typed(const void* x, void* y, int64_t rows, int64_t cols, bool st
         const int64_t n_vec = rows * cols / V;
         const dim3 grid((unsigned)capped_grid(n_vec, (int64_t)kThreads * kUnroll));
         if (stochastic)
-            fq_vec_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, dither_key(seed), offset);
+            fq_vec_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, seed, seed_dev, offset);
         else
-            fq_vec_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, dither_key(seed), offset);
+            fq_vec_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, seed, seed_dev, offset);
     } else {
         const int64_t nblk = (cols + BS - 1) / BS;
         const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));
         if (stochastic)
-            fq_scalar_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, dither_key(seed), offset);
+            fq_scalar_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, seed, seed_dev, offset);
         else
-            fq_scalar_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, dither_key(seed), offset);
+            fq_scalar_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, seed, seed_dev, offset);
     }
 }
 
 template <int DT>
-void launch_fq(const void* x, void* y, int64_t rows, int64_t cols, int bs, bool stochastic, uint64_t seed,
+void launch_fq(const void* x, void* y, int64_t rows, int64_t cols, int bs, bool stochastic, uint64_t seed, const uint64_t* seed_dev,
                uint64_t offset, const DeviceTables& t, hipStream_t st) {
-    if (bs == 8) launch_fq_typed<DT, 8>(x, y, rows, cols, stochastic, seed, offset, t, st);
-    else if (bs == 16) launch_fq_typed<DT, 16>(x, y, rows, cols, stochastic, seed, offset, t, st);
-    else launch_fq_typed<DT, 32>(x, y, rows, cols, stochastic, seed, offset, t, st);
+    if (bs == 8) launch_fq_typed<DT, 8>(x, y, rows, cols, stochastic, seed, seed_dev, offset, t, st);
+    else if (bs == 16) launch_fq_typed<DT, 16>(x, y, rows, cols, stochastic, seed, seed_dev, offset, t, st);
+    else launch_fq_typed<DT, 32>(x, y, rows, cols, stochastic, seed, seed_dev, offset, t, st);
 }
 
 template <int DT, int BS>
-void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochastic, uint64_t seed,
+void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochastic, uint64_t seed, const uint64_t* seed_dev,
                         uint64_t offset, uint8_t* exps, uint8_t* codes, uint8_t* signs, void* fq,
                         const DeviceTables& t, hipStream_t st) {
     using S = typename Elem<DT>::S;
     const int64_t nblk = (cols + BS - 1) / BS;
     const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));
     if (stochastic)
-        quantize_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, dither_key(seed), offset, exps, codes, signs, (S*)fq);
+        quantize_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, seed, seed_dev, offset, exps, codes, signs, (S*)fq);
     else
-        quantize_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, dither_key(seed), offset, exps, codes, signs, (S*)fq);
+        quantize_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, seed, seed_dev, offset, exps, codes, signs, (S*)fq);
 }
 
 template <int DT>
-void launch_quant(const void* x, int64_t rows, int64_t cols, int bs, bool stochastic, uint64_t seed,
+void launch_quant(const void* x, int64_t rows, int64_t cols, int bs, bool stochastic, uint64_t seed, const uint64_t* seed_dev,
                   uint64_t offset, uint8_t* exps, uint8_t* codes, uint8_t* signs, void* fq,
                   const DeviceTables& t, hipStream_t st) {
-    if (bs == 8) launch_quant_typed<DT, 8>(x, rows, cols, stochastic, seed, offset, exps, codes, signs, fq, t, st);
-    else if (bs == 16) launch_quant_typed<DT, 16>(x, rows, cols, stochastic, seed, offset, exps, codes, signs, fq, t, st);
-    else launch_quant_typed<DT, 32>(x, rows, cols, stochastic, seed, offset, exps, codes, signs, fq, t, st);
+    if (bs == 8) launch_quant_typed<DT, 8>(x, rows, cols, stochastic, seed, seed_dev, offset, exps, codes, signs, fq, t, st);
+    else if (bs == 16) launch_quant_typed<DT, 16>(x, rows, cols, stochastic, seed, seed_dev, offset, exps, codes, signs, fq, t, st);
+    else launch_quant_typed<DT, 32>(x, rows, cols, stochastic, seed, seed_dev, offset, exps, codes, signs, fq, t, st);
 }
 
 int check_shape(const char* fn, int64_t rows, int64_t cols, int bs) {
@@ -338,7 +341,7 @@ using namespace axs6;
 
 extern "C" int axs6_nf5_fake_quantize(const void* x, void* y, int32_t dtype, int64_t rows, int64_t cols,
                                       int32_t block_size, int32_t stochastic, uint64_t seed,
-                                      uint64_t offset, void* stream) {
+                                      uint64_t offset, const uint64_t* seed_dev, void* stream) {
     const char* fn = "axs6_nf5_fake_quantize";
     if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
     int rc = check_shape(fn, rows, cols, block_size);
@@ -348,15 +351,15 @@ extern "C" int axs6_nf5_fake_quantize(const void* x, void* y, int32_t dtype, int
     DeviceTables t;
     if ((rc = device_tables(&t))) return rc;
     hipStream_t st = (hipStream_t)stream;
-    if (dtype == AXS6_F32) launch_fq<AXS6_F32>(x, y, rows, cols, block_size, stochastic != 0, seed, offset, t, st);
-    else if (dtype == AXS6_BF16) launch_fq<AXS6_BF16>(x, y, rows, cols, block_size, stochastic != 0, seed, offset, t, st);
-    else launch_fq<AXS6_F16>(x, y, rows, cols, block_size, stochastic != 0, seed, offset, t, st);
+    if (dtype == AXS6_F32) launch_fq<AXS6_F32>(x, y, rows, cols, block_size, stochastic != 0, seed, seed_dev, offset, t, st);
+    else if (dtype == AXS6_BF16) launch_fq<AXS6_BF16>(x, y, rows, cols, block_size, stochastic != 0, seed, seed_dev, offset, t, st);
+    else launch_fq<AXS6_F16>(x, y, rows, cols, block_size, stochastic != 0, seed, seed_dev, offset, t, st);
     return check_launch(fn);
 }
 
 extern "C" int axs6_nf5_quantize(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
                                  int32_t stochastic, uint64_t seed, uint64_t offset, uint8_t* exponents,
-                                 uint8_t* codes, uint8_t* signs, void* fq, void* stream) {
+                                 uint8_t* codes, uint8_t* signs, void* fq, const uint64_t* seed_dev, void* stream) {
     const char* fn = "axs6_nf5_quantize";
     if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
     int rc = check_shape(fn, rows, cols, block_size);
@@ -366,9 +369,9 @@ extern "C" int axs6_nf5_quantize(const void* x, int32_t dtype, int64_t rows, int
     DeviceTables t;
     if ((rc = device_tables(&t))) return rc;
     hipStream_t st = (hipStream_t)stream;
-    if (dtype == AXS6_F32) launch_quant<AXS6_F32>(x, rows, cols, block_size, stochastic != 0, seed, offset, exponents, codes, signs, fq, t, st);
-    else if (dtype == AXS6_BF16) launch_quant<AXS6_BF16>(x, rows, cols, block_size, stochastic != 0, seed, offset, exponents, codes, signs, fq, t, st);
-    else launch_quant<AXS6_F16>(x, rows, cols, block_size, stochastic != 0, seed, offset, exponents, codes, signs, fq, t, st);
+    if (dtype == AXS6_F32) launch_quant<AXS6_F32>(x, rows, cols, block_size, stochastic != 0, seed, seed_dev, offset, exponents, codes, signs, fq, t, st);
+    else if (dtype == AXS6_BF16) launch_quant<AXS6_BF16>(x, rows, cols, block_size, stochastic != 0, seed, seed_dev, offset, exponents, codes, signs, fq, t, st);
+    else launch_quant<AXS6_F16>(x, rows, cols, block_size, stochastic != 0, seed, seed_dev, offset, exponents, codes, signs, fq, t, st);
     return check_launch(fn);
 }
 

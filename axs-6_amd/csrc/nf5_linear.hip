@@ -32,7 +32,7 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct BwdLayout {
-    size_t gmax, t, stats, a1, wqt, a2t, xqt, partial, total;
+    size_t gmax, t, stats, a1, wqt, a2t, xqt, partial, splitk, splitk_bytes, total;
 };
 
 BwdLayout bwd_layout(int64_t M, int64_t N, int64_t K, bool dx, bool dw, bool db) {
@@ -48,6 +48,10 @@ BwdLayout bwd_layout(int64_t M, int64_t N, int64_t K, bool dx, bool dw, bool db)
     L.a2t = dw ? take(2 * (size_t)N * Mp) : 0;
     L.xqt = dw ? take(2 * (size_t)Kp * Mp) : 0;
     L.partial = db ? take(sizeof(float) * (size_t)pack_global_chunks(M) * N) : 0;
+    // split-K partial tiles, shared by the dX and dW GEMMs (they run in order)
+    const size_t sx = dx ? gemm_split_bytes(M, K, Np) : 0, sw = dw ? gemm_split_bytes(N, K, Mp) : 0;
+    L.splitk_bytes = sx > sw ? sx : sw;
+    L.splitk = L.splitk_bytes ? take(L.splitk_bytes) : 0;
     L.total = off;
     return L;
 }
@@ -73,7 +77,7 @@ extern "C" int64_t axs6_linear_padded_k(int64_t k) { return pad_to(k, kGemmK); }
 extern "C" int axs6_nf5_pack_rows(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
                                   int32_t mode, uint64_t seed, uint64_t offset, const int32_t* col_exp,
                                   void* out_f16, int64_t ld_out, int64_t cols_pad, int32_t* row_shift,
-                                  void* stream) {
+                                  const uint64_t* seed_dev, void* stream) {
     const char* fn = "axs6_nf5_pack_rows";
     if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
     if (!valid_block(block_size)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: block_size must be 8, 16 or 32", fn);
@@ -84,7 +88,7 @@ extern "C" int axs6_nf5_pack_rows(const void* x, int32_t dtype, int64_t rows, in
     DeviceTables t;
     int rc = device_tables(&t);
     if (rc) return rc;
-    PackRowsArgs a{x, dtype, rows, cols, block_size, mode != 0, mode == 2, seed, offset, col_exp,
+    PackRowsArgs a{x, dtype, rows, cols, block_size, mode != 0, mode == 2, seed, offset, seed_dev, col_exp,
                    (_Float16*)out_f16, ld_out, cols_pad, row_shift, nullptr, nullptr, nullptr};
     return launch_pack_rows(a, t, (hipStream_t)stream);
 }
@@ -116,9 +120,9 @@ extern "C" int axs6_nf5_linear_forward(const void* x, const void* w, const float
     if ((rc = device_tables(&t))) return rc;
     hipStream_t st = (hipStream_t)stream;
     const int64_t Kp = pad_to(K, kGemmK);
-    PackRowsArgs px{x, dtype, M, K, block_size, quantize_input != 0, false, 0, 0, nullptr,
+    PackRowsArgs px{x, dtype, M, K, block_size, quantize_input != 0, false, 0, 0, nullptr, nullptr,
                     (_Float16*)xq_f16, Kp, Kp, x_shift, nullptr, nullptr, nullptr};
-    PackRowsArgs pw{w, dtype, N, K, block_size, true, false, 0, 0, nullptr,
+    PackRowsArgs pw{w, dtype, N, K, block_size, true, false, 0, 0, nullptr, nullptr,
                     (_Float16*)wq_f16, Kp, Kp, w_shift, nullptr, nullptr, nullptr};
     if ((rc = launch_pack_rows2(px, pw, t, st))) return rc;
     GemmArgs g{(const _Float16*)xq_f16, Kp, (const _Float16*)wq_f16, Kp, M, N, Kp, x_shift, w_shift, nullptr, 0,
@@ -136,7 +140,7 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
                                         int32_t block_size, int32_t quantize_grad, uint64_t seed, uint64_t offset,
                                         const void* xq_f16, const int32_t* x_shift, const void* wq_f16,
                                         const int32_t* w_shift, void* dx, float* dw, float* db, void* workspace,
-                                        size_t workspace_bytes, void* stream) {
+                                        size_t workspace_bytes, const uint64_t* seed_dev, void* stream) {
     const char* fn = "axs6_nf5_linear_backward";
     int rc = check_dims(fn, M, N, K, block_size, dtype);
     if (rc) return rc;
@@ -164,7 +168,7 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
         if ((rc = launch_row_stats(s, t, st))) return rc;
     }
     if (need_dx || need_dw || need_db) {
-        PackTArgs p{dy, dtype, M, N, block_size, fq, fq, seed, offset, x_shift, need_dw ? gmax : nullptr,
+        PackTArgs p{dy, dtype, M, N, block_size, fq, fq, seed, offset, seed_dev, x_shift, need_dw ? gmax : nullptr,
                     need_dw ? (_Float16*)(ws + L.a2t) : nullptr, Mp,
                     need_dx ? (_Float16*)(ws + L.a1) : nullptr, Np, w_shift, tshift,
                     need_db ? (float*)(ws + L.partial) : nullptr};
@@ -174,14 +178,15 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
         _Float16* wqt = (_Float16*)(ws + L.wqt);
         if ((rc = launch_transpose_f16((const _Float16*)wq_f16, N, Kp, Kp, wqt, Kp, Np, Np, st))) return rc;
         GemmArgs g{(const _Float16*)(ws + L.a1), Np, wqt, Np, M, K, Np, tshift, nullptr, nullptr, 0, nullptr,
-                   dx, K, dtype};
+                   dx, K, dtype, L.splitk_bytes ? (float*)(ws + L.splitk) : nullptr, L.splitk_bytes};
         if ((rc = launch_gemm_f16(g, st))) return rc;
     }
     if (need_dw) {
         _Float16* a2t = (_Float16*)(ws + L.a2t);
         _Float16* xqt = (_Float16*)(ws + L.xqt);
         if ((rc = launch_transpose_f16((const _Float16*)xq_f16, M, Kp, Kp, xqt, Kp, Mp, Mp, st))) return rc;
-        GemmArgs g{a2t, Mp, xqt, Mp, N, K, Mp, nullptr, nullptr, gmax, -15, nullptr, dw, K, AXS6_F32};
+        GemmArgs g{a2t, Mp, xqt, Mp, N, K, Mp, nullptr, nullptr, gmax, -15, nullptr, dw, K, AXS6_F32,
+                   L.splitk_bytes ? (float*)(ws + L.splitk) : nullptr, L.splitk_bytes};
         if ((rc = launch_gemm_f16(g, st))) return rc;
     }
     if (need_db && (rc = launch_reduce_partials((const float*)(ws + L.partial), pack_global_chunks(M), N, db, st)))

@@ -87,7 +87,7 @@ __device__ __forceinline__ void store_f16(_Float16* p, const float* v, int sh_ba
 
 struct PackRowsK {
     const void* x; int64_t rows; int64_t cols; int block;
-    uint64_t key; uint64_t offset;      // dither key (dither_key of the call's seed)
+    uint64_t seed; const uint64_t* seed_dev; uint64_t offset;   // dither seed (+ *seed_dev when set)
     const int32_t* colx;
     _Float16* out; int64_t ld_out; int64_t cols_pad;
     int32_t* s_out; int32_t* rmax_out;
@@ -117,6 +117,7 @@ __global__ __launch_bounds__(NT) void pack_rows_kernel(PackRowsK k, PackRowsK k2
     for (int64_t R = blockIdx.x; R < total; R += gridDim.x, parity ^= 1) {
         const bool second = R >= k.rows;
         const PackRowsK q = second ? k2 : k;      // by value: field-wise selects, no stack copy
+        const uint64_t key = MODE == kStochastic ? dither_key(q.seed + (q.seed_dev ? *q.seed_dev : 0ull)) : 0ull;
         const int64_t r = second ? R - k.rows : R;
         const int64_t nvec = q.cols / V;
         const int g = q.block / V;
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(NT) void pack_rows_kernel(PackRowsK k, PackRowsK k2
             m = group_umax_rt(m, g);
             const FqScale s = fq_scale(m, band_s);
             if constexpr (MODE != kRaw) {
-                const DitherVec dv = dither_vec(q.key, q.offset + (uint64_t)(r * q.cols + vi * V));
+                const DitherVec dv = dither_vec(key, q.offset + (uint64_t)(r * q.cols + vi * V));
                 float d[V];
 #pragma unroll
                 for (int e = 0; e < V; ++e) d[e] = (MODE == kStochastic) ? dither_step(dv, e) : 0.0f;
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(NT) void pack_rows_kernel(PackRowsK k, PackRowsK k2
 // row groups in order), so the bias gradient is deterministic.
 struct PackTK {
     const void* x; int64_t rows; int64_t cols; int block;
-    uint64_t key; uint64_t offset;
+    uint64_t seed; const uint64_t* seed_dev; uint64_t offset;
     const int32_t* rowx; const int32_t* gmax;
     _Float16* out; int64_t ld_out;
     _Float16* out_r; int64_t ld_r; const int32_t* colx_r; const int32_t* shift_r;
@@ -248,6 +249,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
     const int tid = threadIdx.x;
     const int tc = tid % TPR, tr = tid / TPR;
     const S* xs = reinterpret_cast<const S*>(k.x);
+    const uint64_t key = MODE == kStochastic ? dither_key(k.seed + (k.seed_dev ? *k.seed_dev : 0ull)) : 0ull;
     stage_tables(lut_s, band_w, k.lut, k.band);
     const int gm = k.gmax ? *k.gmax : INT_MIN;
     const int G = (gm == INT_MIN) ? 0 : gm - kF16MaxExp;
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
             m = group_umax<GL>(m);
             if constexpr (MODE != kRaw) {
                 const FqScale s = fq_scale(m, band_s);
-                const DitherVec dv = dither_vec(k.key, k.offset + (uint64_t)(r * k.cols + c));
+                const DitherVec dv = dither_vec(key, k.offset + (uint64_t)(r * k.cols + c));
                 float d[V];
 #pragma unroll
                 for (int e = 0; e < V; ++e) d[e] = (MODE == kStochastic) ? dither_step(dv, e) : 0.0f;
@@ -616,7 +618,7 @@ int check_pack_rows(const PackRowsArgs& a, RowsShape* sh_out) {
 }
 
 PackRowsK to_kernel_args(const PackRowsArgs& a, const DeviceTables& t) {
-    return PackRowsK{a.x, a.rows, a.cols, a.block, dither_key(a.seed), a.offset, a.colx, a.out, a.ld_out, a.cols_pad,
+    return PackRowsK{a.x, a.rows, a.cols, a.block, a.seed, a.seed_dev, a.offset, a.colx, a.out, a.ld_out, a.cols_pad,
                      a.s_out, a.rmax_out, a.rowx, a.gmax, t.lut, t.band};
 }
 
@@ -667,7 +669,7 @@ int launch_pack_t(const PackTArgs& a, const DeviceTables& t, hipStream_t st) {
     if (a.out_r && (a.ld_r % 8 != 0 || (uintptr_t)a.out_r % 16 != 0 || a.ld_r < pad_to(a.cols, kTile) ||
                     !a.shift_r || (a.colx_r && (uintptr_t)a.colx_r % 16 != 0)))
         return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_t: row-major output must be 16-byte aligned and hold the padded columns");
-    PackTK k{a.x, a.rows, a.cols, a.block, dither_key(a.seed), a.offset, a.rowx, a.gmax, a.out, a.ld_out,
+    PackTK k{a.x, a.rows, a.cols, a.block, a.seed, a.seed_dev, a.offset, a.rowx, a.gmax, a.out, a.ld_out,
              a.out_r, a.ld_r, a.colx_r, a.shift_r, a.partial, t.lut, t.band};
     const int64_t ntx = (a.cols + kTile - 1) / kTile, ntiles = ntx * pack_global_chunks(a.rows);
     const int mode = a.fake_quant ? (a.stochastic ? kStochastic : kNearest) : kRaw;

@@ -275,8 +275,9 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
     fp32 master weights, one fixed synthetic batch (tests/minigpt.py).  A step
     is forward + cross-entropy + backward + AdamW through the Python API.
     Reported: ms/step over the steps after `warmup`, the loss curve at a few
-    points, the same for the unquantized fp32 model, and the CPU reference
-    restatement's ms/step over `ref_steps` steps (host cores)."""
+    points, the same with the step recorded in a HIP graph and replayed
+    (graph_ms_per_step), the same for the unquantized fp32 model, and the CPU
+    reference restatement's ms/step over `ref_steps` steps (host cores)."""
     import torch
 
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -286,14 +287,20 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
     torch.manual_seed(5)
     model = minigpt.build_axs(0, "cuda")
     losses, ms = minigpt.train(model, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize)
+    torch.manual_seed(5)
+    g_losses, g_ms = minigpt.train_graphed(minigpt.build_axs(0, "cuda"), x.cuda(), y.cuda(), steps, warmup=3)
     fp32 = minigpt.base_model(0).cuda()
     fp_losses, fp_ms = minigpt.train(fp32, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize)
+    fg_losses, fg_ms = minigpt.train_graphed(minigpt.base_model(0).cuda(), x.cuda(), y.cuda(), steps, warmup=3)
     pts = [0, steps // 4, steps // 2, 3 * steps // 4, steps - 1]
     out = {
         "metric": "MiniGPT AXS-6 training ms/step (config 5)",
         "ms_per_step": round(ms, 3), "steps": steps, "warmup": warmup,
         "loss": {str(i): round(losses[i], 4) for i in pts},
-        "fp32_model": {"ms_per_step": round(fp_ms, 3), "loss": {str(i): round(fp_losses[i], 4) for i in pts}},
+        "graph_ms_per_step": round(g_ms, 3),
+        "graph_loss": {str(i): round(g_losses[i], 4) for i in pts},
+        "fp32_model": {"ms_per_step": round(fp_ms, 3), "graph_ms_per_step": round(fg_ms, 3),
+                       "loss": {str(i): round(fp_losses[i], 4) for i in pts}},
     }
     if ref_steps:
         from oracle import eager_torch  # noqa: F401  (the CPU reference restatement)

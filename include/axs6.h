@@ -18,7 +18,10 @@
  *     element at flat index i from a keyed hash of the counter offset + i
  *     (key = splitmix64 finaliser of seed; a 32-bit multiply-xorshift hash
  *     per element; top 24 bits), so a (seed, offset) pair reproduces a draw
- *     exactly.
+ *     exactly.  The stochastic entry points also take `seed_dev`, a device
+ *     pointer (may be NULL) whose uint64 value, read when the kernel runs, is
+ *     added to `seed`: a call recorded in a HIP graph then draws fresh values
+ *     on every replay when the caller advances that counter.
  *
  * Python binding: axs-6_amd/axs/_lib.py (ctypes).  The reference entry
  * point each call replaces is cited on its declaration.
@@ -68,7 +71,7 @@ int axs6_get_tables(float* codebook, float* lut, uint8_t* reverse_lut, uint8_t* 
  *           reached through accelerated_fake_quantize (axs/unified/backend.py:495). */
 int axs6_nf5_fake_quantize(const void* x, void* y, int32_t dtype, int64_t rows, int64_t cols,
                            int32_t block_size, int32_t stochastic, uint64_t seed,
-                           uint64_t offset, void* stream);
+                           uint64_t offset, const uint64_t* seed_dev, void* stream);
 
 /* NF5 quantize to the AXSTensor fields, optionally also writing FQ(x):
  *   exponents  u8 [rows, nblk]            (nblk = ceil(cols / block_size))
@@ -79,7 +82,7 @@ int axs6_nf5_fake_quantize(const void* x, void* y, int32_t dtype, int64_t rows, 
 int axs6_nf5_quantize(const void* x, int32_t dtype, int64_t rows, int64_t cols,
                       int32_t block_size, int32_t stochastic, uint64_t seed, uint64_t offset,
                       uint8_t* exponents, uint8_t* codes, uint8_t* signs, void* fq,
-                      void* stream);
+                      const uint64_t* seed_dev, void* stream);
 
 /* Inverse of axs6_nf5_quantize: y[rows, cols] f32 = +-codebook[code] * 2^(e-127).
  * Replaces: dequantize_unified (axs/unified/quantize_unified.py:285). */
@@ -141,7 +144,7 @@ int64_t axs6_linear_padded_k(int64_t k);
 int axs6_nf5_pack_rows(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
                        int32_t mode, uint64_t seed, uint64_t offset, const int32_t* col_exp,
                        void* out_f16, int64_t ld_out, int64_t cols_pad, int32_t* row_shift,
-                       void* stream);
+                       const uint64_t* seed_dev, void* stream);
 
 /* out[M, N] = ldexp(A[M, Kp] . B[N, Kp]^T, row_exp[m] + col_exp[n]) + bias[n]
  * with fp16 A, B (16-byte aligned, lda/ldb multiples of 8, Kp % 64 == 0),
@@ -181,7 +184,7 @@ int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M, int64_t N
                              int32_t block_size, int32_t quantize_grad, uint64_t seed, uint64_t offset,
                              const void* xq_f16, const int32_t* x_shift, const void* wq_f16,
                              const int32_t* w_shift, void* dx, float* dw, float* db, void* workspace,
-                             size_t workspace_bytes, void* stream);
+                             size_t workspace_bytes, const uint64_t* seed_dev, void* stream);
 
 #ifdef __cplusplus
 }

@@ -209,10 +209,12 @@ def build_reference(seed: int = 0, quantize_grad: bool = True, c: GPTConfig | No
 # ---- training loop ----------------------------------------------------------
 
 def train(model: nn.Module, x: torch.Tensor, y: torch.Tensor, steps: int, lr: float = 3e-4,
-          warmup: int = 0, sync=None) -> tuple[list[float], float]:
+          warmup: int = 0, sync=None, capturable: bool = False) -> tuple[list[float], float]:
     """AdamW steps on one batch.  Returns (loss per step, ms per timed step).
-    The first ``warmup`` steps are untimed but part of the curve."""
-    opt = torch.optim.AdamW(model.parameters(), lr=lr)
+    The first ``warmup`` steps are untimed but part of the curve.
+    ``capturable`` selects AdamW's device-side step arithmetic (the form a
+    graph-replayed step uses)."""
+    opt = torch.optim.AdamW(model.parameters(), lr=lr, capturable=capturable)
     losses = []
     t0 = None
     for i in range(steps):
@@ -230,6 +232,50 @@ def train(model: nn.Module, x: torch.Tensor, y: torch.Tensor, steps: int, lr: fl
         sync()
     ms = (time.perf_counter() - t0) * 1e3 / max(steps - warmup, 1) if t0 is not None else float("nan")
     return [float(v) for v in losses], ms
+
+
+def train_graphed(model: nn.Module, x: torch.Tensor, y: torch.Tensor, steps: int, lr: float = 3e-4,
+                  warmup: int = 3) -> tuple[list[float], float]:
+    """The same AdamW training, with the step recorded once in a HIP graph and
+    replayed: forward, loss, backward and the optimiser update run as one
+    graph launch (AdamW with capturable state).  The first ``warmup`` steps run
+    eagerly on a side stream (they initialise the optimiser state and the
+    allocator pools) and are part of the loss curve; the replays are timed.
+    Stochastic FQ calls inside the graph read a device counter the library
+    advances after each of them, so every replay draws a fresh dither.
+    Returns (loss per step, ms per replayed step)."""
+    opt = torch.optim.AdamW(model.parameters(), lr=lr, capturable=True)
+
+    def step():
+        logits = model(x)
+        loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), y.reshape(-1))
+        loss.backward()
+        opt.step()
+        return loss
+
+    losses = []
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(warmup):
+            opt.zero_grad(set_to_none=True)
+            losses.append(step().detach().clone())
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    opt.zero_grad(set_to_none=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_loss = step()
+    n = steps - warmup
+    hist = torch.empty(n, device=x.device)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(n):
+        graph.replay()
+        hist[i].copy_(static_loss)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / max(n, 1)
+    return [float(v) for v in losses] + hist.tolist(), ms
 
 
 UNIFORM_LOSS = math.log(256.0)

@@ -85,18 +85,18 @@ def _status(name, *args):
 
 
 def test_invalid_arguments_rejected_without_device():
-    rc, msg = _status("axs6_nf5_fake_quantize", 1, 1, 0, 4, 32, 17, 0, 0, 0, None)
+    rc, msg = _status("axs6_nf5_fake_quantize", 1, 1, 0, 4, 32, 17, 0, 0, 0, None, None)
     assert rc == 1 and "block_size" in msg
-    rc, msg = _status("axs6_nf5_fake_quantize", 1, 1, 9, 4, 32, 32, 0, 0, 0, None)
+    rc, msg = _status("axs6_nf5_fake_quantize", 1, 1, 9, 4, 32, 32, 0, 0, 0, None, None)
     assert rc == 1 and "dtype" in msg
-    rc, msg = _status("axs6_nf5_fake_quantize", 1, 1, 0, -1, 32, 32, 0, 0, 0, None)
+    rc, msg = _status("axs6_nf5_fake_quantize", 1, 1, 0, -1, 32, 32, 0, 0, 0, None, None)
     assert rc == 1 and "negative" in msg
-    rc, msg = _status("axs6_nf5_fake_quantize", None, None, 0, 4, 32, 32, 0, 0, 0, None)
+    rc, msg = _status("axs6_nf5_fake_quantize", None, None, 0, 4, 32, 32, 0, 0, 0, None, None)
     assert rc == 1 and "null" in msg
     # empty tensors are a no-op, not an error
-    rc, _ = _status("axs6_nf5_fake_quantize", None, None, 0, 0, 32, 32, 0, 0, 0, None)
+    rc, _ = _status("axs6_nf5_fake_quantize", None, None, 0, 0, 32, 32, 0, 0, 0, None, None)
     assert rc == 0
-    rc, msg = _status("axs6_nf5_quantize", 1, 0, 4, 32, 12, 0, 0, 0, 1, 1, None, None, None)
+    rc, msg = _status("axs6_nf5_quantize", 1, 0, 4, 32, 12, 0, 0, 0, 1, 1, None, None, None, None)
     assert rc == 1 and "block_size" in msg
     rc, msg = _status("axs6_nf5_dequantize", 1, 1, None, 1, 4, 32, 7, None)
     assert rc == 1
@@ -104,4 +104,4 @@ def test_invalid_arguments_rejected_without_device():
 
 def test_error_raises_runtime_error():
     with pytest.raises(RuntimeError, match="block_size"):
-        _lib.call("axs6_nf5_fake_quantize", 1, 1, 0, 4, 32, 17, 0, 0, 0, None)
+        _lib.call("axs6_nf5_fake_quantize", 1, 1, 0, 4, 32, 17, 0, 0, 0, None, None)

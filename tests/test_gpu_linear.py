@@ -132,7 +132,11 @@ def test_linear_forward_config4_rows(M, K, N):
     assert err < TOL
 
 
-@pytest.mark.parametrize("M,K,N", [(64, 256, 128), (100, 96, 64), (2048, 768, 3072), (2048, 3072, 768)])
+# The last three shapes run split-K GEMMs: dW of one 256x256 tile over 128
+# K-steps (32 splits); dW over a ragged 5000-row contraction (16 uneven
+# splits); dX of one tile over a 4096-wide contraction (16 splits).
+@pytest.mark.parametrize("M,K,N", [(64, 256, 128), (100, 96, 64), (2048, 768, 3072), (2048, 3072, 768),
+                                   (8192, 256, 256), (5000, 160, 96), (256, 256, 4096)])
 @pytest.mark.parametrize("qgrad", [False, True], ids=["exact_dy", "stochastic_dy"])
 def test_linear_backward_vs_oracle(M, K, N, qgrad):
     from axs.unified import hip_linear
