@@ -95,26 +95,32 @@ struct PackRowsK {
     const float* lut; const uint8_t* band;
 };
 
-// Row pack, persistent: workgroup w handles rows w, w + gridDim.x, ... of the
-// concatenation of k's rows and k2's (two operands in one launch; k2 == k and
-// total == k.rows for one).  NT threads hold a row in registers, NV 16-byte
-// vectors each (NT grows with the row length so that NV <= 4 and occupancy
-// stays high); the LUT and band table are staged once per workgroup.
-template <int DT, int MODE, bool COLX, int NV, int NT>
-__global__ __launch_bounds__(NT) void pack_rows_kernel(PackRowsK k, PackRowsK k2, int64_t total) {
+// Row pack: rows of the concatenation of k's rows and k2's (two operands in
+// one launch; k2 == k and total == k.rows for one).  NT threads hold a row in
+// registers, NV 16-byte vectors each (NT grows with the row length so that
+// NV <= 4 and occupancy stays high).  A workgroup holds RPW row groups and
+// handles rows RPW*w + g, RPW*(w + gridDim.x) + g, ...; with NT == 64 a row
+// is one wave and its reductions need no barrier, so short rows run several
+// to a workgroup (RPW > 1 requires NT == 64).  The LUT and band table are
+// staged once per workgroup.
+template <int DT, int MODE, bool COLX, int NV, int NT, int RPW>
+__global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRowsK k2, int64_t total) {
     using E = Elem<DT>;
     using S = typename E::S;
     constexpr int V = E::V;
     constexpr int NW = NT / 64;
+    constexpr bool WAVE_ROW = NT == 64;
+    static_assert(RPW == 1 || WAVE_ROW, "several rows per workgroup need one wave per row");
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
     __shared__ int red[2][2][NW];         // [row parity][tmax, rmax][wave]
     const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x % NT;     // thread within the row group
     stage_tables(lut_s, band_w, k.lut, k.band);
 
     int parity = 0;
-    for (int64_t R = blockIdx.x; R < total; R += gridDim.x, parity ^= 1) {
+    for (int64_t R = (int64_t)blockIdx.x * RPW + threadIdx.x / NT; R < total;
+         R += (int64_t)gridDim.x * RPW, parity ^= 1) {
         const bool second = R >= k.rows;
         const PackRowsK q = second ? k2 : k;      // by value: field-wise selects, no stack copy
         const uint64_t key = MODE == kStochastic ? dither_key(q.seed + (q.seed_dev ? *q.seed_dev : 0ull)) : 0ull;
@@ -176,17 +182,19 @@ __global__ __launch_bounds__(NT) void pack_rows_kernel(PackRowsK k, PackRowsK k2
         }
         if constexpr (!COLX) tmax = rmax;
 
-        // workgroup max of (tmax, rmax); the parity buffer lets the next row's
-        // writes proceed while slower waves still read this row's values
+        // row max of (tmax, rmax); across waves, the parity buffer lets the
+        // next row's writes proceed while slower waves still read this row's
         tmax = wave_max_i32(tmax);
         rmax = wave_max_i32(rmax);
-        if ((tid & 63) == 0) { red[parity][0][tid >> 6] = tmax; red[parity][1][tid >> 6] = rmax; }
-        __syncthreads();
-        tmax = red[parity][0][0]; rmax = red[parity][1][0];
+        if constexpr (!WAVE_ROW) {
+            if ((tid & 63) == 0) { red[parity][0][tid >> 6] = tmax; red[parity][1][tid >> 6] = rmax; }
+            __syncthreads();
+            tmax = red[parity][0][0]; rmax = red[parity][1][0];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) {
-            tmax = red[parity][0][w] > tmax ? red[parity][0][w] : tmax;
-            rmax = red[parity][1][w] > rmax ? red[parity][1][w] : rmax;
+            for (int w = 1; w < NW; ++w) {
+                tmax = red[parity][0][w] > tmax ? red[parity][0][w] : tmax;
+                rmax = red[parity][1][w] > rmax ? red[parity][1][w] : rmax;
+            }
         }
         const int S_row = (tmax == INT_MIN) ? 0 : tmax - kF16MaxExp;
 
@@ -537,7 +545,10 @@ __global__ void init_gmax_kernel(int32_t* p) { *p = INT_MIN; }
 // NV vectors each.
 struct RowsShape { int nt; int nv; };
 inline RowsShape rows_shape(int64_t nvec) {
-    if (nvec <= 256) return {256, 1};
+    // one wave per row, four rows per workgroup (nt 64)
+    if (nvec <= 64) return {64, 1};
+    if (nvec <= 128) return {64, 2};
+    if (nvec <= 256) return {64, 4};
     if (nvec <= 512) return {256, 2};
     if (nvec <= 1024) return {256, 4};
     if (nvec <= 2048) return {512, 4};
@@ -550,16 +561,20 @@ void dispatch_rows_nv(const PackRowsK& k, const PackRowsK& k2, int64_t rows, Row
     // one row per workgroup (the loop in the kernel runs once): independent
     // workgroups overlap better than a persistent loop (measured)
     const dim3 grid((unsigned)rows);
-    if (sh.nt == 1024) {
-        pack_rows_kernel<DT, MODE, COLX, 4, 1024><<<grid, 1024, 0, st>>>(k, k2, rows);
+    if (sh.nt == 64) {
+        constexpr int RPW = 4;
+        const dim3 g4((unsigned)((rows + RPW - 1) / RPW));
+        if (sh.nv == 1) pack_rows_kernel<DT, MODE, COLX, 1, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
+        else if (sh.nv == 2) pack_rows_kernel<DT, MODE, COLX, 2, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
+        else pack_rows_kernel<DT, MODE, COLX, 4, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
+    } else if (sh.nt == 1024) {
+        pack_rows_kernel<DT, MODE, COLX, 4, 1024, 1><<<grid, 1024, 0, st>>>(k, k2, rows);
     } else if (sh.nt == 512) {
-        pack_rows_kernel<DT, MODE, COLX, 4, 512><<<grid, 512, 0, st>>>(k, k2, rows);
-    } else if (sh.nv == 1) {
-        pack_rows_kernel<DT, MODE, COLX, 1, 256><<<grid, 256, 0, st>>>(k, k2, rows);
+        pack_rows_kernel<DT, MODE, COLX, 4, 512, 1><<<grid, 512, 0, st>>>(k, k2, rows);
     } else if (sh.nv == 2) {
-        pack_rows_kernel<DT, MODE, COLX, 2, 256><<<grid, 256, 0, st>>>(k, k2, rows);
+        pack_rows_kernel<DT, MODE, COLX, 2, 256, 1><<<grid, 256, 0, st>>>(k, k2, rows);
     } else {
-        pack_rows_kernel<DT, MODE, COLX, 4, 256><<<grid, 256, 0, st>>>(k, k2, rows);
+        pack_rows_kernel<DT, MODE, COLX, 4, 256, 1><<<grid, 256, 0, st>>>(k, k2, rows);
     }
 }
 
