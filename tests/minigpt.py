@@ -279,3 +279,27 @@ def train_graphed(model: nn.Module, x: torch.Tensor, y: torch.Tensor, steps: int
 
 
 UNIFORM_LOSS = math.log(256.0)
+
+
+if __name__ == "__main__":
+    # `python tests/minigpt.py --steps 15`: the eager AXS training loop on the
+    # GPU (for kernel traces of one training step)
+    import argparse
+    import os
+    import sys
+
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "axs-6_amd"))
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--steps", type=int, default=15)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--graph", action="store_true", help="record the step in a HIP graph and replay it")
+    a = ap.parse_args()
+    xb, yb = batch(1)
+    torch.manual_seed(5)
+    m = build_axs(0, "cuda")
+    if a.graph:
+        losses, ms = train_graphed(m, xb.cuda(), yb.cuda(), a.steps, warmup=a.warmup)
+    else:
+        losses, ms = train(m, xb.cuda(), yb.cuda(), a.steps, warmup=a.warmup, sync=torch.cuda.synchronize)
+    print(f"minigpt {'graph' if a.graph else 'eager'}: {ms:.3f} ms/step over {a.steps - a.warmup} steps, "
+          f"loss {losses[0]:.4f} -> {losses[-1]:.4f}", flush=True)
