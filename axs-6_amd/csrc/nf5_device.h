@@ -228,7 +228,11 @@ __device__ __forceinline__ void fq_vector(float (&f)[V], const FqScale& s, const
             int i = (int)t;
             i = i < 0 ? 0 : (i > kLutMax ? kLutMax : i);   // in range already; keeps the LDS index bounded
             const float mag = lut[i] * s.scale;
-            f[e] = __uint_as_float(ab == 0u ? 0u : (__float_as_uint(mag) ^ (xb & 0x80000000u)));
+            // +0 where x is +-0, else mag with x's sign -- as a mask, not a
+            // select, so the compiler does not branch around the LUT read per
+            // element: (ab + 0x7fffffff) has bit 31 set exactly when ab != 0
+            const uint32_t nz = (uint32_t)((int32_t)(ab + 0x7fffffffu) >> 31);
+            f[e] = __uint_as_float((__float_as_uint(mag) ^ (xb & 0x80000000u)) & nz);
         }
     }
 }
@@ -287,6 +291,11 @@ __device__ __forceinline__ float dither_step(const DitherVec& v, int e) {
     const uint32_t lo = v.lo0 + (uint32_t)e;
     const uint32_t hg = lo < v.lo0 ? v.hg + 0x9E3779B9u : v.hg;
     return dither_from_hash(dither_mix(lo ^ v.klo ^ hg));
+}
+// Counter low word lo with the high-word term kh = klo ^ hg fixed: for a call
+// whose counters offset .. offset + n - 1 share one high word.
+__device__ __forceinline__ float dither_step32(uint32_t lo, uint32_t kh) {
+    return dither_from_hash(dither_mix(lo ^ kh));
 }
 
 // Stages the LUT (and the band table) in LDS; needs at least 256 threads.

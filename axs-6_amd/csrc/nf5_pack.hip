@@ -239,7 +239,9 @@ struct PackTK {
 constexpr int kTile = 64;          // rows and columns of a transpose tile
 constexpr int kTileLd = kTile + 8; // LDS row stride (halves) of the transposed tile
 
-template <int DT, int MODE, int BS>
+// C32: every dither counter offset .. offset + rows*cols - 1 has the same high
+// word (the common case), so the draw needs only the 32-bit low word.
+template <int DT, int MODE, int BS, bool C32>
 __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t ntx, int64_t ntiles) {
     using E = Elem<DT>;
     using S = typename E::S;
@@ -264,6 +266,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
 
     // persistent over tiles; consecutive workgroups take neighbouring column
     // tiles of one 64-row band, so a band of x streams through once
+    const uint32_t kh = (uint32_t)key ^ ((uint32_t)(k.offset >> 32) * 0x9E3779B9u + (uint32_t)(key >> 32));
     for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
         const int64_t ty = t / ntx, tx = t - ty * ntx;
         const int64_t c0 = tx * kTile, r0 = ty * kTile;
@@ -276,6 +279,25 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
             const int64_t r = r0 + tr + RPP * p;
             raw[p] = (cin && r < k.rows) ? *reinterpret_cast<const u32x4*>(xs + r * k.cols + c)
                                          : u32x4{0u, 0u, 0u, 0u};
+        }
+        // per-tile operands of the two outputs, loaded once: the column
+        // exponents of this thread's V columns, the rows' shifts and exponents
+        int cx[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) cx[e] = 0;
+        if (k.out_r && cin && k.colx_r) {
+#pragma unroll
+            for (int h = 0; h < V / 4; ++h) {
+                const u32x4 c4 = *(reinterpret_cast<const u32x4*>(k.colx_r + c) + h);
+                cx[4 * h] = (int)c4.x; cx[4 * h + 1] = (int)c4.y; cx[4 * h + 2] = (int)c4.z; cx[4 * h + 3] = (int)c4.w;
+            }
+        }
+        int shr[PASSES], shx[PASSES];
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int64_t r = r0 + tr + RPP * p;
+            shr[p] = (k.out_r && r < k.rows) ? k.shift_r[r] : 0;
+            shx[p] = (k.rowx && cin && r < k.rows) ? k.rowx[r] - G : -G;
         }
         float colsum[V];
 #pragma unroll
@@ -295,10 +317,19 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
             m = group_umax<GL>(m);
             if constexpr (MODE != kRaw) {
                 const FqScale s = fq_scale(m, band_s);
-                const DitherVec dv = dither_vec(key, k.offset + (uint64_t)(r * k.cols + c));
                 float d[V];
+                if constexpr (MODE == kStochastic && C32) {
+                    const uint32_t lo = (uint32_t)k.offset + (uint32_t)r * (uint32_t)k.cols + (uint32_t)c;
 #pragma unroll
-                for (int e = 0; e < V; ++e) d[e] = (MODE == kStochastic) ? dither_step(dv, e) : 0.0f;
+                    for (int e = 0; e < V; ++e) d[e] = dither_step32(lo + (uint32_t)e, kh);
+                } else if constexpr (MODE == kStochastic) {
+                    const DitherVec dv = dither_vec(key, k.offset + (uint64_t)(r * k.cols + c));
+#pragma unroll
+                    for (int e = 0; e < V; ++e) d[e] = dither_step(dv, e);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < V; ++e) d[e] = 0.0f;
+                }
                 fq_vector<V>(f, s, lut_s, MODE == kStochastic, d);
             }
             const bool live = cin && r < k.rows;
@@ -309,23 +340,15 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
             if (k.out_r && r < k.rows) {
                 // row-major operand: fp16(v * 2^(colx[c] - shift[r])), zeros in the
                 // padding columns cols <= c < 64 * ceil(cols / 64)
-                int cx[V];
-#pragma unroll
-                for (int h = 0; h < V / 4; ++h) {
-                    const u32x4 c4 = (cin && k.colx_r) ? *(reinterpret_cast<const u32x4*>(k.colx_r + c) + h)
-                                                       : u32x4{0u, 0u, 0u, 0u};
-                    cx[4 * h] = (int)c4.x; cx[4 * h + 1] = (int)c4.y; cx[4 * h + 2] = (int)c4.z; cx[4 * h + 3] = (int)c4.w;
-                }
                 float z[V];
 #pragma unroll
                 for (int e = 0; e < V; ++e) z[e] = cin ? f[e] : 0.0f;
-                store_f16<V>(k.out_r + r * k.ld_r + c, z, -k.shift_r[r], cx);
+                store_f16<V>(k.out_r + r * k.ld_r + c, z, -shr[p], cx);
             }
             if (k.out) {
-                const int sh = (live && k.rowx) ? k.rowx[r] - G : -G;
 #pragma unroll
                 for (int e = 0; e < V; ++e) {
-                    const _Float16 h = live ? (_Float16)__builtin_amdgcn_ldexpf(f[e], sh) : (_Float16)0.0f;
+                    const _Float16 h = live ? (_Float16)__builtin_amdgcn_ldexpf(f[e], shx[p]) : (_Float16)0.0f;
                     tile[(tc * V + e) * kTileLd + lr] = __builtin_bit_cast(uint16_t, h);
                 }
             }
@@ -595,9 +618,12 @@ void dispatch_t_bs(const PackTK& k, int mode, int64_t ntx, int64_t ntiles, hipSt
     // one tile per workgroup: independent workgroups overlap their load,
     // compute and store phases better than a persistent loop (measured)
     const dim3 grid((unsigned)ntiles);
-    if (mode == kRaw) pack_t_kernel<DT, kRaw, BS><<<grid, kPackThreads, 0, st>>>(k, ntx, ntiles);
-    else if (mode == kNearest) pack_t_kernel<DT, kNearest, BS><<<grid, kPackThreads, 0, st>>>(k, ntx, ntiles);
-    else pack_t_kernel<DT, kStochastic, BS><<<grid, kPackThreads, 0, st>>>(k, ntx, ntiles);
+    // one high word for every counter of the call: the 32-bit dither path
+    const bool c32 = (k.offset >> 32) == ((k.offset + (uint64_t)(k.rows * k.cols) - 1) >> 32);
+    if (mode == kRaw) pack_t_kernel<DT, kRaw, BS, false><<<grid, kPackThreads, 0, st>>>(k, ntx, ntiles);
+    else if (mode == kNearest) pack_t_kernel<DT, kNearest, BS, false><<<grid, kPackThreads, 0, st>>>(k, ntx, ntiles);
+    else if (c32) pack_t_kernel<DT, kStochastic, BS, true><<<grid, kPackThreads, 0, st>>>(k, ntx, ntiles);
+    else pack_t_kernel<DT, kStochastic, BS, false><<<grid, kPackThreads, 0, st>>>(k, ntx, ntiles);
 }
 
 template <int DT>
