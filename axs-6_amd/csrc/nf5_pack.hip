@@ -102,8 +102,11 @@ struct PackRowsK {
 // handles rows RPW*w + g, RPW*(w + gridDim.x) + g, ...; with NT == 64 a row
 // is one wave and its reductions need no barrier, so short rows run several
 // to a workgroup (RPW > 1 requires NT == 64).  The LUT and band table are
-// staged once per workgroup.
-template <int DT, int MODE, bool COLX, int NV, int NT, int RPW>
+// staged once per workgroup.  With PF, the loads of a workgroup's next row
+// are issued before the current row's reduction, barrier and stores, so a
+// long row's loads stay in flight while the previous row finishes (a row's
+// maximum, and so its stores, wait for the whole row).
+template <int DT, int MODE, bool COLX, int NV, int NT, int RPW, bool PF = false>
 __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRowsK k2, int64_t total) {
     using E = Elem<DT>;
     using S = typename E::S;
@@ -118,9 +121,26 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
     const int tid = threadIdx.x % NT;     // thread within the row group
     stage_tables(lut_s, band_w, k.lut, k.band);
 
+    auto load_row = [&](int64_t RR, u32x4 (&dst)[NV]) {
+        const bool sec = RR >= k.rows;
+        const int64_t cols = sec ? k2.cols : k.cols;
+        const S* xr = reinterpret_cast<const S*>(sec ? k2.x : k.x) + (sec ? RR - k.rows : RR) * cols;
+        const int64_t nv = cols / V;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int64_t vi = tid + (int64_t)NT * j;
+            dst[j] = vi < nv ? *(reinterpret_cast<const u32x4*>(xr) + vi) : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    const int64_t stride = (int64_t)gridDim.x * RPW;
+    u32x4 pre[NV];
+    if constexpr (PF) {
+        const int64_t R0 = (int64_t)blockIdx.x * RPW + threadIdx.x / NT;
+        if (R0 < total) load_row(R0, pre);
+    }
+
     int parity = 0;
-    for (int64_t R = (int64_t)blockIdx.x * RPW + threadIdx.x / NT; R < total;
-         R += (int64_t)gridDim.x * RPW, parity ^= 1) {
+    for (int64_t R = (int64_t)blockIdx.x * RPW + threadIdx.x / NT; R < total; R += stride, parity ^= 1) {
         const bool second = R >= k.rows;
         const PackRowsK q = second ? k2 : k;      // by value: field-wise selects, no stack copy
         const uint64_t key = MODE == kStochastic ? dither_key(q.seed + (q.seed_dev ? *q.seed_dev : 0ull)) : 0ull;
@@ -132,10 +152,17 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
         float f[NV][V];
         int cx[NV][V];
         u32x4 raw[NV];
+        if constexpr (PF) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j) raw[j] = pre[j];
+            if (R + stride < total) load_row(R + stride, pre);   // next row, in flight meanwhile
+        } else {
+            load_row(R, raw);
+        }
+        (void)xr;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int64_t vi = tid + (int64_t)NT * j;
-            raw[j] = vi < nvec ? *(reinterpret_cast<const u32x4*>(xr) + vi) : u32x4{0u, 0u, 0u, 0u};
             if constexpr (COLX) {
                 // V consecutive column exponents: one or two 16-byte loads
 #pragma unroll
@@ -591,9 +618,13 @@ void dispatch_rows_nv(const PackRowsK& k, const PackRowsK& k2, int64_t rows, Row
         else if (sh.nv == 2) pack_rows_kernel<DT, MODE, COLX, 2, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
         else pack_rows_kernel<DT, MODE, COLX, 4, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
     } else if (sh.nt == 1024) {
-        pack_rows_kernel<DT, MODE, COLX, 4, 1024, 1><<<grid, 1024, 0, st>>>(k, k2, rows);
+        // long rows: two rows per workgroup, the second row's loads issued
+        // while the first is reduced and stored
+        const dim3 g2((unsigned)((rows + 1) / 2));
+        pack_rows_kernel<DT, MODE, COLX, 4, 1024, 1, true><<<g2, 1024, 0, st>>>(k, k2, rows);
     } else if (sh.nt == 512) {
-        pack_rows_kernel<DT, MODE, COLX, 4, 512, 1><<<grid, 512, 0, st>>>(k, k2, rows);
+        const dim3 g2((unsigned)((rows + 1) / 2));
+        pack_rows_kernel<DT, MODE, COLX, 4, 512, 1, true><<<g2, 512, 0, st>>>(k, k2, rows);
     } else if (sh.nv == 2) {
         pack_rows_kernel<DT, MODE, COLX, 2, 256, 1><<<grid, 256, 0, st>>>(k, k2, rows);
     } else {

@@ -1,0 +1,119 @@
+"""Bit-level parity of the GEMM operand packing (`axs6_nf5_pack_rows`).
+
+The packed operand of a row r of x is fully determined by the NF5 format:
+    S[r] = max over the row's finite nonzero blocks of e1 - 15   (0 if none),
+    out[r, c] = fp16(v[r, c] * 2^-S[r])   for c < cols,   0 for cols <= c < cols_pad,
+where 2^e1 is the block's FQ scale (e1 = floor_log2(amax) + 1, the
+exponent rule of quantize_unified.py:154-160 restated in the oracle) and v is
+FQ(x) (mode 1, fused_fake_quantize, quantize_unified.py:121-204) or x itself
+(mode 0).  The expected bits are built here from the oracle's FQ values and
+exponents with numpy's correctly rounded float32 ldexp and float16 casts; the
+kernel must match them exactly.  Row widths cover every launch shape of the
+packing kernel (one wave per row, 256/512/1024 threads per row, and the
+two-rows-per-workgroup prefetch of long rows), with odd row counts so a
+workgroup is left with a single row.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+BS = 32
+
+
+def _data(rows: int, cols: int, seed: int) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    x[rng.random((rows, cols)) < 0.01] *= 100.0
+    if rows >= 8:
+        x[1] = 0.0                                  # no finite nonzero block: S = 0
+        x[2] *= np.float32(1e-38)                   # subnormal inputs
+        x[3, ::7] *= np.float32(1e35)               # huge finite blocks: exponents near the top
+        x[4, 5] = np.inf                            # an infinite block (FQ gives NaN/0 there)
+        x[5, 40 % cols] = np.nan                    # a NaN block
+        x[6] = np.float32(2.0 ** -130)              # scale exponents at the bottom
+    return x
+
+
+def _expected(x: np.ndarray, mode: int, cols_pad: int) -> tuple[np.ndarray, np.ndarray]:
+    rows, cols = x.shape
+    v = oracle.fake_quantize(x, BS) if mode == 1 else x.astype(np.float32)
+    a = np.abs(x).reshape(rows, cols // BS, BS)
+    with np.errstate(invalid="ignore"):
+        amax = a.max(axis=2)                        # NaN where the block holds a NaN
+    finite = np.isfinite(amax) & (amax > 0)
+    e1 = oracle.floor_log2(np.where(finite, amax, 1.0)).astype(np.int64) + 1
+    ok = finite & (e1 < 128)                        # 2^e1 finite in float32
+    tmax = np.where(ok, e1, np.iinfo(np.int64).min).max(axis=1)
+    shift = np.where(tmax == np.iinfo(np.int64).min, 0, tmax - 15).astype(np.int32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        scaled = np.ldexp(v.astype(np.float32), (-shift.astype(np.int64))[:, None]).astype(np.float32)
+        packed = np.zeros((rows, cols_pad), np.float16)
+        packed[:, :cols] = scaled.astype(np.float16)
+    return packed, shift
+
+
+def _pack(x: torch.Tensor, mode: int, cols_pad: int):
+    from axs import _lib
+
+    rows, cols = x.shape
+    out = torch.full((rows, cols_pad), float("nan"), dtype=torch.float16, device=DEV)   # padding must be written
+    shift = torch.full((rows,), -12345, dtype=torch.int32, device=DEV)
+    _lib.call("axs6_nf5_pack_rows", x.data_ptr(), _lib.DTYPE_CODE[x.dtype], rows, cols, BS, mode, 0, 0, None,
+              out.data_ptr(), cols_pad, cols_pad, shift.data_ptr(), None, _lib.stream_of(x))
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), shift.cpu().numpy()
+
+
+def _assert_bits(got: np.ndarray, want: np.ndarray, what: str):
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn), f"{what}: NaN positions differ"
+    g = got.view(np.uint16)[~gn]
+    w = want.view(np.uint16)[~wn]
+    bad = np.flatnonzero(g != w)
+    assert bad.size == 0, f"{what}: {bad.size} values differ, first {g[bad[:4]]} vs {w[bad[:4]]}"
+
+
+# f32 row widths: 8, 64, 128 and 256 vectors (one wave per row), 512 and 1024
+# (256 threads), 1536 (512 threads, prefetch), 2752 and 4096 (1024 threads, prefetch)
+@pytest.mark.parametrize("cols", [32, 256, 512, 1024, 2048, 4096, 6144, 11008, 16384])
+@pytest.mark.parametrize("rows", [37, 1])
+def test_pack_rows_f32_bitexact(rows, cols):
+    print(f"[pack_rows f32 {rows}x{cols}]", flush=True)
+    x = _data(rows, cols, cols + rows)
+    cols_pad = (cols + 63) // 64 * 64
+    got, shift = _pack(torch.from_numpy(x).to(DEV), 1, cols_pad)
+    want, wshift = _expected(x, 1, cols_pad)
+    assert np.array_equal(shift, wshift)
+    _assert_bits(got, want, f"f32 {rows}x{cols}")
+
+
+# bf16 widths: 1376 vectors (512 threads, prefetch) and 4096 (1024 threads, prefetch)
+@pytest.mark.parametrize("cols", [256, 11008, 32768])
+def test_pack_rows_bf16_bitexact(cols):
+    print(f"[pack_rows bf16 37x{cols}]", flush=True)
+    xb = torch.from_numpy(_data(37, cols, 5 + cols)).to(torch.bfloat16)
+    x = xb.float().numpy()
+    cols_pad = (cols + 63) // 64 * 64
+    got, shift = _pack(xb.to(DEV), 1, cols_pad)
+    want, wshift = _expected(x, 1, cols_pad)
+    assert np.array_equal(shift, wshift)
+    _assert_bits(got, want, f"bf16 37x{cols}")
+
+
+@pytest.mark.parametrize("cols", [256, 11008])
+def test_pack_rows_raw_mode_bitexact(cols):
+    """Mode 0 (no FQ, the general matmul's operands): the values themselves."""
+    rng = np.random.default_rng(cols)
+    x = (rng.standard_normal((21, cols)) * 3).astype(np.float32)
+    cols_pad = (cols + 63) // 64 * 64
+    got, shift = _pack(torch.from_numpy(x).to(DEV), 0, cols_pad)
+    want, wshift = _expected(x, 0, cols_pad)
+    assert np.array_equal(shift, wshift)
+    _assert_bits(got, want, f"raw 21x{cols}")
