@@ -7,7 +7,9 @@ selection and the bf16 mixed-precision linear.  ``AXS6Linear`` aliases
 (``has_triton``, ``triton_fused_fake_quantize``, ``triton_fused_linear``) as
 aliases of the HIP ones so existing call sites keep working; they run the
 HIP kernels, not Triton.  The training pipeline (``AXSTrainingPipelineUnified``,
-``AmaxEMA``) and the distributed gradient hooks are not part of this package.
+``AmaxEMA``) runs its gradient unscale, overflow check and clipping as one
+fused device pass.  The distributed gradient hooks are not part of this
+package (the NF5 gradient codec is, in ``axs.unified.distributed``).
 """
 from axs.unified.backend import (
     BackendType,
@@ -40,6 +42,7 @@ from axs.unified.modules_unified import (
     AXSMultiheadAttentionUnified,
     convert_to_axs_unified,
 )
+from axs.unified.training_unified import AmaxEMA, AXSTrainingPipelineUnified
 from axs.unified.quantize_unified import (
     FUSED_NF5_LUT,
     NF5_CODEBOOK,
@@ -93,4 +96,6 @@ __all__ = [
     "axs_linear_mixed_precision",
     "convert_to_axs_mixed_precision",
     "estimate_memory_savings",
+    "AXSTrainingPipelineUnified",
+    "AmaxEMA",
 ]

@@ -292,6 +292,7 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
     fp32 = minigpt.base_model(0).cuda()
     fp_losses, fp_ms = minigpt.train(fp32, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize)
     fg_losses, fg_ms = minigpt.train_graphed(minigpt.base_model(0).cuda(), x.cuda(), y.cuda(), steps, warmup=3)
+    pipe = bench_pipeline(minigpt, x, y, steps=min(steps, 100), warmup=warmup)
     pts = [0, steps // 4, steps // 2, 3 * steps // 4, steps - 1]
     out = {
         "metric": "MiniGPT AXS-6 training ms/step (config 5)",
@@ -301,6 +302,7 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
         "graph_loss": {str(i): round(g_losses[i], 4) for i in pts},
         "fp32_model": {"ms_per_step": round(fp_ms, 3), "graph_ms_per_step": round(fg_ms, 3),
                        "loss": {str(i): round(fp_losses[i], 4) for i in pts}},
+        "pipeline": pipe,
     }
     if ref_steps:
         from oracle import eager_torch  # noqa: F401  (the CPU reference restatement)
@@ -312,6 +314,43 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
                                 "steps_timed": ref_steps, "kind": "port",
                                 "loss": {str(i): round(v, 4) for i, v in enumerate(ref_losses)}}
     return out
+
+
+def bench_pipeline(minigpt, x, y, steps: int = 100, warmup: int = 5):
+    """The MiniGPT step through AXSTrainingPipelineUnified (loss scaling,
+    overflow check and clipping in one fused device pass, one host read per
+    step) beside the same step through a restatement of the reference's
+    pipeline (per-parameter unscale, two host-synchronising inf/NaN checks per
+    parameter, clip_grad_norm_; tests/ref_pipeline.py), same model and batch."""
+    import torch
+    import torch.nn.functional as F
+
+    from axs.unified import AXSTrainingPipelineUnified
+    from ref_pipeline import RefPipeline
+
+    xd, yd = x.cuda(), y.cuda()
+
+    def loss_fn(out, inp):
+        return F.cross_entropy(out.reshape(-1, out.shape[-1]), yd.reshape(-1))
+
+    res = {}
+    for name, cls in (("ms_per_step", AXSTrainingPipelineUnified), ("reference_style_ms_per_step", RefPipeline)):
+        torch.manual_seed(5)
+        model = minigpt.build_axs(0, "cuda")
+        opt = torch.optim.AdamW(model.parameters(), lr=3e-4)
+        p = cls(model, opt, max_grad_norm=1.0)
+        for _ in range(warmup):
+            p.training_step(xd, loss_fn)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            r = p.training_step(xd, loss_fn)
+        torch.cuda.synchronize()
+        res[name] = round((time.perf_counter() - t0) * 1e3 / steps, 3)
+        res[name.replace("ms_per_step", "final_loss")] = round(r["loss"], 4)
+    res["steps"] = steps
+    res["param_tensors"] = sum(1 for _ in model.parameters())
+    return res
 
 
 def cpu_baseline_fq(budget_s: float = 12.0):

@@ -186,6 +186,28 @@ int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M, int64_t N
                              const int32_t* w_shift, void* dx, float* dw, float* db, void* workspace,
                              size_t workspace_bytes, const uint64_t* seed_dev, void* stream);
 
+/* ---- training-step glue ----------------------------------------------------
+ * Gradient unscale + overflow check + global-norm clip over a list of
+ * gradient tensors: replaces the per-parameter `grad.div_(loss_scale)`, the
+ * two host-synchronising isinf/isnan reductions per parameter and
+ * `clip_grad_norm_(params, max_norm)` of AXSTrainingPipelineUnified.training_step
+ * (axs/unified/training_unified.py:224-257, _check_overflow :287-292):
+ *   every element g *= fl(1 / loss_scale) (the fp32 reciprocal, rounded to the
+ *   tensor dtype: what torch's grad.div_(loss_scale) computes on the GPU);
+ *   result[0] = sqrt(sum of g^2 over all tensors), summed in a fixed order;
+ *   result[1] = min(max_norm / (result[0] + 1e-6), 1)  (NaN stays NaN);
+ *   result[2] = number of non-finite values after the division;
+ *   with clip != 0, when result[2] == 0 and result[1] < 1: g *= result[1].
+ * grads, numel and dtypes are HOST arrays of `count` entries (device pointers,
+ * element counts, dtype codes; tensors contiguous and element-aligned).
+ * partials: device floats, at least axs6_multi_tensor_workspace(numel, count)
+ * of them; result: 3 device floats.  Asynchronous: no host synchronisation,
+ * no allocation; the caller reads `result` when it needs the values. */
+int64_t axs6_multi_tensor_workspace(const int64_t* numel, int32_t count);
+int axs6_multi_tensor_unscale_clip(void* const* grads, const int64_t* numel, const int32_t* dtypes, int32_t count,
+                                   float loss_scale, float max_norm, int32_t clip, float* partials,
+                                   int64_t partials_len, float* result, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
