@@ -440,43 +440,59 @@ int run_gemm_lds(const GemmK& k, int splits, hipStream_t st) {
 }
 
 // Split-K finish: out[m, n] = ldexp(sum_z partial[z, m, n], row_exp[m] +
-// col_exp[n] + glob) + bias[n], the splits summed in order z = 0, 1, ... (the
-// result depends on the split count, never on scheduling).  Four columns per
-// thread; partial rows are N floats long.
+// col_exp[n] + glob) + bias[n], the splits summed in a fixed order (the
+// result depends on the split count, never on scheduling); partial rows are
+// N floats long.
 struct SplitReduceK {
     const float* partial; int splits; int64_t stride; int M; int N;
     const int32_t* row_exp; const int32_t* col_exp; const int32_t* glob_exp; int glob_add;
     const float* bias; void* out; int64_t ldo; int out_dtype;
 };
 
+// A workgroup takes 64 groups of four output columns; its four waves sum four
+// consecutive ranges of splits (eight loads in flight each), then the ranges
+// are added in order.
+constexpr int kSplitGroups = 64, kSplitRanges = 4;
+
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(SplitReduceK k) {
+    __shared__ float4 part[kSplitRanges][kSplitGroups];
     const int n4 = (k.N + 3) / 4;
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)k.M * n4) return;
-    const int row = (int)(idx / n4);
-    const int col = (int)(idx - (int64_t)row * n4) * 4;
+    const int lg = threadIdx.x % kSplitGroups, q = threadIdx.x / kSplitGroups;
+    const int64_t idx = (int64_t)blockIdx.x * kSplitGroups + lg;
+    const bool live = idx < (int64_t)k.M * n4;
+    const int row = live ? (int)(idx / n4) : 0;
+    const int col = live ? (int)(idx - (int64_t)row * n4) * 4 : 0;
     const bool full = col + 3 < k.N && k.N % 4 == 0;
     const int64_t o = (int64_t)row * k.N + col;
+    const int per = (k.splits + kSplitRanges - 1) / kSplitRanges;
+    const int z0 = q * per, z1 = (z0 + per) < k.splits ? z0 + per : k.splits;
     float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (full) {
-        // 8 loads in flight per thread; the additions stay in split order
-        int z = 0;
-        for (; z + 8 <= k.splits; z += 8) {
-            float4 q[8];
+    if (live && full) {
+        int z = z0;
+        for (; z + 8 <= z1; z += 8) {
+            float4 w[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) q[u] = *reinterpret_cast<const float4*>(k.partial + (z + u) * k.stride + o);
+            for (int u = 0; u < 8; ++u) w[u] = *reinterpret_cast<const float4*>(k.partial + (z + u) * k.stride + o);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) { v[0] += q[u].x; v[1] += q[u].y; v[2] += q[u].z; v[3] += q[u].w; }
+            for (int u = 0; u < 8; ++u) { v[0] += w[u].x; v[1] += w[u].y; v[2] += w[u].z; v[3] += w[u].w; }
         }
-        for (; z < k.splits; ++z) {
-            const float4 q = *reinterpret_cast<const float4*>(k.partial + z * k.stride + o);
-            v[0] += q.x; v[1] += q.y; v[2] += q.z; v[3] += q.w;
+        for (; z < z1; ++z) {
+            const float4 w = *reinterpret_cast<const float4*>(k.partial + z * k.stride + o);
+            v[0] += w.x; v[1] += w.y; v[2] += w.z; v[3] += w.w;
         }
-    } else {
-        for (int z = 0; z < k.splits; ++z)
+    } else if (live) {
+        for (int z = z0; z < z1; ++z)
 #pragma unroll
             for (int t = 0; t < 4; ++t)
                 if (col + t < k.N) v[t] += k.partial[z * k.stride + o + t];
+    }
+    part[q][lg] = make_float4(v[0], v[1], v[2], v[3]);
+    __syncthreads();
+    if (q != 0 || !live) return;
+#pragma unroll
+    for (int r = 1; r < kSplitRanges; ++r) {
+        const float4 w = part[r][lg];
+        v[0] += w.x; v[1] += w.y; v[2] += w.z; v[3] += w.w;
     }
     const int gexp = k.glob_exp ? (*k.glob_exp == INT_MIN ? 0 : *k.glob_exp + k.glob_add) : 0;
     const int rexp = gexp + (k.row_exp ? k.row_exp[row] : 0);
@@ -586,8 +602,8 @@ int launch_gemm_f16(const GemmArgs& a, hipStream_t st) {
     if (rc || !split) return rc;
     SplitReduceK r{a.split_partial, splits, a.M * a.N, (int)a.M, (int)a.N, a.row_exp, a.col_exp, a.glob_exp,
                    a.glob_add, a.bias, a.out, a.ldo, a.out_dtype};
-    const int64_t threads = a.M * ((a.N + 3) / 4);
-    splitk_reduce_kernel<<<dim3((unsigned)((threads + 255) / 256)), 256, 0, st>>>(r);
+    const int64_t groups = a.M * ((a.N + 3) / 4);
+    splitk_reduce_kernel<<<dim3((unsigned)((groups + kSplitGroups - 1) / kSplitGroups)), 256, 0, st>>>(r);
     return check_launch("gemm_splitk_reduce");
 }
 

@@ -530,19 +530,39 @@ __global__ __launch_bounds__(256) void stats_finalize_kernel(const int32_t* __re
 
 // out[c] = sum over chunks k of partial[k, c], in the order k = 0, 1, ...
 // split into 4 consecutive ranges combined in order: deterministic.
+// db[c] = sum of partial[k, c] over the chunks k, in a fixed order: a
+// workgroup takes 16 columns, its 16 thread groups 16 consecutive ranges of
+// chunks (each summed in order, eight loads in flight), then the ranges are
+// added in order.
+constexpr int kRedCols = 16, kRedRanges = 16;
+
 __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ partial, int64_t chunks,
                                                               int64_t cols, float* __restrict__ out) {
-    __shared__ float part[4][64];
-    const int lc = threadIdx.x & 63, q = threadIdx.x >> 6;
-    const int64_t c = (int64_t)blockIdx.x * 64 + lc;
-    const int64_t per = (chunks + 3) / 4;
+    __shared__ float part[kRedRanges][kRedCols + 1];
+    const int lc = threadIdx.x % kRedCols, q = threadIdx.x / kRedCols;
+    const int64_t c = (int64_t)blockIdx.x * kRedCols + lc;
+    const int64_t per = (chunks + kRedRanges - 1) / kRedRanges;
     const int64_t k0 = q * per, k1 = (k0 + per) < chunks ? k0 + per : chunks;
     float s = 0.0f;
-    if (c < cols)
-        for (int64_t kk = k0; kk < k1; ++kk) s += partial[kk * cols + c];
+    if (c < cols) {
+        int64_t kk = k0;
+        for (; kk + 8 <= k1; kk += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = partial[(kk + u) * cols + c];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += v[u];
+        }
+        for (; kk < k1; ++kk) s += partial[kk * cols + c];
+    }
     part[q][lc] = s;
     __syncthreads();
-    if (q == 0 && c < cols) out[c] = ((part[0][lc] + part[1][lc]) + part[2][lc]) + part[3][lc];
+    if (q == 0 && c < cols) {
+        float t = part[0][lc];
+#pragma unroll
+        for (int r = 1; r < kRedRanges; ++r) t += part[r][lc];
+        out[c] = t;
+    }
 }
 
 // out[c, r] = in[r, c] for r < rows, c < out_rows; zero for rows <= r < rows_pad.
@@ -782,7 +802,8 @@ int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t s
 
 int launch_reduce_partials(const float* partial, int64_t chunks, int64_t cols, float* out, hipStream_t st) {
     if (cols == 0) return AXS6_OK;
-    reduce_partials_kernel<<<dim3((unsigned)((cols + 63) / 64)), 256, 0, st>>>(partial, chunks, cols, out);
+    reduce_partials_kernel<<<dim3((unsigned)((cols + kRedCols - 1) / kRedCols)), 256, 0, st>>>(partial, chunks, cols,
+                                                                                               out);
     return check_launch("reduce_partials");
 }
 
