@@ -384,6 +384,38 @@ def cpu_baseline_fq(budget_s: float = 12.0):
     }
 
 
+def cpu_baseline_linear(budget_s: float = 15.0):
+    """The reference's CPU eager linear forward at 4096^3 (FQ(W), FQ(X) with
+    the eager fused_fake_quantize, fp32 F.linear -- oracle/eager_torch.py
+    restating functional_unified.py:116-123) on the host cores: median of up
+    to 5 calls after a warm-up, bounded by budget_s."""
+    import torch
+
+    from oracle import eager_torch
+
+    threads = torch.get_num_threads()
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(4096, 4096, generator=g)
+    w = torch.randn(4096, 4096, generator=g) * 4096 ** -0.5
+    eager_torch.linear_fwd(x, w, None)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        eager_torch.linear_fwd(x, w, None)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(2 * 4096 ** 3 / med / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"torch-eager restatement of the reference's CPU linear forward (FQ(W), FQ(X), fp32 F.linear; "
+                   f"oracle/eager_torch.py) at 4096^3, median of {len(times)} calls after 1 warm-up, "
+                   f"{threads} threads, {cpu_model()}; {med * 1e3:.1f} ms/call"),
+    }
+
+
 def pmc_pass() -> int:
     """A short run for rocprofv3 counter collection: 5 NF5 fake-quantize
     launches at 8192x4096 f32, 3 linear forwards at 4096^3 and, as the
@@ -550,6 +582,9 @@ def main() -> int:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline_fq()
         log(f"cpu baseline: {out['cpu_baseline']['value']} GB/s")
+        if "linear" in out:
+            out["linear"]["cpu_baseline"] = cpu_baseline_linear()
+            log(f"cpu baseline, linear: {out['linear']['cpu_baseline']['value']} TFLOP/s")
     print(json.dumps(out), flush=True)
     return 0
 
