@@ -4,9 +4,9 @@
 // zero padding (the packing kernels write it).
 //
 // Tiling.  A workgroup of WGM x WGN waves owns a BM x BN tile of C; each wave
-// a (BM/WGM) x (BN/WGN) sub-tile of 32x32 MFMA blocks
-// (v_mfma_f32_32x32x16_f16: K = 16 per instruction, 16 fp32 accumulators per
-// lane).  Per K-step of 64 halves the A and B tiles go from HBM straight into
+// a (BM/WGM) x (BN/WGN) sub-tile of 16x16 MFMA blocks
+// (v_mfma_f32_16x16x32_f16: K = 32 per instruction, 4 fp32 accumulators per
+// lane; 32x32x16 blocks remain as sweep configurations).  Per K-step of 64 halves the A and B tiles go from HBM straight into
 // LDS (buffer_load ... lds; rows past M/N read as zero through the buffer's
 // range check) while the previous slab is multiplied; two LDS slabs, one
 // barrier per step.  Each 64-half row is 8 slots of 16 bytes, XOR-swizzled
@@ -36,6 +36,7 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4m __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;            // halves per K-step (8 slots of 16 bytes)
@@ -128,6 +129,70 @@ __device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const char* as, 
     }
 }
 
+// The wave's accumulators for a WM x WN sub-tile: 32x32 blocks of
+// v_mfma_f32_32x32x16_f16 (16 floats per lane) or 16x16 blocks of
+// v_mfma_f32_16x16x32_f16 (4 floats per lane).  Same 128 floats per lane for
+// a 128x64 sub-tile either way; the 16x16 instruction runs the same FLOPs per
+// cycle with half-size fragments and, in the 256x256 tiles, clocks higher
+// under the power limit (3-5% shorter GEMMs at 4096^3 and the Llama shapes).
+template <int MF, int WM, int WN> struct WaveAcc;
+template <int WM, int WN> struct WaveAcc<32, WM, WN> {
+    static constexpr int TM = WM / 32, TN = WN / 32, R = 16;
+    f32x16 v[TM][TN];
+};
+template <int WM, int WN> struct WaveAcc<16, WM, WN> {
+    static constexpr int TM = WM / 16, TN = WN / 16, R = 4;
+    f32x4m v[TM][TN];
+};
+
+// One K-step on 16x16 blocks: per 32-deep slice, lane l reads row l%16 of
+// its A and B blocks at K-group l/16 (chunk 4*slice + l/16; 16 consecutive
+// rows per 16-lane group, conflict-free under swz), then TM x TN MFMAs.
+template <int BK, int WM, int WN>
+__device__ __forceinline__ void mma_step16(WaveAcc<16, WM, WN>& acc, const char* as, const char* bs, int a_row0,
+                                           int b_row0, int fq) {
+    constexpr int TM = WaveAcc<16, WM, WN>::TM, TN = WaveAcc<16, WM, WN>::TN;
+#pragma unroll
+    for (int kk = 0; kk < BK / 32; ++kk) {
+        const int chunk = kk * 4 + fq;
+        f16x8 af[TM], bf[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const f16x8*>(as + swz<BK>(a_row0 + i * 16, chunk));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const f16x8*>(bs + swz<BK>(b_row0 + j * 16, chunk));
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc.v[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc.v[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_iglp_opt(1);
+}
+
+// Stages the wave's 32-row block row i (32 x WN floats, row stride LDW) in
+// LDS.  32x32 blocks: accumulator r of block (i, j) is row 8*(r/4) +
+// 4*(lane/32) + r%4, column lane%32.  16x16 blocks: accumulator r of block
+// (2i+h, j) is row 16*h + 4*(lane/16) + r, column lane%16 of the 16x16 block.
+// Both write patterns are bank-conflict free with LDW = WN + 4.
+template <int WM, int WN, int LDW>
+__device__ __forceinline__ void stage_block_row(const WaveAcc<32, WM, WN>& acc, int i, float* ws, int lane) {
+    const int fr = lane & 31, fh = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < WaveAcc<32, WM, WN>::TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ws[((r >> 2) * 8 + (r & 3) + fh * 4) * LDW + j * 32 + fr] = acc.v[i][j][r];
+}
+template <int WM, int WN, int LDW>
+__device__ __forceinline__ void stage_block_row(const WaveAcc<16, WM, WN>& acc, int i, float* ws, int lane) {
+    const int fc = lane & 15, fq = lane >> 4;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < WaveAcc<16, WM, WN>::TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ws[(h * 16 + fq * 4 + r) * LDW + j * 16 + fc] = acc.v[2 * i + h][j][r];
+}
+
 // Writes 4 consecutive output values of row `row` starting at column `col`
 // (col % 4 == 0): one vector store when the 4 columns exist and the row
 // segment is aligned, else element by element up to N.
@@ -193,24 +258,19 @@ __device__ __forceinline__ void store4t(void* out, int64_t ldo, int N, int row, 
 // 4 consecutive columns per lane for all PASSES row groups and their row
 // exponents at once -- one LDS wait per block row instead of two per row
 // group -- and write them with the output type fixed at compile time.
-template <int OUT, int TM, int TN, int WM, int WN, int LDW>
-__device__ __forceinline__ void epilogue_store(const f32x16 (&acc)[TM][TN], float* ws, const int (&rexp_l)[WM / 64],
+template <int OUT, int MF, int WM, int WN, int LDW>
+__device__ __forceinline__ void epilogue_store(const WaveAcc<MF, WM, WN>& acc, float* ws, const int (&rexp_l)[WM / 64],
                                                const int (&cexp)[4], const float (&cbias)[4], void* out, int64_t ldo,
                                                int M, int N, int row0, int gcol, bool vec, int lane) {
     constexpr int LANES_PER_ROW = WN / 4;
     constexpr int ROWS_PER_PASS = 64 / LANES_PER_ROW;
     constexpr int PASSES = 32 / ROWS_PER_PASS;
-    const int fr = lane & 31, fh = lane >> 5;
     const int c4 = (lane % LANES_PER_ROW) * 4;
     const int rsub = lane / LANES_PER_ROW;
     const bool full = vec && gcol + 3 < N;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                ws[((r >> 2) * 8 + (r & 3) + fh * 4) * LDW + j * 32 + fr] = acc[i][j][r];
+    for (int i = 0; i < WM / 32; ++i) {
+        stage_block_row<WM, WN, LDW>(acc, i, ws, lane);
         float4 q[PASSES];
         int rx[PASSES];
 #pragma unroll
@@ -249,12 +309,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 // registers are spent on staging.  Lane l of a load instruction lands at
 // byte 16*l of its 1 KiB, i.e. row l/8, slot l%8, and therefore fetches
 // logical chunk (l%8) ^ key(row) -- the same XOR layout the fragment reads use.
-template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED>
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED, int MF>
 __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(GemmK g) {
 #if defined(__HIP_DEVICE_COMPILE__)  // LDS-DMA builtins exist only in the device pass
     constexpr int NW = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
-    constexpr int TM = WM / 32, TN = WN / 32;
     constexpr int RB = BK * 2;                                 // bytes per slab row
     constexpr int SPR = BK / 8;                                // 16-byte slots per row
     constexpr int ROWS_PER_INST = 1024 / RB;                   // rows one wave load fills
@@ -314,13 +373,14 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     for (int i = 0; i < B_INST; ++i) b_goff[i] += kbeg * RB;
     auto lds_ptr = [](char* p) { return (__attribute__((address_space(3))) void*)p; };
 
-    f32x16 acc[TM][TN];
+    using Acc = WaveAcc<MF, WM, WN>;
+    Acc acc;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < Acc::TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < Acc::TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            for (int r = 0; r < Acc::R; ++r) acc.v[i][j][r] = 0.0f;
 
     // prologue: slabs 0 .. STAGES-2
 #pragma unroll
@@ -336,8 +396,9 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
         }
     }
 
-    const int fr = lane & 31;
-    const int fh = lane >> 5;
+    // fragment row and K-group of this lane: l%32, l/32 (32x32) or l%16, l/16 (16x16)
+    const int fr = lane % MF;
+    const int fg = lane / MF;
     const int a_row0 = wm * WM + fr;
     const int b_row0 = wn * WN + fr;
     for (int kt = 0; kt < KT; ++kt) {
@@ -368,13 +429,15 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, lds_ptr(slab + b_loff[i]), 16, b_goff[i] + nk * RB, 0, 0, 0);
         }
         const char* slab = smem + (kt % STAGES) * SLAB;
-        mma_step<BK, TM, TN, SCHED>(acc, slab, slab + BM * RB, a_row0, b_row0, fh);
+        if constexpr (MF == 32)
+            mma_step<BK, Acc::TM, Acc::TN, SCHED>(acc.v, slab, slab + BM * RB, a_row0, b_row0, fg);
+        else
+            mma_step16<BK, WM, WN>(acc, slab, slab + BM * RB, a_row0, b_row0, fg);
     }
 
     // ---- epilogue through LDS ------------------------------------------------
-    // Accumulator r of block (i, j) holds row 8*(r/4) + 4*(lane/32) + r%4,
-    // column lane%32 of that 32x32 block.  Each wave stages its block row i
-    // (32 x WN floats, row stride WN+4 to spread banks) in its own LDS region,
+    // Each wave stages its 32-row block row i (32 x WN floats, row stride
+    // WN+4 to spread banks; stage_block_row) in its own LDS region,
     // then reads it back as 4 consecutive columns per lane.  The slabs are
     // dead once every wave has left the K loop (barrier); after that a wave
     // touches only its own region, and LDS operations of one wave complete in
@@ -413,28 +476,28 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     const bool vec = (g.ldo % 4 == 0) && ((uintptr_t)out % (4 * esize) == 0);
     const int row0 = m0 + wm * WM;
     if (g.out_dtype == AXS6_F32)
-        epilogue_store<AXS6_F32, TM, TN, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+        epilogue_store<AXS6_F32, MF, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
                                                       vec, lane);
     else if (g.out_dtype == AXS6_BF16)
-        epilogue_store<AXS6_BF16, TM, TN, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+        epilogue_store<AXS6_BF16, MF, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
                                                        vec, lane);
     else
-        epilogue_store<AXS6_F16, TM, TN, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+        epilogue_store<AXS6_F16, MF, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
                                                       vec, lane);
 #endif
 }
 
-template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED>
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED, int MF = 32>
 int run_gemm_lds(const GemmK& k, int splits, hipStream_t st) {
     const int tiles = ((k.M + BM - 1) / BM) * ((k.N + BN - 1) / BN);
     const size_t lds = (size_t)STAGES * (BM + BN) * BK * 2;
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED>,
+        (void)hipFuncSetAttribute((const void*)gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED, MF>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         attr_set = true;
     }
-    gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED>
+    gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED, MF>
         <<<dim3((unsigned)tiles, (unsigned)splits), WGM * WGN * 64, lds, st>>>(k);
     return check_launch("gemm_f16_lds");
 }
@@ -514,19 +577,22 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(SplitReduceK k) {
 //   4: 256x256 / 32 / 4 / 4 / 2      5: 256x256 / 32 / 4 / 8 / 3
 //   6: 256x256 / 64 / 2 / 8 / 0      7: 256x128 / 64 / 3 / 8 / 2
 //   8: 128x128 / 64 / 2 / 4 / 2
-// Default: 0, or 8 when the 256x256 tiles do not cover the 256 CUs once.
+// all on 32x32x16 MFMAs; 9 and 10 are 0 and 8 on 16x16x32 MFMAs.
+// Default: 9, or 10 when the 256x256 tiles do not cover the 256 CUs once
+// (measured against 0 and 8: 0-5% shorter on every shape tried, 4096^3, the
+// Llama-7B MLP shapes and the 768/3072 ones).
 // The epilogue of a tile (LDS staging, exponent scaling, stores) costs a
 // fixed ~7 us per 256x256 f32 tile and CU, all of a short-K GEMM's runtime
 // when 32 CUs carry it; 128x128 tiles spread it over 4x the CUs, two
 // workgroups sharing a CU.  AXS6_GEMM_CFG=<n> forces a configuration for
 // launch-shape sweeps.
-constexpr int kCfgSmall = 8;
+constexpr int kCfgBig = 9, kCfgSmall = 10;
 
 int gemm_cfg_env() {
     static int v = [] {
         const char* s = getenv("AXS6_GEMM_CFG");
         int n = s ? atoi(s) : -1;
-        return (n >= 0 && n <= 8) ? n : -1;
+        return (n >= 0 && n <= 10) ? n : -1;
     }();
     return v;
 }
@@ -536,14 +602,21 @@ int64_t tiles_of(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / 
 int pick_cfg(int64_t M, int64_t N) {
     const int env = gemm_cfg_env();
     if (env >= 0) return env;
-    return tiles_of(M, N, 256, 256) < 256 ? kCfgSmall : 0;
+    return tiles_of(M, N, 256, 256) < 256 ? kCfgSmall : kCfgBig;
 }
+
+bool is_small_cfg(int cfg) { return cfg == 8 || cfg == 10; }
+
+// configuration of a split-K launch: one with 64-half K-slabs (the split
+// ranges are counted in them); forced sweep configurations with 32-half
+// slabs fall back to the default large tiles
+int split_cfg(int cfg) { return (cfg == 0 || cfg == 8 || cfg == 9 || cfg == 10) ? cfg : kCfgBig; }
 
 }  // namespace
 
 int gemm_split_count(int64_t M, int64_t N, int64_t Kp) {
-    // split launches use configuration 0 or kCfgSmall (both 64-half K-slabs)
-    const bool small = pick_cfg(M, N) == kCfgSmall;
+    // split launches use configurations with 64-half K-slabs (split_cfg)
+    const bool small = is_small_cfg(split_cfg(pick_cfg(M, N)));
     const int64_t tiles = small ? tiles_of(M, N, 128, 128) : tiles_of(M, N, 256, 256);
     const int64_t iters = Kp / kGemmK;
     if (tiles >= 64 || iters < 8) return 1;
@@ -588,7 +661,7 @@ int launch_gemm_f16(const GemmArgs& a, hipStream_t st) {
             split ? (int)AXS6_F32 : a.out_dtype, per, split ? a.M * a.N : 0};
     int rc;
     const int cfg = pick_cfg(a.M, a.N);
-    switch (split ? (cfg == kCfgSmall ? kCfgSmall : 0) : cfg) {
+    switch (split ? split_cfg(cfg) : cfg) {
         case 1: rc = run_gemm_lds<256, 256, 32, 4, 2, 4, 2>(k, splits, st); break;
         case 2: rc = run_gemm_lds<256, 256, 32, 3, 2, 4, 2>(k, splits, st); break;
         case 3: rc = run_gemm_lds<256, 256, 32, 4, 2, 4, 0>(k, splits, st); break;
@@ -596,8 +669,10 @@ int launch_gemm_f16(const GemmArgs& a, hipStream_t st) {
         case 5: rc = run_gemm_lds<256, 256, 32, 4, 2, 4, 3>(k, splits, st); break;
         case 6: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 0>(k, splits, st); break;
         case 7: rc = run_gemm_lds<256, 128, 64, 3, 4, 2, 2>(k, splits, st); break;
-        case kCfgSmall: rc = run_gemm_lds<128, 128, 64, 2, 2, 2, 2>(k, splits, st); break;
-        default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2>(k, splits, st); break;
+        case 8: rc = run_gemm_lds<128, 128, 64, 2, 2, 2, 2>(k, splits, st); break;
+        case kCfgSmall: rc = run_gemm_lds<128, 128, 64, 2, 2, 2, 2, 16>(k, splits, st); break;
+        case 0: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2>(k, splits, st); break;
+        default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2, 16>(k, splits, st); break;   // kCfgBig
     }
     if (rc || !split) return rc;
     SplitReduceK r{a.split_partial, splits, a.M * a.N, (int)a.M, (int)a.N, a.row_exp, a.col_exp, a.glob_exp,
