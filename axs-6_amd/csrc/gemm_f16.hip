@@ -309,7 +309,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // registers are spent on staging.  Lane l of a load instruction lands at
 // byte 16*l of its 1 KiB, i.e. row l/8, slot l%8, and therefore fetches
 // logical chunk (l%8) ^ key(row) -- the same XOR layout the fragment reads use.
-template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED, int MF>
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED, int MF, int LW>
 __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(GemmK g) {
 #if defined(__HIP_DEVICE_COMPILE__)  // LDS-DMA builtins exist only in the device pass
     constexpr int NW = WGM * WGN;
@@ -317,8 +317,9 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     constexpr int RB = BK * 2;                                 // bytes per slab row
     constexpr int SPR = BK / 8;                                // 16-byte slots per row
     constexpr int ROWS_PER_INST = 1024 / RB;                   // rows one wave load fills
-    constexpr int A_INST = BM / ROWS_PER_INST / NW;            // load instructions per wave per slab
-    constexpr int B_INST = BN / ROWS_PER_INST / NW;
+    static_assert(LW >= 1 && LW <= NW && NW % LW == 0, "loading waves");
+    constexpr int A_INST = BM / ROWS_PER_INST / LW;            // load instructions per loading wave per slab
+    constexpr int B_INST = BN / ROWS_PER_INST / LW;
     constexpr int IPW = A_INST + B_INST;
     constexpr int SLAB = (BM + BN) * RB;
     static_assert(A_INST >= 1 && B_INST >= 1 && STAGES >= 2, "tile shape");
@@ -341,6 +342,8 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
+    // waves 0 .. LW-1 issue the slab loads (wave-uniform branch)
+    const bool loader = wave < LW;
 
     const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void*)g.A, 0, (int)((int64_t)g.M * g.lda * 2), kBufferConfig);
@@ -352,15 +355,15 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     int a_goff[A_INST], a_loff[A_INST], b_goff[B_INST], b_loff[B_INST];
 #pragma unroll
     for (int i = 0; i < A_INST; ++i) {
-        const int row = (wave + NW * i) * ROWS_PER_INST + lrow;     // row of the A slab
+        const int row = (wave % LW + LW * i) * ROWS_PER_INST + lrow;     // row of the A slab
         a_goff[i] = (int)((int64_t)(m0 + row) * g.lda * 2) + ((lslot ^ swz_key<BK>(row)) << 4);
-        a_loff[i] = (wave + NW * i) * 1024;
+        a_loff[i] = (wave % LW + LW * i) * 1024;
     }
 #pragma unroll
     for (int i = 0; i < B_INST; ++i) {
-        const int row = (wave + NW * i) * ROWS_PER_INST + lrow;
+        const int row = (wave % LW + LW * i) * ROWS_PER_INST + lrow;
         b_goff[i] = (int)((int64_t)(n0 + row) * g.ldb * 2) + ((lslot ^ swz_key<BK>(row)) << 4);
-        b_loff[i] = BM * RB + (wave + NW * i) * 1024;
+        b_loff[i] = BM * RB + (wave % LW + LW * i) * 1024;
     }
     // split-K: this workgroup's range of K-steps (k_iters counts 64-half steps)
     static_assert(kGemmK % BK == 0, "K-slab must divide the padding unit");
@@ -385,7 +388,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     // prologue: slabs 0 .. STAGES-2
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s) {
-        if (s < KT) {
+        if (s < KT && loader) {
             char* slab = smem + s * SLAB;
 #pragma unroll
             for (int i = 0; i < A_INST; ++i)
@@ -419,7 +422,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
         // above already orders this wave's LDS fills before the barrier.
         __builtin_amdgcn_s_barrier();
         const int nk = kt + STAGES - 1;
-        if (nk < KT) {
+        if (nk < KT && loader) {
             char* slab = smem + (nk % STAGES) * SLAB;
 #pragma unroll
             for (int i = 0; i < A_INST; ++i)
@@ -487,17 +490,17 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
 #endif
 }
 
-template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED, int MF = 32>
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED, int MF = 32, int LW = WGM * WGN>
 int run_gemm_lds(const GemmK& k, int splits, hipStream_t st) {
     const int tiles = ((k.M + BM - 1) / BM) * ((k.N + BN - 1) / BN);
     const size_t lds = (size_t)STAGES * (BM + BN) * BK * 2;
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED, MF>,
+        (void)hipFuncSetAttribute((const void*)gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED, MF, LW>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         attr_set = true;
     }
-    gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED, MF>
+    gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED, MF, LW>
         <<<dim3((unsigned)tiles, (unsigned)splits), WGM * WGN * 64, lds, st>>>(k);
     return check_launch("gemm_f16_lds");
 }
@@ -571,16 +574,27 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(SplitReduceK k) {
 }
 
 // Launch configurations (BMxBN tile / K-slab / LDS stages / waves /
-// schedule variant of mma_step):
+// schedule variant of mma_step), every wave issuing slab loads unless noted:
 //   0: 256x256 / 64 / 2 / 8 / 2      1: 256x256 / 32 / 4 / 8 / 2
 //   2: 256x256 / 32 / 3 / 8 / 2      3: 256x256 / 32 / 4 / 8 / 0
 //   4: 256x256 / 32 / 4 / 4 / 2      5: 256x256 / 32 / 4 / 8 / 3
 //   6: 256x256 / 64 / 2 / 8 / 0      7: 256x128 / 64 / 3 / 8 / 2
 //   8: 128x128 / 64 / 2 / 4 / 2
-// all on 32x32x16 MFMAs; 9 and 10 are 0 and 8 on 16x16x32 MFMAs.
-// Default: 9, or 10 when the 256x256 tiles do not cover the 256 CUs once
-// (measured against 0 and 8: 0-5% shorter on every shape tried, 4096^3, the
-// Llama-7B MLP shapes and the 768/3072 ones).
+// all on 32x32x16 MFMAs; on 16x16x32 MFMAs:
+//   9: 256x256 / 64 / 2 / 8 / 2, waves 0-3 issue all slab loads
+//  10: 128x128 / 64 / 2 / 4 / 2     11: 9 with every wave loading
+// Default: 9, or 10 when the 256x256 tiles do not cover the 256 CUs once.
+// 16x16x32 against 32x32x16 (11 against 0, 10 against 8): 0-5% shorter on
+// every shape tried (4096^3, the Llama-7B MLP shapes, the 768/3072 ones).
+// Loads from waves 0-3 only (9 against 11): 6-12% shorter on the large
+// shapes.  Waves are placed on the CU's four SIMDs round-robin, so each SIMD
+// holds one loading and one compute-only wave.  When all eight waves leave
+// the barrier and issue their loads together, the address unit (~64 bytes
+// per clock) backs up and both waves of a SIMD stall in the issue, leaving
+// its MFMA pipe idle; with one loader per SIMD the other wave runs its MFMAs
+// meanwhile (the loads still land well inside the K-step).  Measured: the
+// stalled-issue counters SQ_VMEM_TA_ADDR_FIFO_FULL / _CMD_FIFO_FULL were 50x
+// those of hipBLASLt's fp16 kernel with every wave loading.
 // The epilogue of a tile (LDS staging, exponent scaling, stores) costs a
 // fixed ~7 us per 256x256 f32 tile and CU, all of a short-K GEMM's runtime
 // when 32 CUs carry it; 128x128 tiles spread it over 4x the CUs, two
@@ -592,7 +606,7 @@ int gemm_cfg_env() {
     static int v = [] {
         const char* s = getenv("AXS6_GEMM_CFG");
         int n = s ? atoi(s) : -1;
-        return (n >= 0 && n <= 10) ? n : -1;
+        return (n >= 0 && n <= 11) ? n : -1;
     }();
     return v;
 }
@@ -610,7 +624,7 @@ bool is_small_cfg(int cfg) { return cfg == 8 || cfg == 10; }
 // configuration of a split-K launch: one with 64-half K-slabs (the split
 // ranges are counted in them); forced sweep configurations with 32-half
 // slabs fall back to the default large tiles
-int split_cfg(int cfg) { return (cfg == 0 || cfg == 8 || cfg == 9 || cfg == 10) ? cfg : kCfgBig; }
+int split_cfg(int cfg) { return (cfg == 0 || cfg >= 8) ? cfg : kCfgBig; }
 
 }  // namespace
 
@@ -672,7 +686,8 @@ int launch_gemm_f16(const GemmArgs& a, hipStream_t st) {
         case 8: rc = run_gemm_lds<128, 128, 64, 2, 2, 2, 2>(k, splits, st); break;
         case kCfgSmall: rc = run_gemm_lds<128, 128, 64, 2, 2, 2, 2, 16>(k, splits, st); break;
         case 0: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2>(k, splits, st); break;
-        default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2, 16>(k, splits, st); break;   // kCfgBig
+        case 11: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2, 16>(k, splits, st); break;
+        default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2, 16, 4>(k, splits, st); break;   // kCfgBig
     }
     if (rc || !split) return rc;
     SplitReduceK r{a.split_partial, splits, a.M * a.N, (int)a.M, (int)a.N, a.row_exp, a.col_exp, a.glob_exp,
