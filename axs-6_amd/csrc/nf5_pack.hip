@@ -97,16 +97,13 @@ struct PackRowsK {
 
 // Row pack: rows of the concatenation of k's rows and k2's (two operands in
 // one launch; k2 == k and total == k.rows for one).  NT threads hold a row in
-// registers, NV 16-byte vectors each (NT grows with the row length so that
-// NV <= 4 and occupancy stays high).  A workgroup holds RPW row groups and
-// handles rows RPW*w + g, RPW*(w + gridDim.x) + g, ...; with NT == 64 a row
-// is one wave and its reductions need no barrier, so short rows run several
-// to a workgroup (RPW > 1 requires NT == 64).  The LUT and band table are
-// staged once per workgroup.  With PF, the loads of a workgroup's next row
-// are issued before the current row's reduction, barrier and stores, so a
-// long row's loads stay in flight while the previous row finishes (a row's
-// maximum, and so its stores, wait for the whole row).
-template <int DT, int MODE, bool COLX, int NV, int NT, int RPW, bool PF = false>
+// registers, NV 16-byte vectors each (rows_shape picks NT and NV by row
+// length).  A workgroup holds RPW row groups and handles rows RPW*w + g,
+// RPW*(w + gridDim.x) + g, ...; with NT == 64 a row is one wave and its
+// reductions need no barrier, so short rows run several to a workgroup
+// (RPW > 1 requires NT == 64).  The LUT and band table are staged once per
+// workgroup (NT * RPW >= 256 threads).
+template <int DT, int MODE, bool COLX, int NV, int NT, int RPW>
 __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRowsK k2, int64_t total) {
     using E = Elem<DT>;
     using S = typename E::S;
@@ -114,6 +111,7 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
     constexpr int NW = NT / 64;
     constexpr bool WAVE_ROW = NT == 64;
     static_assert(RPW == 1 || WAVE_ROW, "several rows per workgroup need one wave per row");
+    static_assert(NT * RPW >= kLutSize / 4 && NT * RPW >= kBandSize / 4, "table staging takes one thread per word");
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
     __shared__ int red[2][2][NW];         // [row parity][tmax, rmax][wave]
@@ -133,11 +131,6 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
         }
     };
     const int64_t stride = (int64_t)gridDim.x * RPW;
-    u32x4 pre[NV];
-    if constexpr (PF) {
-        const int64_t R0 = (int64_t)blockIdx.x * RPW + threadIdx.x / NT;
-        if (R0 < total) load_row(R0, pre);
-    }
 
     int parity = 0;
     for (int64_t R = (int64_t)blockIdx.x * RPW + threadIdx.x / NT; R < total; R += stride, parity ^= 1) {
@@ -152,13 +145,7 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
         float f[NV][V];
         int cx[NV][V];
         u32x4 raw[NV];
-        if constexpr (PF) {
-#pragma unroll
-            for (int j = 0; j < NV; ++j) raw[j] = pre[j];
-            if (R + stride < total) load_row(R + stride, pre);   // next row, in flight meanwhile
-        } else {
-            load_row(R, raw);
-        }
+        load_row(R, raw);
         (void)xr;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
@@ -621,10 +608,17 @@ inline RowsShape rows_shape(int64_t nvec) {
     if (nvec <= 256) return {64, 4};
     if (nvec <= 512) return {256, 2};
     if (nvec <= 1024) return {256, 4};
-    if (nvec <= 2048) return {512, 4};
-    return {1024, 4};
+    // long rows, measured (one row per workgroup, 8192-16384 rows): for
+    // 1025-2048 vectors 256 x 8 beats 512 x 4 by 12-13%; for 2049-3072
+    // (e.g. 11008 fp32 columns) 768 x 4 beats 1024 x 4 (two rows per
+    // workgroup, the second's loads in flight) by 32%; for 3073-4096 512 x 8
+    // beats it by 20%.  Thread counts of 384, 704 and 1024 were slower at
+    // every length tried.
+    if (nvec <= 2048) return {256, 8};
+    if (nvec <= 3072) return {768, 4};
+    return {512, 8};
 }
-constexpr int64_t kRowsMaxVec = 4096;   // 1024 threads x 4 vectors
+constexpr int64_t kRowsMaxVec = 4096;   // 512 threads x 8 vectors
 
 template <int DT, int MODE, bool COLX>
 void dispatch_rows_nv(const PackRowsK& k, const PackRowsK& k2, int64_t rows, RowsShape sh, hipStream_t st) {
@@ -637,14 +631,12 @@ void dispatch_rows_nv(const PackRowsK& k, const PackRowsK& k2, int64_t rows, Row
         if (sh.nv == 1) pack_rows_kernel<DT, MODE, COLX, 1, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
         else if (sh.nv == 2) pack_rows_kernel<DT, MODE, COLX, 2, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
         else pack_rows_kernel<DT, MODE, COLX, 4, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
-    } else if (sh.nt == 1024) {
-        // long rows: two rows per workgroup, the second row's loads issued
-        // while the first is reduced and stored
-        const dim3 g2((unsigned)((rows + 1) / 2));
-        pack_rows_kernel<DT, MODE, COLX, 4, 1024, 1, true><<<g2, 1024, 0, st>>>(k, k2, rows);
+    } else if (sh.nt == 768) {
+        pack_rows_kernel<DT, MODE, COLX, 4, 768, 1><<<grid, 768, 0, st>>>(k, k2, rows);
     } else if (sh.nt == 512) {
-        const dim3 g2((unsigned)((rows + 1) / 2));
-        pack_rows_kernel<DT, MODE, COLX, 4, 512, 1, true><<<g2, 512, 0, st>>>(k, k2, rows);
+        pack_rows_kernel<DT, MODE, COLX, 8, 512, 1><<<grid, 512, 0, st>>>(k, k2, rows);
+    } else if (sh.nv == 8) {
+        pack_rows_kernel<DT, MODE, COLX, 8, 256, 1><<<grid, 256, 0, st>>>(k, k2, rows);
     } else if (sh.nv == 2) {
         pack_rows_kernel<DT, MODE, COLX, 2, 256, 1><<<grid, 256, 0, st>>>(k, k2, rows);
     } else {

@@ -82,7 +82,9 @@ def _assert_bits(got: np.ndarray, want: np.ndarray, what: str):
 
 # f32 row widths: 8, 64, 128 and 256 vectors (one wave per row), 512 and 1024
 # (256 threads), 1536 (512 threads, prefetch), 2752 and 4096 (1024 threads, prefetch)
-@pytest.mark.parametrize("cols", [32, 256, 512, 1024, 2048, 4096, 6144, 11008, 16384])
+# row lengths cover every thread shape of the kernel (one wave per row; 256 x
+# 2/4/8, 768 x 4, 512 x 8 threads x vectors) and the boundaries between them
+@pytest.mark.parametrize("cols", [32, 256, 512, 1024, 2048, 4096, 6144, 8192, 8224, 11008, 12288, 12320, 16384])
 @pytest.mark.parametrize("rows", [37, 1])
 def test_pack_rows_f32_bitexact(rows, cols):
     print(f"[pack_rows f32 {rows}x{cols}]", flush=True)
@@ -95,7 +97,7 @@ def test_pack_rows_f32_bitexact(rows, cols):
 
 
 # bf16 widths: 1376 vectors (512 threads, prefetch) and 4096 (1024 threads, prefetch)
-@pytest.mark.parametrize("cols", [256, 11008, 32768])
+@pytest.mark.parametrize("cols", [256, 11008, 16384, 16416, 24576, 32768])
 def test_pack_rows_bf16_bitexact(cols):
     print(f"[pack_rows bf16 37x{cols}]", flush=True)
     xb = torch.from_numpy(_data(37, cols, 5 + cols)).to(torch.bfloat16)
