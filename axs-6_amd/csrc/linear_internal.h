@@ -62,8 +62,10 @@ struct RowStatsArgs {
     int32_t* shift;                 // nullable
     const int32_t* rowx;            // nullable (0)
     int32_t* gmax;                  // nullable
-    int32_t* scratch;               // [2 * rows]
+    int32_t* scratch;               // [2 * row_stats_col_tiles(cols) * rows]
 };
+// column tiles of the statistics pass: its scratch holds two ints per tile and row
+int64_t row_stats_col_tiles(int64_t cols);
 int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t st);
 
 int64_t pack_global_chunks(int64_t rows);
@@ -72,9 +74,12 @@ int64_t pack_global_chunks(int64_t rows);
 int launch_reduce_partials(const float* partial, int64_t chunks, int64_t cols, float* out, hipStream_t st);
 
 // out[c, r] = in[r, c] for r < rows, c < out_rows; zero for rows <= r < rows_pad.
-int launch_transpose_f16(const _Float16* in, int64_t rows, int64_t cols, int64_t ld_in,
-                         _Float16* out, int64_t out_rows, int64_t rows_pad, int64_t ld_out,
-                         hipStream_t st);
+struct TransposeF16 {
+    const _Float16* in; int64_t rows; int64_t cols; int64_t ld_in;
+    _Float16* out; int64_t out_rows; int64_t rows_pad; int64_t ld_out;
+};
+// a, and b when not null, in one launch
+int launch_transpose_f16(const TransposeF16& a, const TransposeF16* b, hipStream_t st);
 
 // *p = INT32_MIN (graph-capture safe: a kernel, not a memset).
 int launch_init_gmax(int32_t* p, hipStream_t st);

@@ -42,7 +42,7 @@ BwdLayout bwd_layout(int64_t M, int64_t N, int64_t K, bool dx, bool dw, bool db)
     auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
     L.gmax = take(sizeof(int32_t));
     L.t = take(sizeof(int32_t) * (size_t)M);
-    L.stats = take(2 * sizeof(int32_t) * (size_t)M);
+    L.stats = take(2 * sizeof(int32_t) * (size_t)row_stats_col_tiles(N) * (size_t)M);
     L.a1 = dx ? take(2 * (size_t)M * Np) : 0;
     L.wqt = dx ? take(2 * (size_t)Kp * Np) : 0;
     L.a2t = dw ? take(2 * (size_t)N * Mp) : 0;
@@ -174,17 +174,21 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
                     need_db ? (float*)(ws + L.partial) : nullptr};
         if ((rc = launch_pack_t(p, t, st))) return rc;
     }
+    // contraction-contiguous copies of the forward's operands, one launch
+    _Float16* wqt = need_dx ? (_Float16*)(ws + L.wqt) : nullptr;
+    _Float16* xqt = need_dw ? (_Float16*)(ws + L.xqt) : nullptr;
+    const TransposeF16 tw{(const _Float16*)wq_f16, N, Kp, Kp, wqt, Kp, Np, Np};
+    const TransposeF16 tx{(const _Float16*)xq_f16, M, Kp, Kp, xqt, Kp, Mp, Mp};
+    if (need_dx || need_dw) {
+        if ((rc = launch_transpose_f16(need_dx ? tw : tx, need_dx && need_dw ? &tx : nullptr, st))) return rc;
+    }
     if (need_dx) {
-        _Float16* wqt = (_Float16*)(ws + L.wqt);
-        if ((rc = launch_transpose_f16((const _Float16*)wq_f16, N, Kp, Kp, wqt, Kp, Np, Np, st))) return rc;
         GemmArgs g{(const _Float16*)(ws + L.a1), Np, wqt, Np, M, K, Np, tshift, nullptr, nullptr, 0, nullptr,
                    dx, K, dtype, L.splitk_bytes ? (float*)(ws + L.splitk) : nullptr, L.splitk_bytes};
         if ((rc = launch_gemm_f16(g, st))) return rc;
     }
     if (need_dw) {
         _Float16* a2t = (_Float16*)(ws + L.a2t);
-        _Float16* xqt = (_Float16*)(ws + L.xqt);
-        if ((rc = launch_transpose_f16((const _Float16*)xq_f16, M, Kp, Kp, xqt, Kp, Mp, Mp, st))) return rc;
         GemmArgs g{a2t, Mp, xqt, Mp, N, K, Mp, nullptr, nullptr, gmax, -15, nullptr, dw, K, AXS6_F32,
                    L.splitk_bytes ? (float*)(ws + L.splitk) : nullptr, L.splitk_bytes};
         if ((rc = launch_gemm_f16(g, st))) return rc;

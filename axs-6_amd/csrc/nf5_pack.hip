@@ -392,24 +392,26 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
 }
 
 // Row statistics of x for the packing shifts (block exponents only, no FQ
-// values), streamed over tiles of 64 rows x 256 columns.  For the blocks with
-// a finite nonzero scale 2^e1 (every FQ value of the block is at most 2^e1 in
-// magnitude) each workgroup folds into
-//   tmax[r] = max over blocks of (e1 + max colx over the block's columns)
-//   rmax[r] = max over blocks of e1
-// with atomicMax (both start at INT_MIN); stats_finalize_kernel then writes
-//   shift[r] = tmax[r] - 15 (0 if INT_MIN) and atomicMax(gmax, rmax[r] + rowx[r]).
-// These are the quantities pack_rows derives for a whole row in one workgroup;
-// a row-per-workgroup pass over long rows is latency-bound, this one streams.
+// values), streamed over tiles of RPP*PASSES rows x 256 columns.  For the
+// blocks with a finite nonzero scale 2^e1 (every FQ value of the block is at
+// most 2^e1 in magnitude) the workgroup of column tile tx writes, per row,
+//   tmax[tx][r] = max over its blocks of (e1 + max colx over the block's columns)
+//   rmax[tx][r] = max over its blocks of e1
+// (INT_MIN when no block qualifies); stats_finalize_kernel folds the column
+// tiles in order and writes shift[r] = max_tx tmax - 15 (0 if INT_MIN) and
+// atomicMax(gmax, max_tx rmax + rowx[r]).  These are the quantities pack_rows
+// derives for a whole row in one workgroup; a row-per-workgroup pass over
+// long rows is latency-bound, this one streams.  Plain stores of per-tile
+// maxima, not atomics on a zeroed array: no initialising launch.
 struct StatsK {
     const void* x; int64_t rows; int64_t cols;
-    const int32_t* colx; int32_t* tmax; int32_t* rmax;
-    const uint8_t* band;
+    const int32_t* colx; int32_t* tmax; int32_t* rmax;   // [ntx][rows] each
+    const uint8_t* band; int32_t* gmax;                  // gmax set to INT_MIN by workgroup 0
 };
 
 constexpr int kStatsCols = 256;   // columns of a statistics tile
 
-template <int DT, int BS>
+template <int DT, int BS, int PASSES>
 __global__ __launch_bounds__(256) void stats_tile_kernel(StatsK k, int64_t ntx) {
     using E = Elem<DT>;
     using S = typename E::S;
@@ -417,14 +419,14 @@ __global__ __launch_bounds__(256) void stats_tile_kernel(StatsK k, int64_t ntx) 
     constexpr int G = BS / V > 0 ? BS / V : 1;
     constexpr int TPR = kTile / V;                  // threads per 64-column chunk of a row
     constexpr int RPP = 256 / TPR;                  // rows per pass
-    constexpr int PASSES = kTile / RPP;
     constexpr int CH = kStatsCols / kTile;          // 64-column chunks per tile
     __shared__ uint32_t band_w[kBandSize / 4];
     const int tid = threadIdx.x;
     if (tid < kBandSize / 4) band_w[tid] = reinterpret_cast<const uint32_t*>(k.band)[tid];
     const int tc = tid % TPR, tr = tid / TPR;
     const int64_t ty = blockIdx.x / ntx, tx = blockIdx.x - ty * ntx;
-    const int64_t r0 = ty * kTile, c0 = tx * kStatsCols;
+    const int64_t r0 = ty * (RPP * PASSES), c0 = tx * kStatsCols;
+    if (blockIdx.x == 0 && tid == 0 && k.gmax) *k.gmax = INT_MIN;
     const S* xs = reinterpret_cast<const S*>(k.x);
 
     u32x4 raw[PASSES][CH];
@@ -485,28 +487,27 @@ __global__ __launch_bounds__(256) void stats_tile_kernel(StatsK k, int64_t ntx) 
             tm = o1 > tm ? o1 : tm;
             rm = o2 > rm ? o2 : rm;
         }
-        if (tc == 0 && r < k.rows && rm != INT_MIN) {
-            atomicMax(k.tmax + r, tm);
-            atomicMax(k.rmax + r, rm);
+        if (tc == 0 && r < k.rows) {
+            k.tmax[tx * k.rows + r] = tm;
+            k.rmax[tx * k.rows + r] = rm;
         }
     }
 }
 
-__global__ __launch_bounds__(256) void stats_init_kernel(int32_t* a, int64_t n, int32_t* gmax) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) a[i] = INT_MIN;
-    if (i == 0 && gmax) *gmax = INT_MIN;
-}
-
 __global__ __launch_bounds__(256) void stats_finalize_kernel(const int32_t* __restrict__ tmax,
                                                              const int32_t* __restrict__ rmax, int64_t rows,
-                                                             int32_t* shift, const int32_t* rowx, int32_t* gmax) {
+                                                             int64_t ntx, int32_t* shift, const int32_t* rowx,
+                                                             int32_t* gmax) {
     const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
     int g = INT_MIN;
     if (r < rows) {
-        const int t = tmax[r];
+        int t = INT_MIN, rm = INT_MIN;
+        for (int64_t x = 0; x < ntx; ++x) {
+            const int a = tmax[x * rows + r], b = rmax[x * rows + r];
+            t = a > t ? a : t;
+            rm = b > rm ? b : rm;
+        }
         if (shift) shift[r] = t == INT_MIN ? 0 : t - kF16MaxExp;
-        const int rm = rmax[r];
         if (rm != INT_MIN) g = rm + (rowx ? rowx[r] : 0);
     }
     if (gmax) {
@@ -554,13 +555,19 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
 
 // out[c, r] = in[r, c] for r < rows, c < out_rows; zero for rows <= r < rows_pad.
 // 64 x 64 tiles; 16-byte loads along input rows, 16-byte stores along output
-// rows, the transpose done through LDS with 2-byte accesses.
-__global__ __launch_bounds__(256) void transpose_f16_kernel(const uint16_t* __restrict__ in, int64_t rows,
-                                                            int64_t cols, int64_t ld_in, uint16_t* __restrict__ out,
-                                                            int64_t out_rows, int64_t rows_pad, int64_t ld_out) {
+// rows, the transpose done through LDS with 2-byte accesses.  One launch
+// serves two independent transposes: blockIdx.y below ny0 tiles the first,
+// the rest the second (the backward's two operands; one launch less).
+__global__ __launch_bounds__(256) void transpose_f16_kernel(TransposeF16 j0, TransposeF16 j1, int ny0) {
+    const bool second = (int)blockIdx.y >= ny0;
+    const TransposeF16 j = second ? j1 : j0;
+    const uint16_t* __restrict__ in = reinterpret_cast<const uint16_t*>(j.in);
+    uint16_t* __restrict__ out = reinterpret_cast<uint16_t*>(j.out);
+    const int64_t rows = j.rows, cols = j.cols, ld_in = j.ld_in, out_rows = j.out_rows, rows_pad = j.rows_pad,
+                  ld_out = j.ld_out;
     __shared__ uint16_t tile[kTile * kTileLd];   // tile[c * kTileLd + r]
     const int tid = threadIdx.x;
-    const int64_t c0 = (int64_t)blockIdx.x * kTile, r0 = (int64_t)blockIdx.y * kTile;
+    const int64_t c0 = (int64_t)blockIdx.x * kTile, r0 = (int64_t)(second ? blockIdx.y - ny0 : blockIdx.y) * kTile;
     const bool vec_in = (ld_in % 8 == 0) && ((uintptr_t)in % 16 == 0);
 #pragma unroll
     for (int q = tid; q < kTile * 8; q += 256) {
@@ -763,32 +770,43 @@ int launch_pack_t(const PackTArgs& a, const DeviceTables& t, hipStream_t st) {
     return check_launch("pack_t");
 }
 
+int64_t row_stats_col_tiles(int64_t cols) { return (cols + kStatsCols - 1) / kStatsCols; }
+
 int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t st) {
     if (a.cols % a.block != 0)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "row_stats: cols must be a multiple of block_size");
     if ((uintptr_t)a.x % 16 != 0 || (a.colx && (uintptr_t)a.colx % 16 != 0))
         return fail(AXS6_ERR_INVALID_ARGUMENT, "row_stats: input and column exponents must be 16-byte aligned");
     if (a.rows == 0) return AXS6_OK;
-    const int64_t n = 2 * a.rows;
-    stats_init_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, st>>>(a.scratch, n, a.gmax);
-    int rc = check_launch("row_stats");
-    if (rc) return rc;
-    StatsK k{a.x, a.rows, a.cols, a.colx, a.scratch, a.scratch + a.rows, t.band};
-    const int64_t ntx = (a.cols + kStatsCols - 1) / kStatsCols, nty = (a.rows + kTile - 1) / kTile;
-    const dim3 grid((unsigned)(ntx * nty));
+    const int64_t ntx = row_stats_col_tiles(a.cols);
+    StatsK k{a.x, a.rows, a.cols, a.colx, a.scratch, a.scratch + ntx * a.rows, t.band, a.gmax};
+    // rows per tile: 16 bytes per lane, 16 (f32) or 32 (16-bit) rows per pass;
+    // as many passes as keep >= 1024 workgroups in flight, up to 4
+    const int rpp = a.dtype == AXS6_F32 ? 16 : 32;
+    auto tiles = [&](int passes) { return ntx * ((a.rows + rpp * passes - 1) / (rpp * passes)); };
+    const int passes = tiles(4) >= 1024 ? 4 : (tiles(2) >= 1024 ? 2 : 1);
+    const dim3 grid((unsigned)tiles(passes));
+#define AXS6_STATS_P(DT_, BS_)                                                                       \
+    do {                                                                                             \
+        if (passes == 4) stats_tile_kernel<DT_, BS_, 4><<<grid, 256, 0, st>>>(k, ntx);               \
+        else if (passes == 2) stats_tile_kernel<DT_, BS_, 2><<<grid, 256, 0, st>>>(k, ntx);          \
+        else stats_tile_kernel<DT_, BS_, 1><<<grid, 256, 0, st>>>(k, ntx);                           \
+    } while (0)
 #define AXS6_STATS(DT_)                                                                              \
     do {                                                                                             \
-        if (a.block == 8) stats_tile_kernel<DT_, 8><<<grid, 256, 0, st>>>(k, ntx);                   \
-        else if (a.block == 16) stats_tile_kernel<DT_, 16><<<grid, 256, 0, st>>>(k, ntx);            \
-        else stats_tile_kernel<DT_, 32><<<grid, 256, 0, st>>>(k, ntx);                               \
+        if (a.block == 8) AXS6_STATS_P(DT_, 8);                                                      \
+        else if (a.block == 16) AXS6_STATS_P(DT_, 16);                                               \
+        else AXS6_STATS_P(DT_, 32);                                                                  \
     } while (0)
     if (a.dtype == AXS6_F32) AXS6_STATS(AXS6_F32);
     else if (a.dtype == AXS6_BF16) AXS6_STATS(AXS6_BF16);
     else AXS6_STATS(AXS6_F16);
 #undef AXS6_STATS
-    if ((rc = check_launch("row_stats"))) return rc;
+#undef AXS6_STATS_P
+    int rc = check_launch("row_stats");
+    if (rc) return rc;
     stats_finalize_kernel<<<dim3((unsigned)((a.rows + 255) / 256)), 256, 0, st>>>(
-        a.scratch, a.scratch + a.rows, a.rows, a.shift, a.rowx, a.gmax);
+        a.scratch, a.scratch + ntx * a.rows, a.rows, ntx, a.shift, a.rowx, a.gmax);
     return check_launch("row_stats");
 }
 
@@ -799,12 +817,16 @@ int launch_reduce_partials(const float* partial, int64_t chunks, int64_t cols, f
     return check_launch("reduce_partials");
 }
 
-int launch_transpose_f16(const _Float16* in, int64_t rows, int64_t cols, int64_t ld_in, _Float16* out,
-                         int64_t out_rows, int64_t rows_pad, int64_t ld_out, hipStream_t st) {
-    if (out_rows == 0 || rows_pad == 0) return AXS6_OK;
-    const dim3 grid((unsigned)((out_rows + 63) / 64), (unsigned)((rows_pad + 63) / 64));
-    transpose_f16_kernel<<<grid, 256, 0, st>>>(reinterpret_cast<const uint16_t*>(in), rows, cols, ld_in,
-                                               reinterpret_cast<uint16_t*>(out), out_rows, rows_pad, ld_out);
+int launch_transpose_f16(const TransposeF16& a, const TransposeF16* b, hipStream_t st) {
+    const TransposeF16 none{nullptr, 0, 0, 0, nullptr, 0, 0, 0};
+    const TransposeF16& bb = b ? *b : none;
+    const int64_t gx_a = a.out_rows && a.rows_pad ? (a.out_rows + 63) / 64 : 0;
+    const int64_t gx_b = bb.out_rows && bb.rows_pad ? (bb.out_rows + 63) / 64 : 0;
+    const int64_t ny0 = gx_a ? (a.rows_pad + 63) / 64 : 0, ny1 = gx_b ? (bb.rows_pad + 63) / 64 : 0;
+    if (ny0 + ny1 == 0) return AXS6_OK;
+    // a tile column past one job's out_rows writes nothing for it (orow >= out_rows)
+    const dim3 grid((unsigned)(gx_a > gx_b ? gx_a : gx_b), (unsigned)(ny0 + ny1));
+    transpose_f16_kernel<<<grid, 256, 0, st>>>(ny0 ? a : bb, ny0 ? bb : a, (int)(ny0 ? ny0 : ny1));
     return check_launch("transpose_f16");
 }
 
