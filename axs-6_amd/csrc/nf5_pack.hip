@@ -21,6 +21,8 @@
 //   transpose_f16_kernel / reduce_partials_kernel / init_gmax_kernel.
 #include <limits.h>
 
+#include <type_traits>
+
 #include "nf5_device.h"
 #include "linear_internal.h"
 
@@ -279,20 +281,25 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
     const int G = (gm == INT_MIN) ? 0 : gm - kF16MaxExp;
 
     // persistent over tiles; consecutive workgroups take neighbouring column
-    // tiles of one 64-row band, so a band of x streams through once
+    // tiles of one 64-row band, so a band of x streams through once.  Tiles
+    // wholly inside x (all but the last row band and column tile) run a copy
+    // of the body without bounds tests; both copies compute the same values.
     const uint32_t kh = (uint32_t)key ^ ((uint32_t)(k.offset >> 32) * 0x9E3779B9u + (uint32_t)(key >> 32));
-    for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
-        const int64_t ty = t / ntx, tx = t - ty * ntx;
+    auto tile_body = [&](auto full_tag, int64_t ty, int64_t tx) {
+        constexpr bool FULL = decltype(full_tag)::value;
         const int64_t c0 = tx * kTile, r0 = ty * kTile;
         const int64_t c = c0 + tc * V;
-        const bool cin = c < k.cols;                // cols % block == 0: vectors are whole
+        const bool cin = FULL || c < k.cols;        // cols % block == 0: vectors are whole
+        const int64_t rt = r0 + tr;                 // this thread's row in pass 0
+        const S* xp = xs + rt * k.cols + c;
+        const int64_t x_pass = (int64_t)RPP * k.cols;
 
         u32x4 raw[PASSES];
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
-            const int64_t r = r0 + tr + RPP * p;
-            raw[p] = (cin && r < k.rows) ? *reinterpret_cast<const u32x4*>(xs + r * k.cols + c)
-                                         : u32x4{0u, 0u, 0u, 0u};
+            const int64_t r = rt + RPP * p;
+            raw[p] = (FULL || (cin && r < k.rows)) ? *reinterpret_cast<const u32x4*>(xp + p * x_pass)
+                                                   : u32x4{0u, 0u, 0u, 0u};
         }
         // per-tile operands of the two outputs, loaded once: the column
         // exponents of this thread's V columns, the rows' shifts and exponents
@@ -309,10 +316,15 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
         int shr[PASSES], shx[PASSES];
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
-            const int64_t r = r0 + tr + RPP * p;
-            shr[p] = (k.out_r && r < k.rows) ? k.shift_r[r] : 0;
-            shx[p] = (k.rowx && cin && r < k.rows) ? k.rowx[r] - G : -G;
+            const int64_t r = rt + RPP * p;
+            shr[p] = (k.out_r && (FULL || r < k.rows)) ? k.shift_r[r] : 0;
+            shx[p] = (k.rowx && cin && (FULL || r < k.rows)) ? k.rowx[r] - G : -G;
         }
+        // dither counters offset + r * cols + c (low words: pass p adds p * RPP * cols)
+        const uint32_t lo0 = (uint32_t)k.offset + (uint32_t)rt * (uint32_t)k.cols + (uint32_t)c;
+        const uint32_t lo_pass = (uint32_t)RPP * (uint32_t)k.cols;
+        _Float16* orow = k.out_r ? k.out_r + rt * k.ld_r + c : nullptr;
+        const int64_t o_pass = (int64_t)RPP * k.ld_r;
         float colsum[V];
 #pragma unroll
         for (int e = 0; e < V; ++e) colsum[e] = 0.0f;
@@ -333,7 +345,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
                 const FqScale s = fq_scale(m, band_s);
                 float d[V];
                 if constexpr (MODE == kStochastic && C32) {
-                    const uint32_t lo = (uint32_t)k.offset + (uint32_t)r * (uint32_t)k.cols + (uint32_t)c;
+                    const uint32_t lo = lo0 + (uint32_t)p * lo_pass;
 #pragma unroll
                     for (int e = 0; e < V; ++e) d[e] = dither_step32(lo + (uint32_t)e, kh);
                 } else if constexpr (MODE == kStochastic) {
@@ -346,18 +358,18 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
                 }
                 fq_vector<V>(f, s, lut_s, MODE == kStochastic, d);
             }
-            const bool live = cin && r < k.rows;
+            const bool live = FULL || (cin && r < k.rows);
             if (k.partial) {
 #pragma unroll
                 for (int e = 0; e < V; ++e) colsum[e] += live ? f[e] : 0.0f;
             }
-            if (k.out_r && r < k.rows) {
+            if (k.out_r && (FULL || r < k.rows)) {
                 // row-major operand: fp16(v * 2^(colx[c] - shift[r])), zeros in the
                 // padding columns cols <= c < 64 * ceil(cols / 64)
                 float z[V];
 #pragma unroll
                 for (int e = 0; e < V; ++e) z[e] = cin ? f[e] : 0.0f;
-                store_f16<V>(k.out_r + r * k.ld_r + c, z, -shr[p], cx);
+                store_f16<V>(orow + p * o_pass, z, -shr[p], cx);
             }
             if (k.out) {
 #pragma unroll
@@ -372,7 +384,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
             for (int e = 0; e < V; ++e) csum[tr][tc * V + e] = colsum[e];
         }
         __syncthreads();
-        if (k.partial && tid < kTile && c0 + tid < k.cols) {
+        if (k.partial && tid < kTile && (FULL || c0 + tid < k.cols)) {
             float s = 0.0f;
             for (int q = 0; q < RPP; ++q) s += csum[q][tid];
             k.partial[ty * k.cols + c0 + tid] = s;
@@ -382,12 +394,17 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
 #pragma unroll
             for (int q = tid; q < kTile * 8; q += kPackThreads) {
                 const int oc = q >> 3, j = q & 7;
-                if (c0 + oc < k.cols)
+                if (FULL || c0 + oc < k.cols)
                     *reinterpret_cast<u32x4*>(k.out + (c0 + oc) * k.ld_out + r0 + j * 8) =
                         *reinterpret_cast<const u32x4*>(&tile[oc * kTileLd + j * 8]);
             }
         }
-        __syncthreads();   // tile and csum are rewritten by the next iteration
+        __syncthreads();   // tile and csum are rewritten by the next tile
+    };
+    for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+        const int64_t ty = t / ntx, tx = t - ty * ntx;
+        if ((ty + 1) * kTile <= k.rows && (tx + 1) * kTile <= k.cols) tile_body(std::true_type{}, ty, tx);
+        else tile_body(std::false_type{}, ty, tx);
     }
 }
 
@@ -494,25 +511,50 @@ __global__ __launch_bounds__(256) void stats_tile_kernel(StatsK k, int64_t ntx) 
     }
 }
 
+// A workgroup folds 64 rows: wave w takes the column tiles w, w + 4, ...
+// (eight loads in flight per lane), the four waves meet in LDS.
+constexpr int kFinRows = 64;
+
 __global__ __launch_bounds__(256) void stats_finalize_kernel(const int32_t* __restrict__ tmax,
                                                              const int32_t* __restrict__ rmax, int64_t rows,
                                                              int64_t ntx, int32_t* shift, const int32_t* rowx,
                                                              int32_t* gmax) {
-    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    int g = INT_MIN;
+    __shared__ int part[2][4][kFinRows];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t r = (int64_t)blockIdx.x * kFinRows + lane;
+    int t = INT_MIN, rm = INT_MIN;
     if (r < rows) {
-        int t = INT_MIN, rm = INT_MIN;
-        for (int64_t x = 0; x < ntx; ++x) {
+        int64_t x = w;
+        for (; x + 28 < ntx; x += 32) {
+            int a[8], b[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) { a[u] = tmax[(x + 4 * u) * rows + r]; b[u] = rmax[(x + 4 * u) * rows + r]; }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) { t = a[u] > t ? a[u] : t; rm = b[u] > rm ? b[u] : rm; }
+        }
+        for (; x < ntx; x += 4) {
             const int a = tmax[x * rows + r], b = rmax[x * rows + r];
             t = a > t ? a : t;
             rm = b > rm ? b : rm;
+        }
+    }
+    part[0][w][lane] = t;
+    part[1][w][lane] = rm;
+    __syncthreads();
+    if (w != 0) return;
+    int g = INT_MIN;
+    if (r < rows) {
+#pragma unroll
+        for (int v = 1; v < 4; ++v) {
+            t = part[0][v][lane] > t ? part[0][v][lane] : t;
+            rm = part[1][v][lane] > rm ? part[1][v][lane] : rm;
         }
         if (shift) shift[r] = t == INT_MIN ? 0 : t - kF16MaxExp;
         if (rm != INT_MIN) g = rm + (rowx ? rowx[r] : 0);
     }
     if (gmax) {
         g = wave_max_i32(g);
-        if ((threadIdx.x & 63) == 0 && g != INT_MIN) atomicMax(gmax, g);
+        if (lane == 0 && g != INT_MIN) atomicMax(gmax, g);
     }
 }
 
@@ -805,7 +847,7 @@ int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t s
 #undef AXS6_STATS_P
     int rc = check_launch("row_stats");
     if (rc) return rc;
-    stats_finalize_kernel<<<dim3((unsigned)((a.rows + 255) / 256)), 256, 0, st>>>(
+    stats_finalize_kernel<<<dim3((unsigned)((a.rows + kFinRows - 1) / kFinRows)), 256, 0, st>>>(
         a.scratch, a.scratch + ntx * a.rows, a.rows, ntx, a.shift, a.rowx, a.gmax);
     return check_launch("row_stats");
 }
