@@ -106,6 +106,32 @@ extern "C" int axs6_gemm_f16_nt(const void* a, int64_t lda, const void* b, int64
     return launch_gemm_f16(g, (hipStream_t)stream);
 }
 
+extern "C" int64_t axs6_nf5_row_stats_workspace(int64_t rows, int64_t cols) {
+    if (rows < 0 || cols < 0) return 0;
+    return 2 * (int64_t)sizeof(int32_t) * row_stats_col_tiles(cols) * rows;
+}
+
+extern "C" int axs6_nf5_row_stats(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
+                                  const int32_t* col_exp, int32_t* row_shift, const int32_t* row_exp, int32_t* gmax,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+    const char* fn = "axs6_nf5_row_stats";
+    if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
+    if (!valid_block(block_size))
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: block_size must be 8, 16 or 32 (got %d)", fn, block_size);
+    if (rows < 0 || cols < 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: negative dimension", fn);
+    if (rows == 0 || cols == 0) return AXS6_OK;
+    if (!x || (!row_shift && !gmax)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    const int64_t need = axs6_nf5_row_stats_workspace(rows, cols);
+    if (!workspace || (int64_t)workspace_bytes < need || (uintptr_t)workspace % 16)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: workspace of %lld bytes (16-byte aligned) required", fn,
+                    (long long)need);
+    DeviceTables t;
+    int rc = device_tables(&t);
+    if (rc) return rc;
+    RowStatsArgs s{x, dtype, rows, cols, block_size, col_exp, row_shift, row_exp, gmax, (int32_t*)workspace};
+    return launch_row_stats(s, t, (hipStream_t)stream);
+}
+
 extern "C" int axs6_nf5_linear_forward(const void* x, const void* w, const float* bias, void* y, int32_t dtype,
                                        int64_t M, int64_t N, int64_t K, int32_t block_size,
                                        int32_t quantize_input, void* xq_f16, int32_t* x_shift, void* wq_f16,

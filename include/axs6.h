@@ -146,6 +146,22 @@ int axs6_nf5_pack_rows(const void* x, int32_t dtype, int64_t rows, int64_t cols,
                        void* out_f16, int64_t ld_out, int64_t cols_pad, int32_t* row_shift,
                        const uint64_t* seed_dev, void* stream);
 
+/* Packing statistics of x [rows, cols] (cols % block_size == 0, 16-byte
+ * aligned) without packing it: row_shift[r] = S[r] of axs6_nf5_pack_rows
+ * (the largest exponent e1 of a finite nonzero block of row r plus the
+ * largest col_exp over the block's columns, minus 15; 0 for a row without
+ * such a block; col_exp may be NULL) and *gmax = max over rows of (largest
+ * e1 + row_exp[r]) (INT_MIN when no block qualifies; row_exp may be NULL).
+ * Streams the tensor in tiles instead of one workgroup per row.  The first
+ * pass of the backward's dY packing (the row maxima the reference's
+ * fused_fake_quantize takes per block, axs/unified/quantize_unified.py:
+ * 167-175), exported so its results can be checked against
+ * axs6_nf5_pack_rows; workspace: axs6_nf5_row_stats_workspace bytes. */
+int64_t axs6_nf5_row_stats_workspace(int64_t rows, int64_t cols);
+int axs6_nf5_row_stats(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
+                       const int32_t* col_exp, int32_t* row_shift, const int32_t* row_exp, int32_t* gmax,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* out[M, N] = ldexp(A[M, Kp] . B[N, Kp]^T, row_exp[m] + col_exp[n]) + bias[n]
  * with fp16 A, B (16-byte aligned, lda/ldb multiples of 8, Kp % 64 == 0),
  * fp32 accumulation, out in out_dtype (row_exp, col_exp, bias may be NULL).

@@ -9,9 +9,12 @@ FQ(x) (mode 1, fused_fake_quantize, quantize_unified.py:121-204) or x itself
 (mode 0).  The expected bits are built here from the oracle's FQ values and
 exponents with numpy's correctly rounded float32 ldexp and float16 casts; the
 kernel must match them exactly.  Row widths cover every launch shape of the
-packing kernel (one wave per row, 256/512/1024 threads per row, and the
-two-rows-per-workgroup prefetch of long rows), with odd row counts so a
-workgroup is left with a single row.
+packing kernel (one wave per row; 256, 512 and 768 threads per row), with odd
+row counts so a workgroup is left with a single row.
+
+The same S (with column exponents) and the tensor-wide maximum come from the
+tiled statistics pass of the backward (`axs6_nf5_row_stats`), at row counts
+and widths that exercise its 16-, 32- and 64-row tiles and ragged edges.
 """
 from __future__ import annotations
 
@@ -80,8 +83,6 @@ def _assert_bits(got: np.ndarray, want: np.ndarray, what: str):
     assert bad.size == 0, f"{what}: {bad.size} values differ, first {g[bad[:4]]} vs {w[bad[:4]]}"
 
 
-# f32 row widths: 8, 64, 128 and 256 vectors (one wave per row), 512 and 1024
-# (256 threads), 1536 (512 threads, prefetch), 2752 and 4096 (1024 threads, prefetch)
 # row lengths cover every thread shape of the kernel (one wave per row; 256 x
 # 2/4/8, 768 x 4, 512 x 8 threads x vectors) and the boundaries between them
 @pytest.mark.parametrize("cols", [32, 256, 512, 1024, 2048, 4096, 6144, 8192, 8224, 11008, 12288, 12320, 16384])
@@ -119,3 +120,51 @@ def test_pack_rows_raw_mode_bitexact(cols):
     want, wshift = _expected(x, 0, cols_pad)
     assert np.array_equal(shift, wshift)
     _assert_bits(got, want, f"raw 21x{cols}")
+
+
+def _stats_expected(x: np.ndarray, colx: np.ndarray, rowx: np.ndarray):
+    rows, cols = x.shape
+    a = np.abs(x).reshape(rows, cols // BS, BS)
+    with np.errstate(invalid="ignore"):
+        amax = a.max(axis=2)
+    finite = np.isfinite(amax) & (amax > 0)
+    e1 = oracle.floor_log2(np.where(finite, amax, 1.0)).astype(np.int64) + 1
+    ok = finite & (e1 < 128)
+    lo = np.iinfo(np.int64).min // 2
+    cblk = colx.astype(np.int64).reshape(cols // BS, BS).max(axis=1)
+    tmax = np.where(ok, e1 + cblk[None, :], lo).max(axis=1)
+    shift = np.where(tmax == lo, 0, tmax - 15).astype(np.int32)
+    rmax = np.where(ok, e1, lo).max(axis=1)
+    g = np.where(rmax == lo, lo, rmax + rowx.astype(np.int64)).max()
+    return shift, (np.iinfo(np.int32).min if g == lo else int(g))
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [(37, 256, torch.float32), (37, 11008, torch.float32),
+                                             (300, 1056, torch.float32), (64, 4096, torch.bfloat16),
+                                             (50, 11008, torch.bfloat16), (8192, 11008, torch.float32),
+                                             (8192, 1024, torch.float32), (129, 16416, torch.float16)], ids=str)
+def test_row_stats_bitexact(rows, cols, dtype):
+    from axs import _lib
+
+    print(f"[row_stats {dtype} {rows}x{cols}]", flush=True)
+    rng = np.random.default_rng(rows + cols)
+    x = torch.from_numpy(_data(rows, cols, 3 + cols)).to(dtype)
+    xf = x.float().numpy()
+    colx = rng.integers(-3, 4, cols).astype(np.int32)
+    rowx = rng.integers(-5, 6, rows).astype(np.int32)
+    want_shift, want_g = _stats_expected(xf, colx, rowx)
+    xd, cd, rd = x.to(DEV), torch.from_numpy(colx).to(DEV), torch.from_numpy(rowx).to(DEV)
+    ws = torch.empty(_lib.lib().axs6_nf5_row_stats_workspace(rows, cols), dtype=torch.uint8, device=DEV)
+    shift = torch.full((rows,), -12345, dtype=torch.int32, device=DEV)
+    g = torch.full((1,), 777, dtype=torch.int32, device=DEV)
+    _lib.call("axs6_nf5_row_stats", xd.data_ptr(), _lib.DTYPE_CODE[dtype], rows, cols, BS, cd.data_ptr(),
+              shift.data_ptr(), rd.data_ptr(), g.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(xd))
+    torch.cuda.synchronize()
+    assert np.array_equal(shift.cpu().numpy(), want_shift)
+    assert g.item() == want_g
+    # without column exponents: the row pack's S
+    _lib.call("axs6_nf5_row_stats", xd.data_ptr(), _lib.DTYPE_CODE[dtype], rows, cols, BS, None,
+              shift.data_ptr(), None, None, ws.data_ptr(), ws.numel(), _lib.stream_of(xd))
+    torch.cuda.synchronize()
+    _, pack_shift = _pack(xd, 0, (cols + 63) // 64 * 64)
+    assert np.array_equal(shift.cpu().numpy(), pack_shift)
