@@ -583,7 +583,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(SplitReduceK k) {
 // all on 32x32x16 MFMAs; on 16x16x32 MFMAs:
 //   9: 256x256 / 64 / 2 / 8 / 2, waves 0-3 issue all slab loads
 //  10: 128x128 / 64 / 2 / 4 / 2     11: 9 with every wave loading
-// Default: 9, or 10 when the 256x256 tiles do not cover the 256 CUs once.
+//  12: 128x64 / 64 / 2 / 4 / 2
+// Default: 9; 10 when the 256x256 tiles do not cover the 256 CUs once; 12
+// when the 128x128 ones do not either (8192 x 256 outputs: 128 -> 256
+// workgroups, 9.7 -> 7.5 us at K 256, 15.1 -> 11.0 us at K 1024; 2048 x 768
+// at K 3072 34.5 -> 29.3 us; where 128x128 tiles already fill the CUs,
+// 128x64 ones are up to 11% slower).
 // 16x16x32 against 32x32x16 (11 against 0, 10 against 8): 0-5% shorter on
 // every shape tried (4096^3, the Llama-7B MLP shapes, the 768/3072 ones).
 // Loads from waves 0-3 only (9 against 11): 6-12% shorter on the large
@@ -600,13 +605,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(SplitReduceK k) {
 // when 32 CUs carry it; 128x128 tiles spread it over 4x the CUs, two
 // workgroups sharing a CU.  AXS6_GEMM_CFG=<n> forces a configuration for
 // launch-shape sweeps.
-constexpr int kCfgBig = 9, kCfgSmall = 10;
+constexpr int kCfgBig = 9, kCfgSmall = 10, kCfgNarrow = 12;
 
 int gemm_cfg_env() {
     static int v = [] {
         const char* s = getenv("AXS6_GEMM_CFG");
         int n = s ? atoi(s) : -1;
-        return (n >= 0 && n <= 11) ? n : -1;
+        return (n >= 0 && n <= 12) ? n : -1;
     }();
     return v;
 }
@@ -616,10 +621,17 @@ int64_t tiles_of(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / 
 int pick_cfg(int64_t M, int64_t N) {
     const int env = gemm_cfg_env();
     if (env >= 0) return env;
-    return tiles_of(M, N, 256, 256) < 256 ? kCfgSmall : kCfgBig;
+    if (tiles_of(M, N, 256, 256) >= 256) return kCfgBig;
+    return tiles_of(M, N, 128, 128) >= 256 ? kCfgSmall : kCfgNarrow;
 }
 
-bool is_small_cfg(int cfg) { return cfg == 8 || cfg == 10; }
+// output tile of a configuration
+void cfg_tile(int cfg, int* bm, int* bn) {
+    *bm = 256; *bn = 256;
+    if (cfg == 7) *bn = 128;
+    if (cfg == 8 || cfg == 10) *bm = *bn = 128;
+    if (cfg == kCfgNarrow) { *bm = 128; *bn = 64; }
+}
 
 // configuration of a split-K launch: one with 64-half K-slabs (the split
 // ranges are counted in them); forced sweep configurations with 32-half
@@ -630,8 +642,9 @@ int split_cfg(int cfg) { return (cfg == 0 || cfg >= 8) ? cfg : kCfgBig; }
 
 int gemm_split_count(int64_t M, int64_t N, int64_t Kp) {
     // split launches use configurations with 64-half K-slabs (split_cfg)
-    const bool small = is_small_cfg(split_cfg(pick_cfg(M, N)));
-    const int64_t tiles = small ? tiles_of(M, N, 128, 128) : tiles_of(M, N, 256, 256);
+    int bm, bn;
+    cfg_tile(split_cfg(pick_cfg(M, N)), &bm, &bn);
+    const int64_t tiles = tiles_of(M, N, bm, bn);
     const int64_t iters = Kp / kGemmK;
     if (tiles >= 64 || iters < 8) return 1;
     int64_t s = iters / 4;                                   // at least 4 K-steps per split
@@ -687,6 +700,7 @@ int launch_gemm_f16(const GemmArgs& a, hipStream_t st) {
         case kCfgSmall: rc = run_gemm_lds<128, 128, 64, 2, 2, 2, 2, 16>(k, splits, st); break;
         case 0: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2>(k, splits, st); break;
         case 11: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2, 16>(k, splits, st); break;
+        case kCfgNarrow: rc = run_gemm_lds<128, 64, 64, 2, 2, 2, 2, 16, 4>(k, splits, st); break;
         default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2, 16, 4>(k, splits, st); break;   // kCfgBig
     }
     if (rc || !split) return rc;
