@@ -661,7 +661,42 @@ size_t gemm_split_bytes(int64_t M, int64_t N, int64_t Kp) {
     return s > 1 ? (size_t)s * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
-int launch_gemm_f16(const GemmArgs& a, hipStream_t st) {
+namespace {
+
+// The last round of 256x256 tiles.  With 256 CUs and one tile per CU, an
+// output of R full rounds plus r < 128 tiles takes R + 1 rounds while the
+// r tiles leave most CUs idle.  Such a launch is cut along whichever
+// dimension leaves a multiple of 256 tiles in the first part: that part
+// runs as before, the remainder as a separate launch with its own
+// configuration (128x128 tiles).  8192 x 11008 (K 4096): 1376 tiles =
+// 5 rounds + 96 -> 1280 tiles + an 8192 x 768 remainder, 617 -> 607 us on
+// packed operands (the remainder's 384 small tiles, 1.5 per CU, take ~85 us
+// against the ~20 us their FLOPs would take at the large tiles' rate).
+// Returns the cut (rows or columns, 0 for none).
+struct TailCut { int64_t rows = 0, cols = 0; };
+
+TailCut tail_cut(int64_t M, int64_t N) {
+    TailCut c;
+    const int64_t tm = (M + 255) / 256, tn = (N + 255) / 256, tiles = tm * tn;
+    if (tiles < 256 || tiles % 256 == 0 || tiles % 256 > 128) return c;
+    int64_t best = 0;
+    for (int64_t n1 = tn - 1; n1 >= 1; --n1)
+        if ((tm * n1) % 256 == 0) { best = tm * n1; c.cols = n1 * 256; break; }
+    for (int64_t m1 = tm - 1; m1 >= 1; --m1)
+        if ((m1 * tn) % 256 == 0) {
+            if (m1 * tn > best) { c.cols = 0; c.rows = m1 * 256; }
+            break;
+        }
+    return c;
+}
+
+}  // namespace
+
+static int launch_gemm_one(const GemmArgs& a, hipStream_t st, bool cut);
+
+int launch_gemm_f16(const GemmArgs& a, hipStream_t st) { return launch_gemm_one(a, st, true); }
+
+static int launch_gemm_one(const GemmArgs& a, hipStream_t st, bool cut) {
     if (a.M == 0 || a.N == 0) return AXS6_OK;
     if (a.Kp % 64 != 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: Kp (%lld) must be a multiple of 64", (long long)a.Kp);
     if (a.lda % 8 || a.ldb % 8 || (uintptr_t)a.A % 16 || (uintptr_t)a.B % 16)
@@ -672,6 +707,32 @@ int launch_gemm_f16(const GemmArgs& a, hipStream_t st) {
         return fail(AXS6_ERR_UNSUPPORTED, "gemm: operand larger than 2 GiB");
     if (a.M > INT_MAX || a.N > INT_MAX || a.Kp > INT_MAX)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: dimension exceeds int32");
+    if (cut && gemm_cfg_env() < 0) {
+        const TailCut c = tail_cut(a.M, a.N);
+        if (c.rows || c.cols) {
+            const int esize = a.out_dtype == AXS6_F32 ? 4 : 2;
+            GemmArgs head = a, tail = a;
+            // both parts have enough tiles for one workgroup per CU: no split-K
+            head.split_partial = tail.split_partial = nullptr;
+            head.split_bytes = tail.split_bytes = 0;
+            if (c.cols) {
+                head.N = c.cols;
+                tail.N = a.N - c.cols;
+                tail.B = a.B + c.cols * a.ldb;
+                if (a.col_exp) tail.col_exp = a.col_exp + c.cols;
+                if (a.bias) tail.bias = a.bias + c.cols;
+                tail.out = (char*)a.out + c.cols * esize;
+            } else {
+                head.M = c.rows;
+                tail.M = a.M - c.rows;
+                tail.A = a.A + c.rows * a.lda;
+                if (a.row_exp) tail.row_exp = a.row_exp + c.rows;
+                tail.out = (char*)a.out + c.rows * a.ldo * esize;
+            }
+            const int rc = launch_gemm_one(head, st, false);
+            return rc ? rc : launch_gemm_one(tail, st, false);
+        }
+    }
     const int iters = (int)(a.Kp / kGemmK);
     int splits = 1, per = iters;
     if (a.split_partial) {

@@ -93,6 +93,25 @@ def test_gemm_epilogue_ragged_and_strided_output(N, ldo, offset):
         assert bool((untouched == 7.0).all()), f"{dt}: wrote outside the output rows"
 
 
+@pytest.mark.parametrize("M,N", [(8192, 11008), (11008, 2048)], ids=["column_cut", "row_cut"])
+def test_gemm_tail_cut_exact(M, N):
+    """Outputs whose 256x256 tiles leave a small last round run as two
+    launches (a multiple of 256 tiles, then the remainder with smaller
+    tiles), cut along columns (8192 x 11008) or rows (11008 x 2048); the
+    exponents, bias and output pointers of the second part are offsets of
+    the first's.  Exact on small integers, every element checked."""
+    Kp = 64
+    g = torch.Generator().manual_seed(M + N)
+    A = torch.randint(-4, 5, (M, Kp), generator=g).to(torch.float16)
+    B = torch.randint(-4, 5, (N, Kp), generator=g).to(torch.float16)
+    re = torch.randint(-6, 6, (M,), generator=g, dtype=torch.int32)
+    ce = torch.randint(-6, 6, (N,), generator=g, dtype=torch.int32)
+    bias = torch.randint(-8, 9, (N,), generator=g).float()
+    want = ((A.double() @ B.double().T) * torch.exp2((re[:, None] + ce[None, :]).double())).float() + bias
+    got = _gemm(A.to(DEV), B.to(DEV), M, N, Kp, re.to(DEV), ce.to(DEV), bias.to(DEV)).cpu()
+    assert torch.equal(got, want)
+
+
 def _oracle_linear(x, w, b):
     xq = oracle.fake_quantize(x.numpy(), 32)
     wq = oracle.fake_quantize(w.numpy(), 32)
