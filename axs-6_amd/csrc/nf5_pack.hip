@@ -17,7 +17,15 @@
 //   pack_t_kernel       64 x 64 tiles, one tensor-wide scale (read from a
 //                       device scalar), written transposed: backward dY ->
 //                       the dW operand [N, Mp] directly, plus fixed-order
-//                       column partial sums for the bias gradient.
+//                       column partial sums for the bias gradient; and/or
+//                       the row-major operand with row shifts computed
+//                       beforehand (backward dY -> the dX operand; forward
+//                       rows too long for pack_rows_kernel's registers).
+//   stats_tile_kernel + stats_finalize_kernel
+//                       row shifts and the tensor-wide exponent, streamed
+//                       over 2-D tiles (the backward's dY).
+//   stats_row_kernel    row shifts of rows too long for pack_rows_kernel,
+//                       one workgroup streaming each row.
 //   transpose_f16_kernel / reduce_partials_kernel / init_gmax_kernel.
 #include <limits.h>
 
@@ -408,6 +416,95 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
     }
 }
 
+// Rows longer than pack_rows_kernel holds in registers take two launches: this
+// kernel, one workgroup per row streaming it (U 16-byte vectors in flight per
+// thread), writes what pack_rows writes besides the packed values -- s_out,
+// rmax_out, gmax -- and the zero columns of `out` from 64 * ceil(cols / 64) to
+// cols_pad; then pack_t_kernel writes the row-major operand (values and the
+// zero columns up to 64 * ceil(cols / 64)) with these shifts.  The shift rule
+// is pack_rows_kernel's: S = max over the row's finite nonzero blocks of
+// (e1 + colx[c]) - 15, 0 if there is none.
+template <int DT, int BS>
+__global__ __launch_bounds__(256) void stats_row_kernel(PackRowsK k) {
+    using E = Elem<DT>;
+    using S = typename E::S;
+    constexpr int V = E::V;
+    constexpr int G = BS / V > 0 ? BS / V : 1;     // lanes per NF5 block
+    constexpr int U = 4;
+    __shared__ uint32_t band_w[kBandSize / 4];
+    __shared__ int red[2][4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid < kBandSize / 4) band_w[tid] = reinterpret_cast<const uint32_t*>(k.band)[tid];
+    __syncthreads();
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+    const int64_t r = blockIdx.x;
+    const int64_t nvec = k.cols / V;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(reinterpret_cast<const S*>(k.x) + r * k.cols);
+
+    int tm = INT_MIN, rm = INT_MIN;
+    for (int64_t v0 = 0; v0 < nvec; v0 += 256 * U) {
+        u32x4 raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t vi = v0 + u * 256 + tid;
+            raw[u] = vi < nvec ? xr[vi] : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t vi = v0 + u * 256 + tid;
+            float f[V];
+            E::unpack(raw[u], f);
+            uint32_t m = 0;
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const uint32_t a = __float_as_uint(f[e]) & 0x7fffffffu;
+                m = m > a ? m : a;
+            }
+            // a block is G whole vectors at a multiple of G, so its lanes are
+            // all inside the row or all past its end
+            m = group_umax<G>(m);
+            const FqScale s = fq_scale(m, band_s);
+            if (vi < nvec && !(s.nan_block || s.inf_scale || m == 0u)) {
+                rm = s.e1 > rm ? s.e1 : rm;
+                int cm = 0;
+                if (k.colx) {
+                    cm = INT_MIN;
+#pragma unroll
+                    for (int h = 0; h < V / 4; ++h) {
+                        const u32x4 c4 = *(reinterpret_cast<const u32x4*>(k.colx + vi * V) + h);
+                        const int a = (int)c4.x > (int)c4.y ? (int)c4.x : (int)c4.y;
+                        const int b = (int)c4.z > (int)c4.w ? (int)c4.z : (int)c4.w;
+                        const int ab = a > b ? a : b;
+                        cm = ab > cm ? ab : cm;
+                    }
+                }
+                const int t = s.e1 + cm;
+                tm = t > tm ? t : tm;
+            }
+        }
+    }
+    tm = wave_max_i32(tm);
+    rm = wave_max_i32(rm);
+    if (lane == 0) { red[0][wave] = tm; red[1][wave] = rm; }
+    if (k.out) {
+        _Float16* orow = k.out + r * k.ld_out;
+        const int64_t z0 = ((k.cols + kTile - 1) / kTile) * kTile / 8, z1 = k.cols_pad / 8;   // 8-half chunks
+        for (int64_t z = z0 + tid; z < z1; z += 256) *reinterpret_cast<u32x4*>(orow + z * 8) = u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+    if (tid == 0) {
+        tm = red[0][0]; rm = red[1][0];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            tm = red[0][w] > tm ? red[0][w] : tm;
+            rm = red[1][w] > rm ? red[1][w] : rm;
+        }
+        k.s_out[r] = tm == INT_MIN ? 0 : tm - kF16MaxExp;
+        if (k.rmax_out) k.rmax_out[r] = rm;
+        if (k.gmax && rm != INT_MIN) atomicMax(k.gmax, rm + (k.rowx ? k.rowx[r] : 0));
+    }
+}
+
 // Row statistics of x for the packing shifts (block exponents only, no FQ
 // values), streamed over tiles of RPP*PASSES rows x 256 columns.  For the
 // blocks with a finite nonzero scale 2^e1 (every FQ value of the block is at
@@ -743,9 +840,15 @@ int check_pack_rows(const PackRowsArgs& a, RowsShape* sh_out) {
     if (a.out && (a.ld_out % 8 != 0 || (uintptr_t)a.out % 16 != 0 || a.cols_pad % 8 != 0 || a.cols_pad < a.cols))
         return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: output must be 16-byte aligned with padded width >= cols");
     const int64_t nvec = a.cols / V;
-    if (nvec > kRowsMaxVec)
-        return fail(AXS6_ERR_UNSUPPORTED, "pack_rows: rows of %lld elements exceed the register-resident limit (%lld)",
-                    (long long)a.cols, (long long)(kRowsMaxVec * V));
+    if (nvec > kRowsMaxVec) {
+        // longer than a workgroup holds in registers: statistics pass + tiled pack
+        if (a.out && a.cols_pad < pad_to(a.cols, kTile))
+            return fail(AXS6_ERR_UNSUPPORTED, "pack_rows: rows of more than %lld elements need cols_pad >= "
+                        "64 * ceil(cols / 64) (got cols %lld, cols_pad %lld)", (long long)(kRowsMaxVec * V),
+                        (long long)a.cols, (long long)a.cols_pad);
+        *sh_out = RowsShape{0, 0};
+        return AXS6_OK;
+    }
     *sh_out = rows_shape(nvec);
     return AXS6_OK;
 }
@@ -757,6 +860,29 @@ PackRowsK to_kernel_args(const PackRowsArgs& a, const DeviceTables& t) {
 
 int pack_mode(const PackRowsArgs& a) { return a.fake_quant ? (a.stochastic ? kStochastic : kNearest) : kRaw; }
 
+// Rows past the register-resident limit: the statistics of each row from
+// stats_row_kernel, then the row-major operand from pack_t_kernel with those
+// shifts (same FQ values and dither counters as pack_rows_kernel).
+int launch_pack_rows_long(const PackRowsArgs& a, const DeviceTables& t, hipStream_t st) {
+    const PackRowsK k = to_kernel_args(a, t);
+    const dim3 grid((unsigned)a.rows);
+#define AXS6_STATS_ROW(DT_)                                                                         \
+    do {                                                                                            \
+        if (a.block == 8) stats_row_kernel<DT_, 8><<<grid, 256, 0, st>>>(k);                        \
+        else if (a.block == 16) stats_row_kernel<DT_, 16><<<grid, 256, 0, st>>>(k);                 \
+        else stats_row_kernel<DT_, 32><<<grid, 256, 0, st>>>(k);                                    \
+    } while (0)
+    if (a.dtype == AXS6_F32) AXS6_STATS_ROW(AXS6_F32);
+    else if (a.dtype == AXS6_BF16) AXS6_STATS_ROW(AXS6_BF16);
+    else AXS6_STATS_ROW(AXS6_F16);
+#undef AXS6_STATS_ROW
+    int rc = check_launch("pack_rows");
+    if (rc || !a.out) return rc;
+    const PackTArgs p{a.x, a.dtype, a.rows, a.cols, a.block, a.fake_quant, a.stochastic, a.seed, a.offset,
+                      a.seed_dev, nullptr, nullptr, nullptr, 0, a.out, a.ld_out, a.colx, a.s_out, nullptr};
+    return launch_pack_t(p, t, st);
+}
+
 }  // namespace
 
 int launch_pack_rows(const PackRowsArgs& a, const DeviceTables& t, hipStream_t st) {
@@ -764,6 +890,7 @@ int launch_pack_rows(const PackRowsArgs& a, const DeviceTables& t, hipStream_t s
     int rc = check_pack_rows(a, &sh);
     if (rc) return rc;
     if (a.rows == 0) return AXS6_OK;
+    if (sh.nt == 0) return launch_pack_rows_long(a, t, st);
     const PackRowsK k = to_kernel_args(a, t);
     const bool colx = a.colx != nullptr;
     if (a.dtype == AXS6_F32) dispatch_rows<AXS6_F32>(k, k, a.rows, pack_mode(a), colx, sh, st);
@@ -777,8 +904,8 @@ int launch_pack_rows2(const PackRowsArgs& a, const PackRowsArgs& b, const Device
     int rc = check_pack_rows(a, &sa);
     if (rc) return rc;
     if ((rc = check_pack_rows(b, &sb))) return rc;
-    const bool same = a.dtype == b.dtype && pack_mode(a) == pack_mode(b) && sa.nt == sb.nt && sa.nv == sb.nv &&
-                      (a.colx != nullptr) == (b.colx != nullptr);
+    const bool same = sa.nt != 0 && a.dtype == b.dtype && pack_mode(a) == pack_mode(b) && sa.nt == sb.nt &&
+                      sa.nv == sb.nv && (a.colx != nullptr) == (b.colx != nullptr);
     if (!same || a.rows == 0 || b.rows == 0) {
         if ((rc = launch_pack_rows(a, t, st))) return rc;
         return launch_pack_rows(b, t, st);

@@ -139,7 +139,9 @@ int64_t axs6_linear_padded_k(int64_t k);
  * mode 0 = values as given, 1 = NF5 FQ nearest, 2 = NF5 FQ stochastic;
  * out_f16[r, c] = fp16(v * 2^(col_exp[c] - row_shift[r])) for c < cols, zero up
  * to cols_pad (out_f16 may be NULL to compute row_shift only; col_exp may be
- * NULL).  The FQ(x) + fp16-operand half of the fused Triton linear's tile
+ * NULL).  Rows longer than 16384 f32 / 32768 16-bit values are packed in two
+ * passes and need cols_pad >= 64 * ceil(cols / 64) (else
+ * AXS6_ERR_UNSUPPORTED).  The FQ(x) + fp16-operand half of the fused Triton linear's tile
  * prologue (axs/unified/triton_kernels.py:152-180), run once per operand. */
 int axs6_nf5_pack_rows(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
                        int32_t mode, uint64_t seed, uint64_t offset, const int32_t* col_exp,

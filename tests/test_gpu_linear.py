@@ -118,8 +118,10 @@ def _oracle_linear(x, w, b):
     return xq, wq, oracle.linear_reference(xq, wq, None if b is None else b.numpy())
 
 
+# K 20000 (f32) is past the row pack's register-resident length: statistics
+# pass + tiled pack
 @pytest.mark.parametrize("M,K,N", [(64, 256, 128), (100, 96, 64), (2048, 768, 3072), (2048, 3072, 768),
-                                   (4096, 4096, 4096)])
+                                   (4096, 4096, 4096), (64, 20000, 96)])
 def test_linear_forward_vs_oracle(M, K, N):
     from axs.unified import hip_linear
 
@@ -151,11 +153,12 @@ def test_linear_forward_config4_rows(M, K, N):
     assert err < TOL
 
 
-# The last three shapes run split-K GEMMs: dW of one 256x256 tile over 128
-# K-steps (32 splits); dW over a ragged 5000-row contraction (16 uneven
-# splits); dX of one tile over a 4096-wide contraction (16 splits).
+# Three shapes run split-K GEMMs: dW of one 256x256 tile over 128 K-steps (32
+# splits); dW over a ragged 5000-row contraction (16 uneven splits); dX of one
+# tile over a 4096-wide contraction (16 splits).  K 20000 packs its forward
+# operands in two passes (rows past the register-resident length).
 @pytest.mark.parametrize("M,K,N", [(64, 256, 128), (100, 96, 64), (2048, 768, 3072), (2048, 3072, 768),
-                                   (8192, 256, 256), (5000, 160, 96), (256, 256, 4096)])
+                                   (8192, 256, 256), (5000, 160, 96), (256, 256, 4096), (96, 20000, 64)])
 @pytest.mark.parametrize("qgrad", [False, True], ids=["exact_dy", "stochastic_dy"])
 def test_linear_backward_vs_oracle(M, K, N, qgrad):
     from axs.unified import hip_linear

@@ -44,32 +44,39 @@ def _data(rows: int, cols: int, seed: int) -> np.ndarray:
     return x
 
 
-def _expected(x: np.ndarray, mode: int, cols_pad: int) -> tuple[np.ndarray, np.ndarray]:
+def _expected(x: np.ndarray, mode: int, cols_pad: int, colx: np.ndarray | None = None,
+              u: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """Packed bits and row shifts; mode 1 FQ with nearest rounding, 2 with the
+    dither u, 0 raw; colx optional per-column exponents."""
     rows, cols = x.shape
-    v = oracle.fake_quantize(x, BS) if mode == 1 else x.astype(np.float32)
+    v = oracle.fake_quantize(x, BS, u if mode == 2 else None) if mode else x.astype(np.float32)
     a = np.abs(x).reshape(rows, cols // BS, BS)
     with np.errstate(invalid="ignore"):
         amax = a.max(axis=2)                        # NaN where the block holds a NaN
     finite = np.isfinite(amax) & (amax > 0)
     e1 = oracle.floor_log2(np.where(finite, amax, 1.0)).astype(np.int64) + 1
     ok = finite & (e1 < 128)                        # 2^e1 finite in float32
-    tmax = np.where(ok, e1, np.iinfo(np.int64).min).max(axis=1)
-    shift = np.where(tmax == np.iinfo(np.int64).min, 0, tmax - 15).astype(np.int32)
+    cx = np.zeros(cols, np.int64) if colx is None else colx.astype(np.int64)
+    cblk = cx.reshape(cols // BS, BS).max(axis=1)
+    lo = np.iinfo(np.int64).min // 2
+    tmax = np.where(ok, e1 + cblk[None, :], lo).max(axis=1)
+    shift = np.where(tmax == lo, 0, tmax - 15).astype(np.int32)
     with np.errstate(over="ignore", invalid="ignore"):
-        scaled = np.ldexp(v.astype(np.float32), (-shift.astype(np.int64))[:, None]).astype(np.float32)
+        scaled = np.ldexp(v.astype(np.float32), cx[None, :] - shift.astype(np.int64)[:, None]).astype(np.float32)
         packed = np.zeros((rows, cols_pad), np.float16)
         packed[:, :cols] = scaled.astype(np.float16)
     return packed, shift
 
 
-def _pack(x: torch.Tensor, mode: int, cols_pad: int):
+def _pack(x: torch.Tensor, mode: int, cols_pad: int, colx: torch.Tensor | None = None, seed: int = 0,
+          offset: int = 0):
     from axs import _lib
 
     rows, cols = x.shape
     out = torch.full((rows, cols_pad), float("nan"), dtype=torch.float16, device=DEV)   # padding must be written
     shift = torch.full((rows,), -12345, dtype=torch.int32, device=DEV)
-    _lib.call("axs6_nf5_pack_rows", x.data_ptr(), _lib.DTYPE_CODE[x.dtype], rows, cols, BS, mode, 0, 0, None,
-              out.data_ptr(), cols_pad, cols_pad, shift.data_ptr(), None, _lib.stream_of(x))
+    _lib.call("axs6_nf5_pack_rows", x.data_ptr(), _lib.DTYPE_CODE[x.dtype], rows, cols, BS, mode, seed, offset,
+              _lib.ptr(colx), out.data_ptr(), cols_pad, cols_pad, shift.data_ptr(), None, _lib.stream_of(x))
     torch.cuda.synchronize()
     return out.cpu().numpy(), shift.cpu().numpy()
 
@@ -84,8 +91,10 @@ def _assert_bits(got: np.ndarray, want: np.ndarray, what: str):
 
 
 # row lengths cover every thread shape of the kernel (one wave per row; 256 x
-# 2/4/8, 768 x 4, 512 x 8 threads x vectors) and the boundaries between them
-@pytest.mark.parametrize("cols", [32, 256, 512, 1024, 2048, 4096, 6144, 8192, 8224, 11008, 12288, 12320, 16384])
+# 2/4/8, 768 x 4, 512 x 8 threads x vectors), the boundaries between them, and
+# rows past the register-resident 16384 (statistics pass + tiled pack)
+@pytest.mark.parametrize("cols", [32, 256, 512, 1024, 2048, 4096, 6144, 8192, 8224, 11008, 12288, 12320, 16384,
+                                  16416, 20000, 65536])
 @pytest.mark.parametrize("rows", [37, 1])
 def test_pack_rows_f32_bitexact(rows, cols):
     print(f"[pack_rows f32 {rows}x{cols}]", flush=True)
@@ -97,8 +106,8 @@ def test_pack_rows_f32_bitexact(rows, cols):
     _assert_bits(got, want, f"f32 {rows}x{cols}")
 
 
-# bf16 widths: 1376 vectors (512 threads, prefetch) and 4096 (1024 threads, prefetch)
-@pytest.mark.parametrize("cols", [256, 11008, 16384, 16416, 24576, 32768])
+# bf16 widths up to the register-resident 32768 and past it
+@pytest.mark.parametrize("cols", [256, 11008, 16384, 16416, 24576, 32768, 32800, 40000])
 def test_pack_rows_bf16_bitexact(cols):
     print(f"[pack_rows bf16 37x{cols}]", flush=True)
     xb = torch.from_numpy(_data(37, cols, 5 + cols)).to(torch.bfloat16)
@@ -120,6 +129,38 @@ def test_pack_rows_raw_mode_bitexact(cols):
     want, wshift = _expected(x, 0, cols_pad)
     assert np.array_equal(shift, wshift)
     _assert_bits(got, want, f"raw 21x{cols}")
+
+
+@pytest.mark.parametrize("cols", [4096, 12320, 20000, 40960])
+def test_pack_rows_stochastic_colx_bitexact(cols):
+    """Mode 2 (dither counters offset + r * cols + c) with per-column
+    exponents, in registers and past the register-resident length."""
+    print(f"[pack_rows stochastic colx 37x{cols}]", flush=True)
+    rng = np.random.default_rng(cols + 1)
+    x = _data(37, cols, 9 + cols)
+    colx = rng.integers(-6, 7, cols).astype(np.int32)
+    seed, offset = 0x5EED0123, 12345
+    cols_pad = (cols + 63) // 64 * 64
+    got, shift = _pack(torch.from_numpy(x).to(DEV), 2, cols_pad, torch.from_numpy(colx).to(DEV), seed, offset)
+    want, wshift = _expected(x, 2, cols_pad, colx, oracle.uniform(seed, offset, x.size).reshape(x.shape))
+    assert np.array_equal(shift, wshift)
+    _assert_bits(got, want, f"stochastic colx 37x{cols}")
+
+
+def test_pack_rows_long_padding():
+    """Past the register-resident length: zero columns up to a cols_pad beyond
+    64 * ceil(cols / 64); a cols_pad short of that is refused (the tiled pack
+    writes zeros up to it)."""
+    from axs import _lib
+
+    cols = 20000
+    x = _data(5, cols, 4)
+    got, shift = _pack(torch.from_numpy(x).to(DEV), 1, 20224)
+    want, wshift = _expected(x, 1, 20224)
+    assert np.array_equal(shift, wshift)
+    _assert_bits(got, want, "long, cols_pad 20224")
+    with pytest.raises(_lib.LibraryError, match="cols_pad"):
+        _pack(torch.from_numpy(x).to(DEV), 1, 20000)
 
 
 def _stats_expected(x: np.ndarray, colx: np.ndarray, rowx: np.ndarray):
