@@ -40,7 +40,6 @@ typedef float f32x4m __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;            // halves per K-step (8 slots of 16 bytes)
-constexpr int kRowBytes = kBK * 2;
 constexpr int kGroupM = 8;
 constexpr int kBufferConfig = 0x00020000;   // raw 32-bit buffer access, gfx9 family
 

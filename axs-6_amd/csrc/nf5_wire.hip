@@ -12,8 +12,16 @@
 // _pack_gradient (:70-115), i.e. quantize_unified with nearest rounding.
 //
 // One thread handles one group of four values (three bytes); a block is
-// bs/4 neighbouring lanes, whose amax is a DPP reduction.  Byte traffic is
-// small next to the 4 B/value read, so the stores stay byte-granular.
+// bs/4 neighbouring lanes, whose amax is a DPP reduction.
+//
+// Fast path (cols % bs == 0, so the blocks tile the flattened tensor, and
+// aligned pointers): a lane loads its group as one 16-byte (f32) or 8-byte
+// vector; a workgroup assembles the records of kWireTiles tiles of 256
+// groups in LDS -- 800, 832 or 896 bytes per tile for bs 32, 16, 8, each a
+// multiple of 16 -- and writes them as whole 16-byte vectors.  Unpacking
+// reverses it: 16-byte record loads into LDS, one 16-byte f32 store per
+// group.  Ragged rows (the virtual zero padding) and unaligned pointers take
+// the general kernels, one group per thread with byte accesses.
 #include "nf5_device.h"
 
 namespace axs6 {
@@ -37,10 +45,31 @@ struct WireGeom {
     int64_t rows, cols, nblk, groups;   // groups = rows * nblk * bs / 4
 };
 
-// x [rows, cols] -> records.  Exponent: e = clamp(floor(log2(max(amax,
-// 1e-45))) + 1 + 127, 0, 255), 0 for an all-zero block (and for NaN/inf
-// amax, whose int cast is INT_MIN); index = trunc(clamp(|x| / 2^(e-127), 0, 1)
-// * 1023); code = reverse_lut[index]; sign = x < 0.
+// Record fields of one group of four values of a block whose largest |x|
+// has the float bits m (reduced over the block's lanes).  Exponent:
+// e = clamp(floor(log2(max(amax, 1e-45))) + 1 + 127, 0, 255), 0 for an
+// all-zero block (and for NaN/inf amax, whose int cast is INT_MIN);
+// index = trunc(clamp(|x| / 2^(e-127), 0, 1) * 1023); code = reverse_lut[index];
+// q = code | (x < 0) << 5.  Returns e.
+__device__ __forceinline__ int wire_codes(const float (&f)[4], uint32_t m, const uint8_t* band_s,
+                                          const uint8_t* rev_s, int (&qv)[4]) {
+    int e8 = (m == 0u || m >= kInfBits) ? 0 : floor_log2_torch(m, band_s) + 1 + kExpBias;
+    e8 = e8 < 0 ? 0 : (e8 > 255 ? 255 : e8);
+    const int se = e8 - kExpBias;           // scale 2^se, se in [-127, 128]
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t ab = __float_as_uint(f[e]) & 0x7fffffffu;
+        float n;
+        if (se >= 128) n = ab >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;
+        else n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -se);
+        n = n > 1.0f ? 1.0f : n;            // clamp(0, 1); NaN passes to the index rule
+        const int idx = lut_index(n, false, 0.0f);
+        qv[e] = (int)rev_s[idx] | ((f[e] < 0.0f ? 1 : 0) << 5);
+    }
+    return e8;
+}
+
+// x [rows, cols] -> records (general path), one group per thread.
 template <int DT, int BS>
 __global__ __launch_bounds__(kThreads) void wire_pack_kernel(const typename Elem<DT>::S* __restrict__ x, WireGeom g,
                                                              const uint8_t* __restrict__ band_g,
@@ -77,20 +106,8 @@ __global__ __launch_bounds__(kThreads) void wire_pack_kernel(const typename Elem
             m = m > a ? m : a;
         }
         m = group_umax<GPB>(m);
-        int e8 = (m == 0u || m >= kInfBits) ? 0 : floor_log2_torch(m, band_s) + 1 + kExpBias;
-        e8 = e8 < 0 ? 0 : (e8 > 255 ? 255 : e8);
-        const int se = e8 - kExpBias;           // scale 2^se, se in [-127, 128]
         int qv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t ab = __float_as_uint(f[e]) & 0x7fffffffu;
-            float n;
-            if (se >= 128) n = ab >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;
-            else n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -se);
-            n = n > 1.0f ? 1.0f : n;            // clamp(0, 1); NaN passes to the index rule
-            const int idx = lut_index(n, false, 0.0f);
-            qv[e] = (int)rev_s[idx] | ((f[e] < 0.0f ? 1 : 0) << 5);
-        }
+        const int e8 = wire_codes(f, m, band_s, rev_s, qv);
         if (vq) {
             uint8_t* rec = buf + blk * REC;
             if (j4 == 0) rec[0] = (uint8_t)e8;
@@ -99,8 +116,159 @@ __global__ __launch_bounds__(kThreads) void wire_pack_kernel(const typename Elem
     }
 }
 
+// Fast-path geometry: kWireTiles tiles of kThreads groups per workgroup
+// iteration; a tile's records take wire_tile_bytes<BS>() bytes.
+constexpr int kWireTiles = 4;
+template <int BS>
+constexpr int wire_tile_bytes() { return kThreads / (BS / 4) * (1 + BS * 3 / 4); }
+
+// The four values of group q (flat index 4q), as floats.
+template <int DT>
+__device__ __forceinline__ void load_group(const typename Elem<DT>::S* x, int64_t q, float (&f)[4]) {
+    using E = Elem<DT>;
+    if constexpr (DT == AXS6_F32) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(x + q * 4);
+        f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
+        f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+    } else {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v = *reinterpret_cast<const u32x2*>(x + q * 4);
+        using S = typename E::S;
+        f[0] = E::to_f(__builtin_bit_cast(S, (uint16_t)(v.x & 0xffffu)));
+        f[1] = E::to_f(__builtin_bit_cast(S, (uint16_t)(v.x >> 16)));
+        f[2] = E::to_f(__builtin_bit_cast(S, (uint16_t)(v.y & 0xffffu)));
+        f[3] = E::to_f(__builtin_bit_cast(S, (uint16_t)(v.y >> 16)));
+    }
+}
+
+// Fast-path pack: groups = rows * cols / 4 with cols % BS == 0; x aligned to
+// its 4-value group, buf to 16 bytes.  Same record bytes as wire_pack_kernel.
+template <int DT, int BS>
+__global__ __launch_bounds__(kThreads) void wire_pack_vec_kernel(const typename Elem<DT>::S* __restrict__ x,
+                                                                 int64_t groups, const uint8_t* __restrict__ band_g,
+                                                                 const uint8_t* __restrict__ rev_g,
+                                                                 uint8_t* __restrict__ buf) {
+    constexpr int GPB = BS / 4;
+    constexpr int REC = 1 + BS * 3 / 4;
+    constexpr int TB = wire_tile_bytes<BS>();
+    constexpr int U = kWireTiles;
+    static_assert(TB % 16 == 0 && kThreads % GPB == 0, "tiles of whole blocks and 16-byte chunks");
+    __shared__ uint32_t band_w[kBandSize / 4];
+    __shared__ uint8_t rev_s[kLutSize];
+    __shared__ __align__(16) uint8_t recs[U * TB];
+    const int tid = threadIdx.x;
+    reinterpret_cast<uint32_t*>(rev_s)[tid] = reinterpret_cast<const uint32_t*>(rev_g)[tid];
+    if (tid < kBandSize / 4) band_w[tid] = reinterpret_cast<const uint32_t*>(band_g)[tid];
+    __syncthreads();
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+    const int64_t ntiles = (groups + kThreads - 1) / kThreads;
+    const int64_t total_bytes = groups / GPB * REC;
+    uint8_t* rec = recs + (tid / GPB) * REC;   // this lane's block record within a tile
+    const int j4 = tid % GPB;
+
+    for (int64_t t0 = (int64_t)blockIdx.x * U; t0 < ntiles; t0 += (int64_t)gridDim.x * U) {
+        float f[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t q = (t0 + u) * kThreads + tid;
+            if (q < groups) load_group<DT>(x, q, f[u]);
+            else f[u][0] = f[u][1] = f[u][2] = f[u][3] = 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            uint32_t m = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t a = __float_as_uint(f[u][e]) & 0x7fffffffu;
+                m = m > a ? m : a;
+            }
+            // a block is GPB lanes at a multiple of GPB: all inside or all past the end
+            m = group_umax<GPB>(m);
+            int qv[4];
+            const int e8 = wire_codes(f[u], m, band_s, rev_s, qv);
+            if (j4 == 0) rec[u * TB] = (uint8_t)e8;
+            pack3(qv, rec + u * TB + 1 + 3 * j4);
+        }
+        __syncthreads();
+        // the U tiles' records are contiguous in buf from t0 * TB
+        const int64_t base = t0 * TB;
+        const int64_t left = total_bytes - base;
+        const int nbytes = left < U * TB ? (int)left : U * TB;
+        for (int c = tid; c * 16 < nbytes; c += kThreads) {
+            if (c * 16 + 16 <= nbytes) {
+                *reinterpret_cast<u32x4*>(buf + base + c * 16) = *reinterpret_cast<const u32x4*>(recs + c * 16);
+            } else {
+                for (int b = c * 16; b < nbytes; ++b) buf[base + b] = recs[b];
+            }
+        }
+        __syncthreads();   // recs is rewritten by the next iteration
+    }
+}
+
+// Fast-path unpack, the inverse geometry: y [groups * 4] f32 (16-byte aligned), buf 16-byte aligned.
+template <int BS>
+__global__ __launch_bounds__(kThreads) void wire_unpack_vec_kernel(const uint8_t* __restrict__ buf, int64_t groups,
+                                                                   const float* __restrict__ cb_g,
+                                                                   float* __restrict__ y) {
+    constexpr int GPB = BS / 4;
+    constexpr int REC = 1 + BS * 3 / 4;
+    constexpr int TB = wire_tile_bytes<BS>();
+    constexpr int U = kWireTiles;
+    static_assert(TB % 16 == 0 && kThreads % GPB == 0, "tiles of whole blocks and 16-byte chunks");
+    __shared__ float cb[kLevels];
+    __shared__ __align__(16) uint8_t recs[U * TB];
+    const int tid = threadIdx.x;
+    if (tid < kLevels) cb[tid] = cb_g[tid];
+    const int64_t ntiles = (groups + kThreads - 1) / kThreads;
+    const int64_t total_bytes = groups / GPB * REC;
+    const uint8_t* rec = recs + (tid / GPB) * REC;
+    const int j4 = tid % GPB;
+
+    for (int64_t t0 = (int64_t)blockIdx.x * U; t0 < ntiles; t0 += (int64_t)gridDim.x * U) {
+        const int64_t base = t0 * TB;
+        const int64_t left = total_bytes - base;
+        const int nbytes = left < U * TB ? (int)left : U * TB;
+        for (int c = tid; c * 16 < nbytes; c += kThreads) {
+            if (c * 16 + 16 <= nbytes) {
+                *reinterpret_cast<u32x4*>(recs + c * 16) = *reinterpret_cast<const u32x4*>(buf + base + c * 16);
+            } else {
+                for (int b = c * 16; b < nbytes; ++b) recs[b] = buf[base + b];
+            }
+        }
+        __syncthreads();   // records (and, the first time, the codebook) staged
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t q = (t0 + u) * kThreads + tid;
+            if (q < groups) {
+                const uint8_t* r = rec + u * TB;
+                const float scale = pow2_float((int)r[0] - kExpBias);
+                int qv[4];
+                unpack3(r + 1 + 3 * j4, qv);
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float a = cb[qv[e] & 0x1F] * scale;
+                    v[e] = (qv[e] & 0x20) ? -a : a;
+                }
+                u32x4 w;
+                w.x = __float_as_uint(v[0]); w.y = __float_as_uint(v[1]);
+                w.z = __float_as_uint(v[2]); w.w = __float_as_uint(v[3]);
+                *reinterpret_cast<u32x4*>(y + q * 4) = w;
+            }
+        }
+        __syncthreads();   // recs is rewritten by the next iteration
+    }
+}
+
+unsigned wire_vec_grid(int64_t groups) {
+    const int64_t ntiles = (groups + kThreads - 1) / kThreads;
+    const int64_t wgs = (ntiles + kWireTiles - 1) / kWireTiles;
+    return (unsigned)(wgs < 32768 ? (wgs > 0 ? wgs : 1) : 32768);
+}
+
 // records -> y [rows, cols] f32: codebook[code] * 2^(e-127), negated where the
 // sign bit is set (_unpack_from_flat_buffer + _unpack_gradient, :118-144,201-232).
+// General path, one group per thread.
 template <int BS>
 __global__ __launch_bounds__(kThreads) void wire_unpack_kernel(const uint8_t* __restrict__ buf, WireGeom g,
                                                                const float* __restrict__ cb_g, float* __restrict__ y) {
@@ -211,8 +379,24 @@ extern "C" int axs6_nf5_pack_wire(const void* x, int32_t dtype, int64_t rows, in
     if ((rc = device_tables(&t))) return rc;
     const int64_t nblk = (cols + block_size - 1) / block_size;
     const WireGeom g{rows, cols, nblk, rows * nblk * (block_size / 4)};
-    const dim3 grid(wire_grid(g.groups));
     hipStream_t st = (hipStream_t)stream;
+    const int esize = dtype == AXS6_F32 ? 4 : 2;
+    if (cols % block_size == 0 && (uintptr_t)x % (4 * esize) == 0 && (uintptr_t)buffer % 16 == 0) {
+        const dim3 vgrid(wire_vec_grid(g.groups));
+#define AXS6_WIRE_VEC(DT_)                                                                                     \
+    do {                                                                                                       \
+        using S_ = typename Elem<DT_>::S;                                                                      \
+        if (block_size == 8) wire_pack_vec_kernel<DT_, 8><<<vgrid, kThreads, 0, st>>>((const S_*)x, g.groups, t.band, t.rev, buffer);   \
+        else if (block_size == 16) wire_pack_vec_kernel<DT_, 16><<<vgrid, kThreads, 0, st>>>((const S_*)x, g.groups, t.band, t.rev, buffer); \
+        else wire_pack_vec_kernel<DT_, 32><<<vgrid, kThreads, 0, st>>>((const S_*)x, g.groups, t.band, t.rev, buffer);     \
+    } while (0)
+        if (dtype == AXS6_F32) AXS6_WIRE_VEC(AXS6_F32);
+        else if (dtype == AXS6_BF16) AXS6_WIRE_VEC(AXS6_BF16);
+        else AXS6_WIRE_VEC(AXS6_F16);
+#undef AXS6_WIRE_VEC
+        return check_launch(fn);
+    }
+    const dim3 grid(wire_grid(g.groups));
 #define AXS6_WIRE(DT_)                                                                                         \
     do {                                                                                                       \
         using S_ = typename Elem<DT_>::S;                                                                      \
@@ -238,8 +422,15 @@ extern "C" int axs6_nf5_unpack_wire(const uint8_t* buffer, int64_t rows, int64_t
     if ((rc = device_tables(&t))) return rc;
     const int64_t nblk = (cols + block_size - 1) / block_size;
     const WireGeom g{rows, cols, nblk, rows * nblk * (block_size / 4)};
-    const dim3 grid(wire_grid(g.groups));
     hipStream_t st = (hipStream_t)stream;
+    if (cols % block_size == 0 && (uintptr_t)y % 16 == 0 && (uintptr_t)buffer % 16 == 0) {
+        const dim3 vgrid(wire_vec_grid(g.groups));
+        if (block_size == 8) wire_unpack_vec_kernel<8><<<vgrid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
+        else if (block_size == 16) wire_unpack_vec_kernel<16><<<vgrid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
+        else wire_unpack_vec_kernel<32><<<vgrid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
+        return check_launch(fn);
+    }
+    const dim3 grid(wire_grid(g.groups));
     if (block_size == 8) wire_unpack_kernel<8><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);
     else if (block_size == 16) wire_unpack_kernel<16><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);
     else wire_unpack_kernel<32><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);

@@ -45,14 +45,45 @@ def _oracle_buffer(x2: np.ndarray, bs: int) -> np.ndarray:
     return oracle.wire_pack(exps, codes, signs)
 
 
+# (64, 256), (300, 512), (7, 96), (1, 8): rows tile into whole blocks (the
+# vector kernels; 300 x 512 ends in a partial workgroup iteration, 7 x 96 in a
+# partial tile whose record bytes end mid 16-byte chunk); the others are
+# ragged for some block sizes (the general kernels)
 @pytest.mark.parametrize("bs", [8, 16, 32])
-@pytest.mark.parametrize("shape", [(64, 256), (37, 100), (5, 33), (1, 8)], ids=str)
+@pytest.mark.parametrize("shape", [(64, 256), (300, 512), (7, 96), (37, 100), (5, 33), (1, 8)], ids=str)
 def test_pack_wire_bitexact(bs, shape):
-    from axs.unified.distributed import pack_gradient_to_buffer
+    from axs.unified.distributed import pack_gradient_to_buffer, unpack_buffer_to_gradient
 
     x = _data(shape, 7 * bs + shape[1])
-    got = pack_gradient_to_buffer(x.to(DEV), bs).cpu().numpy().view(np.uint8)
-    assert np.array_equal(got, _oracle_buffer(x.numpy(), bs))
+    buf = pack_gradient_to_buffer(x.to(DEV), bs)
+    assert np.array_equal(buf.cpu().numpy().view(np.uint8), _oracle_buffer(x.numpy(), bs))
+    y = unpack_buffer_to_gradient(buf, shape, bs).cpu().numpy()
+    exps, codes, signs = oracle.quantize(x.numpy(), bs)
+    assert bits_equal(y, oracle.dequantize(exps, codes, signs, shape[1], bs))
+
+
+@pytest.mark.parametrize("bs", [8, 32])
+def test_wire_unaligned_pointers(bs):
+    """Pointers off the vector kernels' alignment take the general kernels:
+    same bytes and values."""
+    from axs import _lib
+
+    rows, cols = 40, 128
+    x = _data((rows, cols + 1), 21 + bs)[:, 1:].contiguous()
+    nbytes = _lib.lib().axs6_nf5_wire_bytes(rows, cols, bs)
+    want = _oracle_buffer(x.numpy(), bs)
+    xs = torch.zeros(rows * cols + 1, device=DEV)
+    xs[1:] = x.reshape(-1).to(DEV)                       # input 4 bytes past a 16-byte boundary
+    raw = torch.zeros(nbytes + 16, dtype=torch.uint8, device=DEV)
+    st = _lib.stream_of(xs)
+    _lib.call("axs6_nf5_pack_wire", xs[1:].data_ptr(), _lib.F32, rows, cols, bs, raw[3:].data_ptr(), st)
+    torch.cuda.synchronize()
+    assert np.array_equal(raw[3:3 + nbytes].cpu().numpy(), want)
+    y = torch.zeros(rows * cols + 1, device=DEV)
+    _lib.call("axs6_nf5_unpack_wire", raw[3:].data_ptr(), rows, cols, bs, y[1:].data_ptr(), st)
+    torch.cuda.synchronize()
+    exps, codes, signs = oracle.quantize(x.numpy(), bs)
+    assert bits_equal(y[1:].cpu().numpy().reshape(rows, cols), oracle.dequantize(exps, codes, signs, cols, bs))
 
 
 @pytest.mark.parametrize("bs", [8, 16, 32])
@@ -68,12 +99,13 @@ def test_pack_wire_edge_cases(bs):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_pack_wire_16bit_inputs(dtype):
+@pytest.mark.parametrize("bs,cols", [(32, 320), (8, 328), (16, 100)])
+def test_pack_wire_16bit_inputs(dtype, bs, cols):
     from axs.unified.distributed import pack_gradient_to_buffer
 
-    x = _data((48, 320), 3).to(dtype)
-    got = pack_gradient_to_buffer(x.to(DEV), 32).cpu().numpy().view(np.uint8)
-    assert np.array_equal(got, _oracle_buffer(x.float().numpy(), 32))
+    x = _data((48, cols), 3 + bs).to(dtype)
+    got = pack_gradient_to_buffer(x.to(DEV), bs).cpu().numpy().view(np.uint8)
+    assert np.array_equal(got, _oracle_buffer(x.float().numpy(), bs))
 
 
 def test_components_round_trip_and_match_fused():
