@@ -217,6 +217,110 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(
     }
 }
 
+// Vector form of quantize_kernel for rows that tile into whole blocks
+// (cols % BS == 0: codes and signs are then the flat [rows * cols] layout,
+// exponents one per BS flat values) and aligned pointers: each lane takes one
+// 16-byte vector of V values, a block is G = BS / V neighbouring lanes (DPP
+// amax), and the lane writes its V codes and V signs as one V-byte store.
+// Same arithmetic and dither counters as quantize_kernel.
+template <int DT, int BS, bool STOCH>
+__global__ __launch_bounds__(kThreads) void quantize_vec_kernel(
+    const typename Elem<DT>::S* x, int64_t n_vec, const float* __restrict__ lut_g, const uint8_t* __restrict__ band_g,
+    const uint8_t* __restrict__ rev_g, uint64_t seed, const uint64_t* __restrict__ seed_dev, uint64_t offset,
+    uint8_t* __restrict__ exps, uint8_t* __restrict__ codes, uint8_t* __restrict__ signs, typename Elem<DT>::S* fq) {
+    using E = Elem<DT>;
+    constexpr int V = E::V;
+    constexpr int G = BS / V > 0 ? BS / V : 1;
+    static_assert(BS % V == 0, "a vector lies inside one block");
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
+    __shared__ float lut_s[kLutSize];
+    __shared__ uint32_t band_w[kBandSize / 4];
+    __shared__ uint8_t rev_s[kLutSize];
+    reinterpret_cast<uint32_t*>(rev_s)[threadIdx.x] = reinterpret_cast<const uint32_t*>(rev_g)[threadIdx.x];
+    stage_tables(lut_s, band_w, lut_g, band_g);
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+    const u32x4* xv = reinterpret_cast<const u32x4*>(x);
+    const int64_t step = (int64_t)gridDim.x * kThreads;
+    // the bound is rounded up to whole waves so every lane of a block's DPP
+    // group runs every iteration
+    const int64_t span = (n_vec + 63) / 64 * 64;
+    for (int64_t vi = (int64_t)blockIdx.x * kThreads + threadIdx.x; vi < span; vi += step) {
+        const bool live = vi < n_vec;
+        float f[V];
+        E::unpack(live ? xv[vi] : u32x4{0u, 0u, 0u, 0u}, f);
+        uint32_t m = 0;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const uint32_t a = __float_as_uint(f[e]) & 0x7fffffffu;
+            m = m > a ? m : a;
+        }
+        m = group_umax<G>(m);
+        int ex = (m == 0u || m >= kInfBits) ? 0 : floor_log2_torch(m, band_s) + 1 + kExpBias;
+        ex = ex < 0 ? 0 : (ex > 255 ? 255 : ex);
+        const int se = ex - kExpBias;              // scale = 2^se, se in [-127, 128]
+        float d[V];
+        const DitherVec dv = dither_vec(key, offset + (uint64_t)(vi * V));
+#pragma unroll
+        for (int e = 0; e < V; ++e) d[e] = STOCH ? dither_step(dv, e) : 0.0f;
+        uint32_t cw[2] = {0u, 0u}, sw[2] = {0u, 0u};   // V bytes of codes and signs
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const uint32_t ab = __float_as_uint(f[e]) & 0x7fffffffu;
+            float n;
+            if (se >= 128) n = ab >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;   // x / inf
+            else n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -se);
+            n = (n > 1.0f) ? 1.0f : n;             // clamp(0, 1); NaN passes through
+            const int idx = lut_index(n, STOCH, d[e]);
+            cw[e / 4] |= (uint32_t)rev_s[idx] << (8 * (e % 4));
+            sw[e / 4] |= (f[e] < 0.0f ? 1u : 0u) << (8 * (e % 4));
+        }
+        if (live) {
+            if constexpr (V == 4) {
+                reinterpret_cast<uint32_t*>(codes)[vi] = cw[0];
+                if (signs) reinterpret_cast<uint32_t*>(signs)[vi] = sw[0];
+            } else {
+                reinterpret_cast<u32x2*>(codes)[vi] = u32x2{cw[0], cw[1]};
+                if (signs) reinterpret_cast<u32x2*>(signs)[vi] = u32x2{sw[0], sw[1]};
+            }
+            if (vi % G == 0) exps[vi / G] = (uint8_t)ex;
+        }
+        if (fq) {
+            const FqScale sc = fq_scale(m, band_s);
+            fq_vector<V>(f, sc, lut_s, STOCH, d);
+            if (live) reinterpret_cast<u32x4*>(fq)[vi] = E::pack(f);
+        }
+    }
+}
+
+// Vector form of dequantize_kernel (cols % bs == 0, 4-byte aligned codes and
+// signs, 16-byte aligned y): four values per lane, one 16-byte store.
+__global__ __launch_bounds__(kThreads) void dequantize_vec_kernel(const uint8_t* __restrict__ exps,
+                                                                  const uint8_t* __restrict__ codes,
+                                                                  const uint8_t* __restrict__ signs,
+                                                                  float* __restrict__ y, int64_t n4, int bs,
+                                                                  const float* __restrict__ cb_g) {
+    __shared__ float cb[kLevels];
+    if (threadIdx.x < kLevels) cb[threadIdx.x] = cb_g[threadIdx.x];
+    __syncthreads();
+    const int sh = bs == 8 ? 1 : (bs == 16 ? 2 : 3);    // groups of 4 per block: 2^sh
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kThreads) {
+        const uint32_t cw = reinterpret_cast<const uint32_t*>(codes)[i];
+        const uint32_t sw = signs ? reinterpret_cast<const uint32_t*>(signs)[i] : 0u;
+        const float scale = pow2_float((int)exps[i >> sh] - kExpBias);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float a = cb[(cw >> (8 * e)) & 31] * scale;
+            v[e] = ((sw >> (8 * e)) & 0xffu) ? -a : a;
+        }
+        u32x4 w;
+        w.x = __float_as_uint(v[0]); w.y = __float_as_uint(v[1]);
+        w.z = __float_as_uint(v[2]); w.w = __float_as_uint(v[3]);
+        reinterpret_cast<u32x4*>(y)[i] = w;
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t* __restrict__ exps,
                                                               const uint8_t* __restrict__ codes,
                                                               const uint8_t* __restrict__ signs,
@@ -309,6 +413,17 @@ void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochast
                         uint64_t offset, uint8_t* exps, uint8_t* codes, uint8_t* signs, void* fq,
                         const DeviceTables& t, hipStream_t st) {
     using S = typename Elem<DT>::S;
+    constexpr int V = Elem<DT>::V;
+    if (cols % BS == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)codes % V == 0 && (uintptr_t)signs % V == 0 &&
+        (uintptr_t)fq % 16 == 0) {
+        const int64_t n_vec = rows * cols / V;
+        const dim3 grid((unsigned)capped_grid(n_vec, (int64_t)kThreads));
+        if (stochastic)
+            quantize_vec_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, n_vec, t.lut, t.band, t.rev, seed, seed_dev, offset, exps, codes, signs, (S*)fq);
+        else
+            quantize_vec_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, n_vec, t.lut, t.band, t.rev, seed, seed_dev, offset, exps, codes, signs, (S*)fq);
+        return;
+    }
     const int64_t nblk = (cols + BS - 1) / BS;
     const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));
     if (stochastic)
@@ -385,6 +500,12 @@ extern "C" int axs6_nf5_dequantize(const uint8_t* exponents, const uint8_t* code
     DeviceTables t;
     if ((rc = device_tables(&t))) return rc;
     const int64_t nblk = (cols + block_size - 1) / block_size;
+    if (cols % block_size == 0 && (uintptr_t)codes % 4 == 0 && (uintptr_t)signs % 4 == 0 && (uintptr_t)y % 16 == 0) {
+        const int64_t n4 = rows * cols / 4;
+        dequantize_vec_kernel<<<dim3((unsigned)capped_grid(n4, kThreads)), kThreads, 0, (hipStream_t)stream>>>(
+            exponents, codes, signs, y, n4, block_size, t.codebook);
+        return check_launch(fn);
+    }
     const dim3 grid((unsigned)capped_grid(rows * cols, kThreads));
     dequantize_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(exponents, codes, signs, y, rows, cols, nblk,
                                                                   block_size, t.codebook);

@@ -16,6 +16,8 @@ linear TFLOP/s @4096^3 bf16"):
     (6*M*N*K FLOPs per step).
   * "wire": the 6.25-bit gradient wire format (quantize+pack, unpack) at
     8192x4096, GB/s.
+  * "codec": quantize (exponents, codes, signs and the FQ output) and
+    dequantize at 8192x4096, GB/s.
   * "minigpt": config 5, the MiniGPT training step with every nn.Linear
     converted (ms/step and the loss curve, beside the fp32 model).
 Inputs are synthetic, resident in HBM before the timed region.  K steps are
@@ -219,6 +221,44 @@ def bench_wire(reps: int = 20, warmup: int = 3):
             "pack_ms": round(pack_ms, 5), "unpack_ms": round(unpack_ms, 5),
             "pack_gbs": round(nbytes / (pack_ms * 1e-3) / 1e9, 1),
             "unpack_gbs": round(nbytes / (unpack_ms * 1e-3) / 1e9, 1)}
+
+
+def bench_codec(reps: int = 20, warmup: int = 3):
+    """quantize_unified / dequantize_unified (the AXSTensor codec, config 1's
+    operation) on one 8192x4096 f32 tensor, block 32, nearest rounding.
+    Algorithmic bytes per value: quantize with the FQ output 4 read + 1 code +
+    1 sign + 1/32 exponent + 4 FQ written = 10.03; dequantize 1 + 1 + 1/32
+    read + 4 written = 6.03.  HIP-event device time per call."""
+    import torch
+
+    from axs.unified.hip_kernels import hip_dequantize, hip_quantize
+
+    g = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.randn(*FQ_SHAPE, device="cuda", generator=g)
+    e, c, s, _ = hip_quantize(x, 32)
+    rows, cols = FQ_SHAPE
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    q_ms = timed(lambda: hip_quantize(x, 32, with_fake_quantized=True))
+    d_ms = timed(lambda: hip_dequantize(e, c, s, rows, cols, 32))
+    n = x.numel()
+    q_bytes = n * (4 + 1 + 1 + 4) + n // 32
+    d_bytes = n * (1 + 1 + 4) + n // 32
+    return {"metric": "NF5 quantize (+FQ output) / dequantize GB/s @8192x4096 fp32, block 32",
+            "quantize_ms": round(q_ms, 5), "dequantize_ms": round(d_ms, 5),
+            "quantize_gbs": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
+            "dequantize_gbs": round(d_bytes / (d_ms * 1e-3) / 1e9, 1)}
 
 
 LIN_TRAIN_SHAPES = [(8192, 4096, 11008), (8192, 11008, 4096), (2048, 768, 3072), (2048, 3072, 768)]
@@ -576,6 +616,9 @@ def main() -> int:
 
     out["wire"] = bench_wire()
     log(f"wire 8192x4096: pack {out['wire']['pack_gbs']} GB/s, unpack {out['wire']['unpack_gbs']} GB/s")
+    out["codec"] = bench_codec()
+    log(f"codec 8192x4096: quantize {out['codec']['quantize_gbs']} GB/s, "
+        f"dequantize {out['codec']['dequantize_gbs']} GB/s")
 
     if not a.no_linear:
         log("linear fwd+bwd (config 4) ...")

@@ -198,6 +198,45 @@ def test_quantize_vs_oracle(bs, shape):
         assert bits_equal(fq, oracle.fake_quantize(x.numpy(), bs, u))
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_quantize_16bit_vs_oracle(dt, bs):
+    """16-bit inputs on the vector kernel (8 values per lane): codes, signs,
+    exponents and the FQ output, nearest and stochastic."""
+    x = config2_input((64, 256), 90 + bs).to(dt)
+    x[0, :5] = torch.tensor([float("nan"), 0.0, -0.0, 1e-40, -3e38]).to(dt)
+    xf = x.float().numpy()
+    from axs.unified.hip_kernels import hip_quantize
+
+    for rounding, seed in (("nearest", None), ("stochastic", 7)):
+        e, c, s, fq = hip_quantize(x.to(DEV), bs, rounding, with_fake_quantized=True, seed=seed)
+        u = oracle.uniform(seed, 0, x.numel()) if seed else None
+        oe, oc, os_ = oracle.quantize(xf, bs, u)
+        assert np.array_equal(e.cpu().numpy(), oe) and np.array_equal(c.cpu().numpy(), oc)
+        assert np.array_equal(s.cpu().numpy(), os_)
+        want = torch.from_numpy(oracle.fake_quantize(xf, bs, u)).to(dt)
+        got = fq.cpu()
+        nan = torch.isnan(want)                 # NaN payloads differ between conversions: positions only
+        assert torch.equal(torch.isnan(got), nan)
+        assert torch.equal(got.view(torch.int16)[~nan], want.view(torch.int16)[~nan])
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_quantize_without_optional_outputs(bs):
+    """No signs and no FQ output (null pointers) on the vector kernel."""
+    from axs import _lib
+
+    x = config2_input((40, 192), 70 + bs).to(DEV)
+    nblk = 192 // bs
+    e = torch.empty((40, nblk), dtype=torch.uint8, device=DEV)
+    c = torch.empty((40, 192), dtype=torch.uint8, device=DEV)
+    _lib.call("axs6_nf5_quantize", x.data_ptr(), _lib.F32, 40, 192, bs, 0, 0, 0, e.data_ptr(), c.data_ptr(),
+              None, None, None, _lib.stream_of(x))
+    torch.cuda.synchronize()
+    oe, oc, _ = oracle.quantize(x.cpu().numpy(), bs)
+    assert np.array_equal(e.cpu().numpy(), oe) and np.array_equal(c.cpu().numpy().reshape(oc.shape), oc)
+
+
 def test_config1_golden():
     g = load_golden("config1.npz")
     gen = torch.Generator().manual_seed(0)
@@ -213,11 +252,13 @@ def test_config1_golden():
         assert sha(fq) == str(g["fq_sha"])
 
 
+# 101 columns: ragged rows (general kernel); 128: whole blocks (vector kernel)
+@pytest.mark.parametrize("cols", [101, 128])
 @pytest.mark.parametrize("bs", [8, 16, 32])
-def test_dequantize_vs_oracle(bs):
+def test_dequantize_vs_oracle(bs, cols):
     from axs.unified.quantize_unified import dequantize_unified, quantize_unified
 
-    x = config2_input((200, 96 + 5), 80 + bs)
+    x = config2_input((200, cols), 80 + bs)
     q = quantize_unified(x.to(DEV), bs)
     d = dequantize_unified(q).cpu().numpy()
     oe, oc, os_ = oracle.quantize(x.numpy(), bs)
