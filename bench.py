@@ -18,6 +18,8 @@ linear TFLOP/s @4096^3 bf16"):
     8192x4096, GB/s.
   * "codec": quantize (exponents, codes, signs and the FQ output) and
     dequantize at 8192x4096, GB/s.
+  * "configs": the smaller config-1/2 shapes (FQ at 256^2 and 4096^2,
+    quantize/dequantize at 1024^2), device time per launch.
   * "minigpt": config 5, the MiniGPT training step with every nn.Linear
     converted (ms/step and the loss curve, beside the fp32 model).
 Inputs are synthetic, resident in HBM before the timed region.  K steps are
@@ -259,6 +261,40 @@ def bench_codec(reps: int = 20, warmup: int = 3):
             "quantize_ms": round(q_ms, 5), "dequantize_ms": round(d_ms, 5),
             "quantize_gbs": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
             "dequantize_gbs": round(d_bytes / (d_ms * 1e-3) / 1e9, 1)}
+
+
+def bench_configs(steps: int = 200, warmup: int = 20):
+    """The smaller shapes of configs 1 and 2, timed like the headline (graph
+    replays, device time per launch): FQ at 256^2 and 4096^2 (config 2), and
+    quantize + dequantize of config 1's 1024^2 tensor (x = 0.02 N(0,1))."""
+    import torch
+
+    from axs.unified.hip_kernels import hip_dequantize, hip_fused_fake_quantize, hip_quantize
+
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(5)
+    for shape in ((256, 256), (4096, 4096)):
+        x = torch.randn(*shape, device="cuda", generator=g)
+        launch = lambda: hip_fused_fake_quantize(x, 32, "nearest")  # noqa: E731
+        _, gpu_ms, _ = time_steps(launch, launch, steps, warmup)
+        nbytes = 8 * x.numel()
+        out[f"fq_{shape[0]}x{shape[1]}"] = {"us_per_launch": round(gpu_ms * 1e3, 2),
+                                             "gbs": round(nbytes / (gpu_ms * 1e-3) / 1e9, 1),
+                                             "frac": round(nbytes / (gpu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    x = torch.randn(1024, 1024, device="cuda", generator=g) * 0.02
+    e, c, s_, _ = hip_quantize(x, 32)
+    q = lambda: hip_quantize(x, 32)  # noqa: E731
+    d = lambda: hip_dequantize(e, c, s_, 1024, 1024, 32)  # noqa: E731
+    _, q_ms, _ = time_steps(q, q, steps, warmup)
+    _, d_ms, _ = time_steps(d, d, steps, warmup)
+    n = x.numel()
+    out["config1_quantize_1024x1024"] = {"us_per_launch": round(q_ms * 1e3, 2),
+                                         "gbs": round(n * 6.03125 / (q_ms * 1e-3) / 1e9, 1)}
+    out["config1_dequantize_1024x1024"] = {"us_per_launch": round(d_ms * 1e3, 2),
+                                           "gbs": round(n * 6.03125 / (d_ms * 1e-3) / 1e9, 1)}
+    out["note"] = ("device time per launch from HIP-graph replays; shapes below ~4M values are "
+                   "launch-latency-bound, not HBM-bound")
+    return out
 
 
 LIN_TRAIN_SHAPES = [(8192, 4096, 11008), (8192, 11008, 4096), (2048, 768, 3072), (2048, 3072, 768)]
@@ -616,6 +652,8 @@ def main() -> int:
 
     out["wire"] = bench_wire()
     log(f"wire 8192x4096: pack {out['wire']['pack_gbs']} GB/s, unpack {out['wire']['unpack_gbs']} GB/s")
+    out["configs"] = bench_configs()
+    log(f"configs: {out['configs']}")
     out["codec"] = bench_codec()
     log(f"codec 8192x4096: quantize {out['codec']['quantize_gbs']} GB/s, "
         f"dequantize {out['codec']['dequantize_gbs']} GB/s")
