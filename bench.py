@@ -170,7 +170,9 @@ def bench_fq(steps: int, warmup: int):
             "copy_gpu_ms": copy_ms}
 
 
-def bench_linear(steps: int, warmup: int):
+def bench_linear(steps: int, warmup: int, dtype=None):
+    """Config 3's forward at 4096^3 (fp32 X, W, Y; or `dtype` inputs and
+    output, without the per-kernel split)."""
     import torch
 
     from axs.unified import hip_linear
@@ -180,11 +182,15 @@ def bench_linear(steps: int, warmup: int):
     X = torch.randn(M, K, device="cuda", generator=g)
     W = torch.randn(N, K, device="cuda", generator=g) * K ** -0.5
     b = torch.zeros(N, device="cuda")
+    if dtype is not None:
+        X, W = X.to(dtype), W.to(dtype)
 
     def step():
         hip_linear.linear_forward(X, W, b, 32, True)
 
     wall_ms, gpu_ms, eager_ms = time_steps(step, step, steps, warmup)
+    if dtype is not None:
+        return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "eager_ms": eager_ms, "flops": 2.0 * M * N * K}
     kern = hip_linear.last_forward_kernel_times(X, W, b, reps=max(steps, 10))
     return {"wall_ms": wall_ms, "gpu_ms": gpu_ms, "eager_ms": eager_ms, "flops": 2.0 * M * N * K,
             "kernels": kern}
@@ -647,6 +653,13 @@ def main() -> int:
                              "end_to_end_frac": round(tflops / BF16_DENSE_PEAK_TFLOPS, 4),
                              "traffic": load_traffic("linear_4096_traffic.json")},
             }
+            lb = bench_linear(max(a.steps // 2, 10), max(a.warmup // 2, 3), dtype=torch.bfloat16)
+            tb = lb["flops"] / (lb["wall_ms"] * 1e-3) / 1e12
+            out["linear"]["bf16_io"] = {
+                "note": "the same forward with bf16 X, W and Y (FQ of the bf16 values, fp16 MFMA, bf16 out)",
+                "ms_per_step": round(lb["wall_ms"], 5), "device_ms_per_step": round(lb["gpu_ms"], 5),
+                "value": round(tb, 1), "unit": "TFLOP/s", "end_to_end_frac": round(tb / BF16_DENSE_PEAK_TFLOPS, 4)}
+            log(f"linear 4096^3 fwd, bf16 I/O: {lb['wall_ms']*1e3:.1f} us/step, {tb:.0f} TFLOP/s")
         except NotImplementedError as e:
             log(f"linear: skipped ({e})")
 
