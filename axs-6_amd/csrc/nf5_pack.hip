@@ -752,7 +752,10 @@ inline RowsShape rows_shape(int64_t nvec) {
     if (nvec <= 64) return {64, 1};
     if (nvec <= 128) return {64, 2};
     if (nvec <= 256) return {64, 4};
-    if (nvec <= 512) return {256, 2};
+    // 257-512 vectors still one wave per row, 8 vectors per lane: 4-13%
+    // shorter than 256 threads x 2 (16384 rows of 1536-2048 f32 or
+    // 2560-4096 bf16 columns)
+    if (nvec <= 512) return {64, 8};
     if (nvec <= 1024) return {256, 4};
     // long rows, measured (one row per workgroup, 8192-16384 rows): for
     // 1025-2048 vectors 256 x 8 beats 512 x 4 by 12-13%; for 2049-3072
@@ -776,7 +779,8 @@ void dispatch_rows_nv(const PackRowsK& k, const PackRowsK& k2, int64_t rows, Row
         const dim3 g4((unsigned)((rows + RPW - 1) / RPW));
         if (sh.nv == 1) pack_rows_kernel<DT, MODE, COLX, 1, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
         else if (sh.nv == 2) pack_rows_kernel<DT, MODE, COLX, 2, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
-        else pack_rows_kernel<DT, MODE, COLX, 4, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
+        else if (sh.nv == 4) pack_rows_kernel<DT, MODE, COLX, 4, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
+        else pack_rows_kernel<DT, MODE, COLX, 8, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
     } else if (sh.nt == 768) {
         pack_rows_kernel<DT, MODE, COLX, 4, 768, 1><<<grid, 768, 0, st>>>(k, k2, rows);
     } else if (sh.nt == 512) {
