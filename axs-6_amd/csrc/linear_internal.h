@@ -78,8 +78,10 @@ struct TransposeF16 {
     const _Float16* in; int64_t rows; int64_t cols; int64_t ld_in;
     _Float16* out; int64_t out_rows; int64_t rows_pad; int64_t ld_out;
 };
-// a, and b when not null, in one launch
-int launch_transpose_f16(const TransposeF16& a, const TransposeF16* b, hipStream_t st);
+// a, and b when not null, in one launch; with db (and partial), the same
+// launch also writes db[c] = sum_k partial[k, c] (launch_reduce_partials)
+int launch_transpose_f16(const TransposeF16& a, const TransposeF16* b, hipStream_t st,
+                         const float* partial = nullptr, int64_t chunks = 0, int64_t cols = 0, float* db = nullptr);
 
 // *p = INT32_MIN (graph-capture safe: a kernel, not a memset).
 int launch_init_gmax(int32_t* p, hipStream_t st);

@@ -205,8 +205,15 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
     _Float16* xqt = need_dw ? (_Float16*)(ws + L.xqt) : nullptr;
     const TransposeF16 tw{(const _Float16*)wq_f16, N, Kp, Kp, wqt, Kp, Np, Np};
     const TransposeF16 tx{(const _Float16*)xq_f16, M, Kp, Kp, xqt, Kp, Mp, Mp};
+    // the bias gradient's ordered reduction of the pack's partial sums rides in
+    // the same launch (or runs alone when no operand is transposed)
+    const float* partial = need_db ? (const float*)(ws + L.partial) : nullptr;
     if (need_dx || need_dw) {
-        if ((rc = launch_transpose_f16(need_dx ? tw : tx, need_dx && need_dw ? &tx : nullptr, st))) return rc;
+        if ((rc = launch_transpose_f16(need_dx ? tw : tx, need_dx && need_dw ? &tx : nullptr, st, partial,
+                                       pack_global_chunks(M), N, db)))
+            return rc;
+    } else if (need_db && (rc = launch_reduce_partials(partial, pack_global_chunks(M), N, db, st))) {
+        return rc;
     }
     if (need_dx) {
         GemmArgs g{(const _Float16*)(ws + L.a1), Np, wqt, Np, M, K, Np, tshift, nullptr, nullptr, 0, nullptr,
@@ -219,7 +226,5 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
                    L.splitk_bytes ? (float*)(ws + L.splitk) : nullptr, L.splitk_bytes};
         if ((rc = launch_gemm_f16(g, st))) return rc;
     }
-    if (need_db && (rc = launch_reduce_partials((const float*)(ws + L.partial), pack_global_chunks(M), N, db, st)))
-        return rc;
     return AXS6_OK;
 }

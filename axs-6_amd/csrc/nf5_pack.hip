@@ -663,11 +663,13 @@ __global__ __launch_bounds__(256) void stats_finalize_kernel(const int32_t* __re
 // added in order.
 constexpr int kRedCols = 16, kRedRanges = 16;
 
-__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ partial, int64_t chunks,
-                                                              int64_t cols, float* __restrict__ out) {
+// out[c] = sum_k partial[k, c] for the kRedCols columns of block `bx`: 16
+// ranges of k summed by 16 thread groups, then the ranges added in order.
+__device__ __forceinline__ void reduce_partials_block(const float* __restrict__ partial, int64_t chunks,
+                                                      int64_t cols, float* __restrict__ out, int64_t bx) {
     __shared__ float part[kRedRanges][kRedCols + 1];
     const int lc = threadIdx.x % kRedCols, q = threadIdx.x / kRedCols;
-    const int64_t c = (int64_t)blockIdx.x * kRedCols + lc;
+    const int64_t c = bx * kRedCols + lc;
     const int64_t per = (chunks + kRedRanges - 1) / kRedRanges;
     const int64_t k0 = q * per, k1 = (k0 + per) < chunks ? k0 + per : chunks;
     float s = 0.0f;
@@ -692,12 +694,27 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
     }
 }
 
+__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ partial, int64_t chunks,
+                                                              int64_t cols, float* __restrict__ out) {
+    reduce_partials_block(partial, chunks, cols, out, blockIdx.x);
+}
+
 // out[c, r] = in[r, c] for r < rows, c < out_rows; zero for rows <= r < rows_pad.
 // 64 x 64 tiles; 16-byte loads along input rows, 16-byte stores along output
 // rows, the transpose done through LDS with 2-byte accesses.  One launch
 // serves two independent transposes: blockIdx.y below ny0 tiles the first,
-// the rest the second (the backward's two operands; one launch less).
-__global__ __launch_bounds__(256) void transpose_f16_kernel(TransposeF16 j0, TransposeF16 j1, int ny0) {
+// the next ny1 rows the second (the backward's two operands; one launch
+// less); rows past those, when red.blocks > 0, run the bias-gradient
+// reduction (reduce_partials_block), block (y - ny0 - ny1) * gridDim.x + x.
+struct ReduceJob { const float* partial; int64_t chunks; int64_t cols; float* out; int64_t blocks; };
+
+__global__ __launch_bounds__(256) void transpose_f16_kernel(TransposeF16 j0, TransposeF16 j1, int ny0, int ny1,
+                                                            ReduceJob red) {
+    if ((int)blockIdx.y >= ny0 + ny1) {      // uniform per workgroup
+        const int64_t rb = (int64_t)(blockIdx.y - ny0 - ny1) * gridDim.x + blockIdx.x;
+        if (rb < red.blocks) reduce_partials_block(red.partial, red.chunks, red.cols, red.out, rb);
+        return;
+    }
     const bool second = (int)blockIdx.y >= ny0;
     const TransposeF16 j = second ? j1 : j0;
     const uint16_t* __restrict__ in = reinterpret_cast<const uint16_t*>(j.in);
@@ -990,16 +1007,23 @@ int launch_reduce_partials(const float* partial, int64_t chunks, int64_t cols, f
     return check_launch("reduce_partials");
 }
 
-int launch_transpose_f16(const TransposeF16& a, const TransposeF16* b, hipStream_t st) {
+int launch_transpose_f16(const TransposeF16& a, const TransposeF16* b, hipStream_t st, const float* partial,
+                         int64_t chunks, int64_t cols, float* db) {
     const TransposeF16 none{nullptr, 0, 0, 0, nullptr, 0, 0, 0};
     const TransposeF16& bb = b ? *b : none;
     const int64_t gx_a = a.out_rows && a.rows_pad ? (a.out_rows + 63) / 64 : 0;
     const int64_t gx_b = bb.out_rows && bb.rows_pad ? (bb.out_rows + 63) / 64 : 0;
     const int64_t ny0 = gx_a ? (a.rows_pad + 63) / 64 : 0, ny1 = gx_b ? (bb.rows_pad + 63) / 64 : 0;
-    if (ny0 + ny1 == 0) return AXS6_OK;
+    const bool red = db && partial && cols > 0;
+    if (ny0 + ny1 == 0) return red ? launch_reduce_partials(partial, chunks, cols, db, st) : AXS6_OK;
     // a tile column past one job's out_rows writes nothing for it (orow >= out_rows)
-    const dim3 grid((unsigned)(gx_a > gx_b ? gx_a : gx_b), (unsigned)(ny0 + ny1));
-    transpose_f16_kernel<<<grid, 256, 0, st>>>(ny0 ? a : bb, ny0 ? bb : a, (int)(ny0 ? ny0 : ny1));
+    const int64_t gx = gx_a > gx_b ? gx_a : gx_b;
+    const ReduceJob rj{partial, chunks, cols, db, red ? (cols + kRedCols - 1) / kRedCols : 0};
+    const int64_t nyr = (rj.blocks + gx - 1) / gx;
+    const dim3 grid((unsigned)gx, (unsigned)(ny0 + ny1 + nyr));
+    // the jobs in order: a (when it has tiles), then b
+    transpose_f16_kernel<<<grid, 256, 0, st>>>(ny0 ? a : bb, ny0 ? bb : a, (int)(ny0 ? ny0 : ny1),
+                                               (int)(ny0 ? ny1 : 0), rj);
     return check_launch("transpose_f16");
 }
 

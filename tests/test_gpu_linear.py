@@ -208,6 +208,29 @@ def test_linear_backward_config4_sampled(M, K, N):
     assert e_dx < TOL and e_dw < TOL and e_db < 1e-5
 
 
+@pytest.mark.parametrize("need", [(False, False, True), (False, True, True), (True, False, True), (True, True, False)],
+                         ids=["db", "dw_db", "dx_db", "dx_dw"])
+def test_linear_backward_gradient_subsets(need):
+    """Each subset of (dX, dW, db): the bias reduction runs inside the
+    operand-transpose launch, or alone when nothing is transposed."""
+    from axs.unified import hip_linear
+
+    M, K, N = 300, 160, 96
+    x = gauss((M, K), 41, outliers=True)
+    w = gauss((N, K), 42, scale=K ** -0.5)
+    b = gauss((N,), 43)
+    dy = gauss((M, N), 44)
+    xq, wq, _ = _oracle_linear(x, w, b)
+    _, saved = hip_linear.forward_train(x.to(DEV), w.to(DEV), b.to(DEV), 32, True)
+    dx, dw, db = hip_linear.backward(dy.to(DEV), saved, 32, False, *need)
+    d = dy.numpy().astype(np.float64)
+    for got, want, on in ((dx, d @ wq.astype(np.float64), need[0]), (dw, d.T @ xq.astype(np.float64), need[1]),
+                          (db, d.sum(0), need[2])):
+        assert (got is None) == (not on)
+        if on:
+            assert oracle.rel_l2(got.cpu().numpy(), want) < (1e-5 if got.dim() == 1 else TOL)
+
+
 def test_linear_ragged_and_3d():
     from axs.unified import hip_linear
 
