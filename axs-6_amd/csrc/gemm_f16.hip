@@ -618,6 +618,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(SplitReduceK k) {
 // workgroups sharing a CU.  AXS6_GEMM_CFG=<n> forces a configuration for
 // launch-shape sweeps.
 constexpr int kCfgBig = 9, kCfgSmall = 10, kCfgNarrow = 12;
+constexpr int kNarrowDeepSteps = 32;   // 64-deep K-steps per workgroup from which 12 runs three slabs
 
 int gemm_cfg_env() {
     static int v = [] {
@@ -773,7 +774,12 @@ static int launch_gemm_one(const GemmArgs& a, hipStream_t st, bool cut) {
         case kCfgSmall: rc = run_gemm_lds<128, 128, 64, 2, 2, 2, 2, 16>(k, splits, st); break;
         case 0: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2>(k, splits, st); break;
         case 11: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2, 16>(k, splits, st); break;
-        case kCfgNarrow: rc = run_gemm_lds<128, 64, 64, 2, 2, 2, 2, 16, 4>(k, splits, st); break;
+        case kCfgNarrow:
+            // a long contraction on the small tiles: a third slab in flight
+            // (2048 x 768, K 3072: 28.5 -> 21.3 us; at K <= 1024 it costs 3-5%)
+            if (per >= kNarrowDeepSteps) rc = run_gemm_lds<128, 64, 64, 3, 2, 2, 2, 16, 4>(k, splits, st);
+            else rc = run_gemm_lds<128, 64, 64, 2, 2, 2, 2, 16, 4>(k, splits, st);
+            break;
         default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2, 16, 4>(k, splits, st); break;   // kCfgBig
     }
     if (rc || !split) return rc;

@@ -35,8 +35,10 @@ def _gemm(a16, b16, M, N, Kp, rexp=None, cexp=None, bias=None, out_dtype=torch.f
     return out
 
 
+# (2048, 768, 3072) and (1000, 200, 2112): small tiles with a long
+# contraction (three K-slabs in flight)
 @pytest.mark.parametrize("M,N,Kp", [(128, 128, 64), (256, 384, 512), (100, 72, 128), (1, 33, 64),
-                                    (300, 260, 1024), (4096, 4096, 256)])
+                                    (300, 260, 1024), (4096, 4096, 256), (2048, 768, 3072), (1000, 200, 2112)])
 def test_gemm_exact_small_integers(M, N, Kp):
     # small integers are exact in fp16 and their products sum exactly in fp32
     g = torch.Generator().manual_seed(M * 7 + N)
