@@ -90,6 +90,21 @@ def test_half_dtypes_vs_oracle(dt, bs):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
+def test_bf16_nan_and_rounding_bits():
+    """bf16 outputs are rounded to nearest even from the f32 FQ value, and a
+    NaN block is written as 0x7FC0 (torch's bf16 NaN)."""
+    x = config2_input((64, 512), 77)
+    x[3, 7] = float("nan")
+    xb = x.to(torch.bfloat16)
+    got = _fq(xb.to(DEV), 32).cpu().view(torch.int16)
+    want = torch.from_numpy(oracle.fake_quantize(xb.float().numpy(), 32)).to(torch.bfloat16).view(torch.int16)
+    nan = (got[3, :32] & 0x7FFF) > 0x7F80
+    assert bool(nan.all()) and bool(((got[3, :32] & 0xFFFF) == 0x7FC0).all())
+    mask = torch.ones_like(got, dtype=torch.bool)
+    mask[3, :32] = False
+    assert torch.equal(got[mask], want[mask])
+
+
 def test_exponent_range_and_bands():
     # blocks spanning the whole float32 range, incl. subnormals and overflow
     rng = np.random.default_rng(5)
