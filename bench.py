@@ -271,20 +271,22 @@ def bench_codec(reps: int = 20, warmup: int = 3):
 
 def bench_configs(steps: int = 200, warmup: int = 20):
     """The smaller shapes of configs 1 and 2, timed like the headline (graph
-    replays, device time per launch): FQ at 256^2 and 4096^2 (config 2), and
-    quantize + dequantize of config 1's 1024^2 tensor (x = 0.02 N(0,1))."""
+    replays, device time per launch): FQ at 256^2 and 4096^2 (config 2), the
+    headline FQ shape in bf16 (4 B per value of traffic), and quantize +
+    dequantize of config 1's 1024^2 tensor (x = 0.02 N(0,1))."""
     import torch
 
     from axs.unified.hip_kernels import hip_dequantize, hip_fused_fake_quantize, hip_quantize
 
     out = {}
     g = torch.Generator(device="cuda").manual_seed(5)
-    for shape in ((256, 256), (4096, 4096)):
-        x = torch.randn(*shape, device="cuda", generator=g)
+    for shape, dt in (((256, 256), torch.float32), ((4096, 4096), torch.float32), (FQ_SHAPE, torch.bfloat16)):
+        x = torch.randn(*shape, device="cuda", generator=g).to(dt)
         launch = lambda: hip_fused_fake_quantize(x, 32, "nearest")  # noqa: E731
         _, gpu_ms, _ = time_steps(launch, launch, steps, warmup)
-        nbytes = 8 * x.numel()
-        out[f"fq_{shape[0]}x{shape[1]}"] = {"us_per_launch": round(gpu_ms * 1e3, 2),
+        nbytes = 2 * x.element_size() * x.numel()
+        tag = "" if dt == torch.float32 else "_bf16"
+        out[f"fq_{shape[0]}x{shape[1]}{tag}"] = {"us_per_launch": round(gpu_ms * 1e3, 2),
                                              "gbs": round(nbytes / (gpu_ms * 1e-3) / 1e9, 1),
                                              "frac": round(nbytes / (gpu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     x = torch.randn(1024, 1024, device="cuda", generator=g) * 0.02
