@@ -662,33 +662,50 @@ def main() -> int:
                 "ms_per_step": round(lb["wall_ms"], 5), "device_ms_per_step": round(lb["gpu_ms"], 5),
                 "value": round(tb, 1), "unit": "TFLOP/s", "end_to_end_frac": round(tb / BF16_DENSE_PEAK_TFLOPS, 4)}
             log(f"linear 4096^3 fwd, bf16 I/O: {lb['wall_ms']*1e3:.1f} us/step, {tb:.0f} TFLOP/s")
-        except NotImplementedError as e:
-            log(f"linear: skipped ({e})")
+        except Exception as e:  # noqa: BLE001 - reported in the JSON line
+            import traceback
 
-    out["wire"] = bench_wire()
-    log(f"wire 8192x4096: pack {out['wire']['pack_gbs']} GB/s, unpack {out['wire']['unpack_gbs']} GB/s")
-    out["configs"] = bench_configs()
-    log(f"configs: {out['configs']}")
-    out["codec"] = bench_codec()
-    log(f"codec 8192x4096: quantize {out['codec']['quantize_gbs']} GB/s, "
-        f"dequantize {out['codec']['dequantize_gbs']} GB/s")
+            traceback.print_exc(file=sys.stderr)
+            out.setdefault("linear", {})["error"] = f"{type(e).__name__}: {e}"
+
+    def leg(dst: dict, key: str, fn, *args, **kw) -> bool:
+        """Runs one secondary measurement into dst[key]; a Python exception in
+        it is recorded there (and its traceback logged) instead of losing the
+        headline line."""
+        try:
+            dst[key] = fn(*args, **kw)
+            return True
+        except Exception as e:  # noqa: BLE001 - reported in the JSON line
+            import traceback
+
+            traceback.print_exc(file=sys.stderr)
+            dst[key] = {"error": f"{type(e).__name__}: {e}"}
+            return False
+
+    if leg(out, "wire", bench_wire):
+        log(f"wire 8192x4096: pack {out['wire']['pack_gbs']} GB/s, unpack {out['wire']['unpack_gbs']} GB/s")
+    if leg(out, "configs", bench_configs):
+        log(f"configs: {out['configs']}")
+    if leg(out, "codec", bench_codec):
+        log(f"codec 8192x4096: quantize {out['codec']['quantize_gbs']} GB/s, "
+            f"dequantize {out['codec']['dequantize_gbs']} GB/s")
 
     if not a.no_linear:
         log("linear fwd+bwd (config 4) ...")
-        out["linear_train"] = bench_linear_train()
+        leg(out, "linear_train", bench_linear_train)
 
     if not a.no_minigpt:
         log("minigpt (config 5) ...")
-        out["minigpt"] = bench_minigpt(ref_steps=0 if a.no_cpu_baseline else 3)
-        log(f"minigpt: {out['minigpt']['ms_per_step']} ms/step, loss {out['minigpt']['loss']}")
+        if leg(out, "minigpt", bench_minigpt, ref_steps=0 if a.no_cpu_baseline else 3):
+            log(f"minigpt: {out['minigpt']['ms_per_step']} ms/step, loss {out['minigpt']['loss']}")
 
     if not a.no_cpu_baseline:
         log("cpu baseline ...")
-        out["cpu_baseline"] = cpu_baseline_fq()
-        log(f"cpu baseline: {out['cpu_baseline']['value']} GB/s")
-        if "linear" in out:
-            out["linear"]["cpu_baseline"] = cpu_baseline_linear()
-            log(f"cpu baseline, linear: {out['linear']['cpu_baseline']['value']} TFLOP/s")
+        if leg(out, "cpu_baseline", cpu_baseline_fq):
+            log(f"cpu baseline: {out['cpu_baseline']['value']} GB/s")
+        if "linear" in out and "roofline" in out["linear"]:
+            if leg(out["linear"], "cpu_baseline", cpu_baseline_linear):
+                log(f"cpu baseline, linear: {out['linear']['cpu_baseline']['value']} TFLOP/s")
     print(json.dumps(out), flush=True)
     return 0
 
