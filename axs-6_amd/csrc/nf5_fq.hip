@@ -245,10 +245,15 @@ __global__ __launch_bounds__(kThreads) void quantize_vec_kernel(
     // the bound is rounded up to whole waves so every lane of a block's DPP
     // group runs every iteration
     const int64_t span = (n_vec + 63) / 64 * 64;
-    for (int64_t vi = (int64_t)blockIdx.x * kThreads + threadIdx.x; vi < span; vi += step) {
+    int64_t vi = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    // the next iteration's vector is loaded before this one is processed
+    u32x4 cur = vi < n_vec ? xv[vi] : u32x4{0u, 0u, 0u, 0u};
+    for (; vi < span; vi += step) {
         const bool live = vi < n_vec;
+        const u32x4 nxt = vi + step < n_vec ? xv[vi + step] : u32x4{0u, 0u, 0u, 0u};
         float f[V];
-        E::unpack(live ? xv[vi] : u32x4{0u, 0u, 0u, 0u}, f);
+        E::unpack(cur, f);
+        cur = nxt;
         uint32_t m = 0;
 #pragma unroll
         for (int e = 0; e < V; ++e) {
@@ -417,7 +422,7 @@ void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochast
     if (cols % BS == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)codes % V == 0 && (uintptr_t)signs % V == 0 &&
         (uintptr_t)fq % 16 == 0) {
         const int64_t n_vec = rows * cols / V;
-        const dim3 grid((unsigned)capped_grid(n_vec, (int64_t)kThreads));
+        const dim3 grid((unsigned)capped_grid(n_vec, (int64_t)kThreads * 2));   // two iterations per workgroup
         if (stochastic)
             quantize_vec_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, n_vec, t.lut, t.band, t.rev, seed, seed_dev, offset, exps, codes, signs, (S*)fq);
         else
