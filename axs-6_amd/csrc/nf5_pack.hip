@@ -853,6 +853,8 @@ namespace {
 
 int check_pack_rows(const PackRowsArgs& a, RowsShape* sh_out) {
     const int V = a.dtype == AXS6_F32 ? 4 : 8;
+    if (a.rows > INT_MAX)   // one workgroup (or a quarter of one) per row: the grid is 32-bit
+        return fail(AXS6_ERR_UNSUPPORTED, "pack_rows: %lld rows exceed the launch grid", (long long)a.rows);
     if (a.cols % a.block != 0)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: cols (%lld) must be a multiple of block_size", (long long)a.cols);
     if ((uintptr_t)a.x % 16 != 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: input not 16-byte aligned");
