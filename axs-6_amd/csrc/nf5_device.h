@@ -96,13 +96,16 @@ template <> struct Elem<AXS6_F16> {
             f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, hi);
         }
     }
+    // two values per v_cvt_pk_f16_f32, which gives the same bits as the
+    // scalar v_cvt_f16_f32 for every float32 input (all 2^32 compared on the GPU)
     __device__ static u32x4 pack(const float* f) {
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
         uint32_t w[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            uint16_t lo = __builtin_bit_cast(uint16_t, (_Float16)f[2 * i]);
-            uint16_t hi = __builtin_bit_cast(uint16_t, (_Float16)f[2 * i + 1]);
-            w[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+            const f32x2 v = {f[2 * i], f[2 * i + 1]};
+            w[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
         }
         u32x4 r;
         r.x = w[0]; r.y = w[1]; r.z = w[2]; r.w = w[3];
