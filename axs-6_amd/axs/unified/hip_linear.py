@@ -41,6 +41,13 @@ def _pad_rows(t: torch.Tensor, mult: int) -> torch.Tensor:
     return F.pad(t, (0, 0, 0, pad)) if pad else t
 
 
+def _dense(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous with a 16-byte aligned data pointer (the packing kernels
+    load 16-byte vectors); a view at an element offset is copied."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone(memory_format=torch.contiguous_format)
+
+
 class Saved:
     """Packed operands of a forward, kept for its backward."""
 
@@ -74,8 +81,8 @@ def _forward(input, weight, bias, block_size, quantize_input):
     x2 = input.reshape(-1, K).to(dtype)
     w2 = weight.to(dtype)
     k_true, n_true = K, N
-    x2 = _pad_last(x2, block_size).contiguous()
-    w2 = _pad_rows(_pad_last(w2, block_size), block_size).contiguous()
+    x2 = _dense(_pad_last(x2, block_size))
+    w2 = _dense(_pad_rows(_pad_last(w2, block_size), block_size))
     M, Kb = x2.shape
     Nb = w2.shape[0]
     b = None
@@ -91,7 +98,10 @@ def _forward(input, weight, bias, block_size, quantize_input):
     sx = torch.empty((M,), dtype=torch.int32, device=dev)
     sw = torch.empty((Nb,), dtype=torch.int32, device=dev)
     y = torch.empty((M, Nb), dtype=dtype, device=dev)
-    if M and Nb:
+    if M and Nb and not Kb:
+        # an empty contraction: F.linear gives the bias (or zeros)
+        y.copy_(b.to(dtype).expand(M, Nb) if b is not None else torch.zeros((), dtype=dtype, device=dev).expand(M, Nb))
+    elif M and Nb:
         with _on_device(x2):
             _lib.call("axs6_nf5_linear_forward", x2.data_ptr(), w2.data_ptr(), _lib.ptr(b), y.data_ptr(),
                       _lib.DTYPE_CODE[dtype], M, Nb, Kb, block_size, int(bool(quantize_input)),
@@ -123,7 +133,7 @@ def backward(grad_output, saved: Saved, block_size: int, quantize_grad: bool,
     dy = grad_output.reshape(-1, saved.n_true).to(saved.dtype)
     if N != saved.n_true:
         dy = _pad_last(dy, block_size)
-    dy = dy.contiguous()
+    dy = _dense(dy)
     dx = torch.empty((M, K), dtype=saved.dtype, device=dev) if need_x else None
     dw = torch.empty((N, K), dtype=torch.float32, device=dev) if need_w else None
     db = torch.empty((N,), dtype=torch.float32, device=dev) if need_b else None
@@ -140,8 +150,12 @@ def backward(grad_output, saved: Saved, block_size: int, quantize_grad: bool,
                       _lib.stream_of(dy))
             if ctr is not None:
                 ctr.add_(1)
-    elif need_w:
-        dw.zero_()
+    else:
+        # no rows (M == 0): the reference's dYq^T X and sum over rows give zeros
+        if dw is not None:
+            dw.zero_()
+        if db is not None:
+            db.zero_()
     if dx is not None:
         if K != saved.k_true:
             dx = dx[:, :saved.k_true]
@@ -167,8 +181,8 @@ def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     if b.shape[0] != K:
         raise RuntimeError(f"{fn}: shapes {tuple(a.shape)} and {tuple(b.shape)} do not contract")
     N = b.shape[1]
-    a2 = _pad_last(a.reshape(-1, K).float(), 32).contiguous()
-    bt = _pad_last(b.float().t(), 32).contiguous()          # [N, K'] rows along the contraction
+    a2 = _dense(_pad_last(a.reshape(-1, K).float(), 32))
+    bt = _dense(_pad_last(b.float().t(), 32))               # [N, K'] rows along the contraction
     M, Kb = a2.shape
     Kp = padded_k(Kb)
     dev = a2.device

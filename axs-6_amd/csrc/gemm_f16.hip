@@ -6,7 +6,7 @@
 // Tiling.  A workgroup of WGM x WGN waves owns a BM x BN tile of C; each wave
 // a (BM/WGM) x (BN/WGN) sub-tile of 16x16 MFMA blocks
 // (v_mfma_f32_16x16x32_f16: K = 32 per instruction, 4 fp32 accumulators per
-// lane; 32x32x16 blocks remain as sweep configurations).  Per K-step of 64 halves the A and B tiles go from HBM straight into
+// lane).  Per K-step of 64 halves the A and B tiles go from HBM straight into
 // LDS (buffer_load ... lds; rows past M/N read as zero through the buffer's
 // range check) while the previous slab is multiplied; two LDS slabs, one
 // barrier per step.  Each 64-half row is 8 slots of 16 bytes, XOR-swizzled
@@ -27,7 +27,6 @@
 // (two 128-byte rows per instruction) cost ~8% of the 4096^3 GEMM, the staged
 // stores ~1%.
 #include <limits.h>
-#include <stdlib.h>
 
 #include "linear_internal.h"
 
@@ -35,11 +34,9 @@ namespace axs6 {
 namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4m __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 64;            // halves per K-step (8 slots of 16 bytes)
 constexpr int kGroupM = 8;
 constexpr int kBufferConfig = 0x00020000;   // raw 32-bit buffer access, gfx9 family
 
@@ -76,70 +73,13 @@ __device__ __forceinline__ int swz(int row, int chunk) {
     return row * (BK * 2) + ((chunk ^ swz_key<BK>(row)) << 4);
 }
 
-// One K-step (64 halves = 4 MFMA K-slices) of the wave's TM x TN blocks.
-// SCHED 0: reads then MFMAs per slice (compiler scheduling); 1/2: the same
-// with the compiler's GEMM interleave strategy iglp_opt(0/1); 3: the next
-// slice's fragments are read into a second register set while the current
-// slice's MFMAs issue.
-template <int BK, int TM, int TN, int SCHED>
-__device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const char* as, const char* bs, int a_row0,
-                                         int b_row0, int fh) {
-    if constexpr (SCHED == 3) {
-        f16x8 af[2][TM], bf[2][TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i) af[0][i] = *reinterpret_cast<const f16x8*>(as + swz<BK>(a_row0 + i * 32, fh));
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bf[0][j] = *reinterpret_cast<const f16x8*>(bs + swz<BK>(b_row0 + j * 32, fh));
-#pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
-            const int cur = kk & 1;
-            if (kk + 1 < BK / 16) {
-                const int chunk = (kk + 1) * 2 + fh;
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-                    af[cur ^ 1][i] = *reinterpret_cast<const f16x8*>(as + swz<BK>(a_row0 + i * 32, chunk));
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    bf[cur ^ 1][j] = *reinterpret_cast<const f16x8*>(bs + swz<BK>(b_row0 + j * 32, chunk));
-            }
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][i], bf[cur][j], acc[i][j], 0, 0, 0);
-        }
-    } else {
-#pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
-            const int chunk = kk * 2 + fh;
-            f16x8 af[TM], bf[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const f16x8*>(as + swz<BK>(a_row0 + i * 32, chunk));
-#pragma unroll
-            for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const f16x8*>(bs + swz<BK>(b_row0 + j * 32, chunk));
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if constexpr (SCHED == 1) __builtin_amdgcn_iglp_opt(0);
-        if constexpr (SCHED == 2) __builtin_amdgcn_iglp_opt(1);
-    }
-}
-
-// The wave's accumulators for a WM x WN sub-tile: 32x32 blocks of
-// v_mfma_f32_32x32x16_f16 (16 floats per lane) or 16x16 blocks of
-// v_mfma_f32_16x16x32_f16 (4 floats per lane).  Same 128 floats per lane for
-// a 128x64 sub-tile either way; the 16x16 instruction runs the same FLOPs per
-// cycle with half-size fragments and, in the 256x256 tiles, clocks higher
-// under the power limit (3-5% shorter GEMMs at 4096^3 and the Llama shapes).
-template <int MF, int WM, int WN> struct WaveAcc;
-template <int WM, int WN> struct WaveAcc<32, WM, WN> {
-    static constexpr int TM = WM / 32, TN = WN / 32, R = 16;
-    f32x16 v[TM][TN];
-};
-template <int WM, int WN> struct WaveAcc<16, WM, WN> {
+// The wave's accumulators for a WM x WN sub-tile: 16x16 blocks of
+// v_mfma_f32_16x16x32_f16, 4 floats per lane (128 per lane for a 128x64
+// sub-tile).  The 16x16x32 instruction runs the same FLOPs per cycle as the
+// 32x32x16 one with half-size fragments and, in the 256x256 tiles, clocks
+// higher under the power limit (3-5% shorter GEMMs at 4096^3 and the Llama
+// shapes than the same kernel on 32x32x16 blocks).
+template <int WM, int WN> struct WaveAcc {
     static constexpr int TM = WM / 16, TN = WN / 16, R = 4;
     f32x4m v[TM][TN];
 };
@@ -148,9 +88,9 @@ template <int WM, int WN> struct WaveAcc<16, WM, WN> {
 // its A and B blocks at K-group l/16 (chunk 4*slice + l/16; 16 consecutive
 // rows per 16-lane group, conflict-free under swz), then TM x TN MFMAs.
 template <int BK, int WM, int WN>
-__device__ __forceinline__ void mma_step16(WaveAcc<16, WM, WN>& acc, const char* as, const char* bs, int a_row0,
+__device__ __forceinline__ void mma_step16(WaveAcc<WM, WN>& acc, const char* as, const char* bs, int a_row0,
                                            int b_row0, int fq) {
-    constexpr int TM = WaveAcc<16, WM, WN>::TM, TN = WaveAcc<16, WM, WN>::TN;
+    constexpr int TM = WaveAcc<WM, WN>::TM, TN = WaveAcc<WM, WN>::TN;
 #pragma unroll
     for (int kk = 0; kk < BK / 32; ++kk) {
         const int chunk = kk * 4 + fq;
@@ -169,25 +109,16 @@ __device__ __forceinline__ void mma_step16(WaveAcc<16, WM, WN>& acc, const char*
 }
 
 // Stages the wave's 32-row block row i (32 x WN floats, row stride LDW) in
-// LDS.  32x32 blocks: accumulator r of block (i, j) is row 8*(r/4) +
-// 4*(lane/32) + r%4, column lane%32.  16x16 blocks: accumulator r of block
-// (2i+h, j) is row 16*h + 4*(lane/16) + r, column lane%16 of the 16x16 block.
-// Both write patterns are bank-conflict free with LDW = WN + 4.
+// LDS: accumulator r of block (2i+h, j) is row 16*h + 4*(lane/16) + r,
+// column lane%16 of the 16x16 block.  The write pattern is bank-conflict
+// free with LDW = WN + 4.
 template <int WM, int WN, int LDW>
-__device__ __forceinline__ void stage_block_row(const WaveAcc<32, WM, WN>& acc, int i, float* ws, int lane) {
-    const int fr = lane & 31, fh = lane >> 5;
-#pragma unroll
-    for (int j = 0; j < WaveAcc<32, WM, WN>::TN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) ws[((r >> 2) * 8 + (r & 3) + fh * 4) * LDW + j * 32 + fr] = acc.v[i][j][r];
-}
-template <int WM, int WN, int LDW>
-__device__ __forceinline__ void stage_block_row(const WaveAcc<16, WM, WN>& acc, int i, float* ws, int lane) {
+__device__ __forceinline__ void stage_block_row(const WaveAcc<WM, WN>& acc, int i, float* ws, int lane) {
     const int fc = lane & 15, fq = lane >> 4;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int j = 0; j < WaveAcc<16, WM, WN>::TN; ++j)
+        for (int j = 0; j < WaveAcc<WM, WN>::TN; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) ws[(h * 16 + fq * 4 + r) * LDW + j * 16 + fc] = acc.v[2 * i + h][j][r];
 }
@@ -269,8 +200,8 @@ __device__ __forceinline__ void store4t(void* out, int64_t ldo, int N, int row, 
 // 4 consecutive columns per lane for all PASSES row groups and their row
 // exponents at once -- one LDS wait per block row instead of two per row
 // group -- and write them with the output type fixed at compile time.
-template <int OUT, int MF, int WM, int WN, int LDW>
-__device__ __forceinline__ void epilogue_store(const WaveAcc<MF, WM, WN>& acc, float* ws, const int (&rexp_l)[WM / 64],
+template <int OUT, int WM, int WN, int LDW>
+__device__ __forceinline__ void epilogue_store(const WaveAcc<WM, WN>& acc, float* ws, const int (&rexp_l)[WM / 64],
                                                const int (&cexp)[4], const float (&cbias)[4], void* out, int64_t ldo,
                                                int M, int N, int row0, int gcol, bool vec, bool nt, int lane) {
     constexpr int LANES_PER_ROW = WN / 4;
@@ -320,7 +251,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // registers are spent on staging.  Lane l of a load instruction lands at
 // byte 16*l of its 1 KiB, i.e. row l/8, slot l%8, and therefore fetches
 // logical chunk (l%8) ^ key(row) -- the same XOR layout the fragment reads use.
-template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED, int MF, int LW>
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int LW>
 __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(GemmK g) {
 #if defined(__HIP_DEVICE_COMPILE__)  // LDS-DMA builtins exist only in the device pass
     constexpr int NW = WGM * WGN;
@@ -387,7 +318,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     for (int i = 0; i < B_INST; ++i) b_goff[i] += kbeg * RB;
     auto lds_ptr = [](char* p) { return (__attribute__((address_space(3))) void*)p; };
 
-    using Acc = WaveAcc<MF, WM, WN>;
+    using Acc = WaveAcc<WM, WN>;
     Acc acc;
 #pragma unroll
     for (int i = 0; i < Acc::TM; ++i)
@@ -410,9 +341,9 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
         }
     }
 
-    // fragment row and K-group of this lane: l%32, l/32 (32x32) or l%16, l/16 (16x16)
-    const int fr = lane % MF;
-    const int fg = lane / MF;
+    // fragment row and K-group of this lane
+    const int fr = lane % 16;
+    const int fg = lane / 16;
     const int a_row0 = wm * WM + fr;
     const int b_row0 = wn * WN + fr;
     for (int kt = 0; kt < KT; ++kt) {
@@ -443,10 +374,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, lds_ptr(slab + b_loff[i]), 16, b_goff[i] + nk * RB, 0, 0, 0);
         }
         const char* slab = smem + (kt % STAGES) * SLAB;
-        if constexpr (MF == 32)
-            mma_step<BK, Acc::TM, Acc::TN, SCHED>(acc.v, slab, slab + BM * RB, a_row0, b_row0, fg);
-        else
-            mma_step16<BK, WM, WN>(acc, slab, slab + BM * RB, a_row0, b_row0, fg);
+        mma_step16<BK, WM, WN>(acc, slab, slab + BM * RB, a_row0, b_row0, fg);
     }
 
     // ---- epilogue through LDS ------------------------------------------------
@@ -491,28 +419,28 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     const bool nt = g.split_stride == 0;     // final output: streaming stores
     const int row0 = m0 + wm * WM;
     if (g.out_dtype == AXS6_F32)
-        epilogue_store<AXS6_F32, MF, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+        epilogue_store<AXS6_F32, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
                                                       vec, nt, lane);
     else if (g.out_dtype == AXS6_BF16)
-        epilogue_store<AXS6_BF16, MF, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+        epilogue_store<AXS6_BF16, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
                                                        vec, nt, lane);
     else
-        epilogue_store<AXS6_F16, MF, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+        epilogue_store<AXS6_F16, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
                                                       vec, nt, lane);
 #endif
 }
 
-template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int SCHED, int MF = 32, int LW = WGM * WGN>
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int LW = WGM * WGN>
 int run_gemm_lds(const GemmK& k, int splits, hipStream_t st) {
     const int tiles = ((k.M + BM - 1) / BM) * ((k.N + BN - 1) / BN);
     const size_t lds = (size_t)STAGES * (BM + BN) * BK * 2;
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED, MF, LW>,
+        (void)hipFuncSetAttribute((const void*)gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, LW>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         attr_set = true;
     }
-    gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, SCHED, MF, LW>
+    gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, LW>
         <<<dim3((unsigned)tiles, (unsigned)splits), WGM * WGN * 64, lds, st>>>(k);
     return check_launch("gemm_f16_lds");
 }
@@ -585,55 +513,36 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(SplitReduceK k) {
     store4(k.out, k.ldo, k.N, k.out_dtype, row, col, v, vec);
 }
 
-// Launch configurations (BMxBN tile / K-slab / LDS stages / waves /
-// schedule variant of mma_step), every wave issuing slab loads unless noted:
-//   0: 256x256 / 64 / 2 / 8 / 2      1: 256x256 / 32 / 4 / 8 / 2
-//   2: 256x256 / 32 / 3 / 8 / 2      3: 256x256 / 32 / 4 / 8 / 0
-//   4: 256x256 / 32 / 4 / 4 / 2      5: 256x256 / 32 / 4 / 8 / 3
-//   6: 256x256 / 64 / 2 / 8 / 0      7: 256x128 / 64 / 3 / 8 / 2
-//   8: 128x128 / 64 / 2 / 4 / 2
-// all on 32x32x16 MFMAs; on 16x16x32 MFMAs:
-//   9: 256x256 / 64 / 2 / 8 / 2, waves 0-3 issue all slab loads
-//  10: 128x128 / 64 / 2 / 4 / 2     11: 9 with every wave loading
-//  12: 128x64 / 64 / 2 / 4 / 2
-// Default: 9; 10 when the 256x256 tiles do not cover the 256 CUs once; 12
-// when the 128x128 ones do not either (8192 x 256 outputs: 128 -> 256
-// workgroups, 9.7 -> 7.5 us at K 256, 15.1 -> 11.0 us at K 1024; 2048 x 768
-// at K 3072 34.5 -> 29.3 us; where 128x128 tiles already fill the CUs,
-// 128x64 ones are up to 11% slower).
-// 16x16x32 against 32x32x16 (11 against 0, 10 against 8): 0-5% shorter on
-// every shape tried (4096^3, the Llama-7B MLP shapes, the 768/3072 ones).
-// Loads from waves 0-3 only (9 against 11): 6-12% shorter on the large
-// shapes.  Waves are placed on the CU's four SIMDs round-robin, so each SIMD
-// holds one loading and one compute-only wave.  When all eight waves leave
-// the barrier and issue their loads together, the address unit (~64 bytes
-// per clock) backs up and both waves of a SIMD stall in the issue, leaving
-// its MFMA pipe idle; with one loader per SIMD the other wave runs its MFMAs
-// meanwhile (the loads still land well inside the K-step).  Measured: the
-// stalled-issue counters SQ_VMEM_TA_ADDR_FIFO_FULL / _CMD_FIFO_FULL were 50x
-// those of hipBLASLt's fp16 kernel with every wave loading.
+// Launch configurations (BMxBN tile / 64-half K-slab / LDS stages / waves),
+// all on 16x16x32 MFMAs:
+//   big:    256x256 / 2 stages / 8 waves (2x4), waves 0-3 issue the slab loads
+//   small:  128x128 / 2 stages / 4 waves (2x2)
+//   narrow: 128x64 / 2 stages (3 on contractions of 32+ K-steps) / 4 waves
+// Big by default; small when the 256x256 tiles do not cover the 256 CUs
+// once; narrow when the 128x128 ones do not either (8192 x 256 outputs: 128
+// -> 256 workgroups, 9.7 -> 7.5 us at K 256, 15.1 -> 11.0 us at K 1024;
+// 2048 x 768 at K 3072 34.5 -> 29.3 us; where 128x128 tiles already fill the
+// CUs, 128x64 ones are up to 11% slower).
+// Loads from waves 0-3 only (against every wave loading): 6-12% shorter on
+// the large shapes.  Waves are placed on the CU's four SIMDs round-robin, so
+// each SIMD holds one loading and one compute-only wave.  When all eight
+// waves leave the barrier and issue their loads together, the address unit
+// (~64 bytes per clock) backs up and both waves of a SIMD stall in the
+// issue, leaving its MFMA pipe idle; with one loader per SIMD the other wave
+// runs its MFMAs meanwhile (the loads still land well inside the K-step).
+// Measured: the stalled-issue counters SQ_VMEM_TA_ADDR_FIFO_FULL /
+// _CMD_FIFO_FULL were 50x those of hipBLASLt's fp16 kernel with every wave
+// loading.
 // The epilogue of a tile (LDS staging, exponent scaling, stores) costs a
 // fixed ~7 us per 256x256 f32 tile and CU, all of a short-K GEMM's runtime
 // when 32 CUs carry it; 128x128 tiles spread it over 4x the CUs, two
-// workgroups sharing a CU.  AXS6_GEMM_CFG=<n> forces a configuration for
-// launch-shape sweeps.
-constexpr int kCfgBig = 9, kCfgSmall = 10, kCfgNarrow = 12;
-constexpr int kNarrowDeepSteps = 32;   // 64-deep K-steps per workgroup from which 12 runs three slabs
-
-int gemm_cfg_env() {
-    static int v = [] {
-        const char* s = getenv("AXS6_GEMM_CFG");
-        int n = s ? atoi(s) : -1;
-        return (n >= 0 && n <= 12) ? n : -1;
-    }();
-    return v;
-}
+// workgroups sharing a CU.
+enum GemmCfg { kCfgBig = 0, kCfgSmall = 1, kCfgNarrow = 2 };
+constexpr int kNarrowDeepSteps = 32;   // 64-deep K-steps per workgroup from which narrow runs three slabs
 
 int64_t tiles_of(int64_t M, int64_t N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 int pick_cfg(int64_t M, int64_t N) {
-    const int env = gemm_cfg_env();
-    if (env >= 0) return env;
     if (tiles_of(M, N, 256, 256) >= 256) return kCfgBig;
     return tiles_of(M, N, 128, 128) >= 256 ? kCfgSmall : kCfgNarrow;
 }
@@ -641,22 +550,16 @@ int pick_cfg(int64_t M, int64_t N) {
 // output tile of a configuration
 void cfg_tile(int cfg, int* bm, int* bn) {
     *bm = 256; *bn = 256;
-    if (cfg == 7) *bn = 128;
-    if (cfg == 8 || cfg == 10) *bm = *bn = 128;
+    if (cfg == kCfgSmall) *bm = *bn = 128;
     if (cfg == kCfgNarrow) { *bm = 128; *bn = 64; }
 }
-
-// configuration of a split-K launch: one with 64-half K-slabs (the split
-// ranges are counted in them); forced sweep configurations with 32-half
-// slabs fall back to the default large tiles
-int split_cfg(int cfg) { return (cfg == 0 || cfg >= 8) ? cfg : kCfgBig; }
 
 }  // namespace
 
 int gemm_split_count(int64_t M, int64_t N, int64_t Kp) {
-    // split launches use configurations with 64-half K-slabs (split_cfg)
+    if (M <= 0 || N <= 0) return 1;   // nothing to split (and no division by a zero tile count)
     int bm, bn;
-    cfg_tile(split_cfg(pick_cfg(M, N)), &bm, &bn);
+    cfg_tile(pick_cfg(M, N), &bm, &bn);
     const int64_t tiles = tiles_of(M, N, bm, bn);
     const int64_t iters = Kp / kGemmK;
     if (tiles >= 64 || iters < 8) return 1;
@@ -715,12 +618,14 @@ static int launch_gemm_one(const GemmArgs& a, hipStream_t st, bool cut) {
     if (a.lda % 8 || a.ldb % 8 || (uintptr_t)a.A % 16 || (uintptr_t)a.B % 16)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: operands must be 16-byte aligned with ld a multiple of 8");
     if (a.Kp > a.lda || a.Kp > a.ldb) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: Kp exceeds the leading dimension");
+    if (a.ldo < a.N) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: ldo (%lld) is smaller than N (%lld)",
+                                 (long long)a.ldo, (long long)a.N);
     // buffer offsets are 32-bit: every operand byte (plus one tile of rows) must be addressable
     if ((a.M + 256) * a.lda * 2 >= ((int64_t)1 << 31) || (a.N + 256) * a.ldb * 2 >= ((int64_t)1 << 31))
         return fail(AXS6_ERR_UNSUPPORTED, "gemm: operand larger than 2 GiB");
     if (a.M > INT_MAX || a.N > INT_MAX || a.Kp > INT_MAX)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: dimension exceeds int32");
-    if (cut && gemm_cfg_env() < 0) {
+    if (cut) {
         const TailCut c = tail_cut(a.M, a.N);
         if (c.rows || c.cols) {
             const int esize = a.out_dtype == AXS6_F32 ? 4 : 2;
@@ -762,25 +667,15 @@ static int launch_gemm_one(const GemmArgs& a, hipStream_t st, bool cut) {
             split ? (int)AXS6_F32 : a.out_dtype, per, split ? a.M * a.N : 0};
     int rc;
     const int cfg = pick_cfg(a.M, a.N);
-    switch (split ? split_cfg(cfg) : cfg) {
-        case 1: rc = run_gemm_lds<256, 256, 32, 4, 2, 4, 2>(k, splits, st); break;
-        case 2: rc = run_gemm_lds<256, 256, 32, 3, 2, 4, 2>(k, splits, st); break;
-        case 3: rc = run_gemm_lds<256, 256, 32, 4, 2, 4, 0>(k, splits, st); break;
-        case 4: rc = run_gemm_lds<256, 256, 32, 4, 2, 2, 2>(k, splits, st); break;
-        case 5: rc = run_gemm_lds<256, 256, 32, 4, 2, 4, 3>(k, splits, st); break;
-        case 6: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 0>(k, splits, st); break;
-        case 7: rc = run_gemm_lds<256, 128, 64, 3, 4, 2, 2>(k, splits, st); break;
-        case 8: rc = run_gemm_lds<128, 128, 64, 2, 2, 2, 2>(k, splits, st); break;
-        case kCfgSmall: rc = run_gemm_lds<128, 128, 64, 2, 2, 2, 2, 16>(k, splits, st); break;
-        case 0: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2>(k, splits, st); break;
-        case 11: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2, 16>(k, splits, st); break;
+    switch (cfg) {
+        case kCfgSmall: rc = run_gemm_lds<128, 128, 64, 2, 2, 2>(k, splits, st); break;
         case kCfgNarrow:
             // a long contraction on the small tiles: a third slab in flight
             // (2048 x 768, K 3072: 28.5 -> 21.3 us; at K <= 1024 it costs 3-5%)
-            if (per >= kNarrowDeepSteps) rc = run_gemm_lds<128, 64, 64, 3, 2, 2, 2, 16, 4>(k, splits, st);
-            else rc = run_gemm_lds<128, 64, 64, 2, 2, 2, 2, 16, 4>(k, splits, st);
+            if (per >= kNarrowDeepSteps) rc = run_gemm_lds<128, 64, 64, 3, 2, 2>(k, splits, st);
+            else rc = run_gemm_lds<128, 64, 64, 2, 2, 2>(k, splits, st);
             break;
-        default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 2, 16, 4>(k, splits, st); break;   // kCfgBig
+        default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 4>(k, splits, st); break;   // kCfgBig
     }
     if (rc || !split) return rc;
     SplitReduceK r{a.split_partial, splits, a.M * a.N, (int)a.M, (int)a.N, a.row_exp, a.col_exp, a.glob_exp,

@@ -13,10 +13,7 @@ namespace axs6 {
 namespace {
 
 constexpr int kThreads = 256;
-#ifndef AXS6_FQ_UNROLL
-#define AXS6_FQ_UNROLL 2
-#endif
-constexpr int kUnroll = AXS6_FQ_UNROLL;  // 16-byte vectors in flight per thread
+constexpr int kUnroll = 2;  // 16-byte vectors in flight per thread
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 

@@ -23,7 +23,6 @@
 // General path (ragged last dim or unaligned views): one element per lane,
 // one block per `block` lanes, shuffle reductions.
 #include <math.h>
-#include <stdlib.h>
 
 #pragma clang fp contract(off)
 
@@ -32,23 +31,11 @@
 namespace axs6 {
 namespace {
 
-// Streaming loads/stores.  Plain (cached) accesses measured faster on MI355X
-// than nontemporal ones at every unroll depth and grid size tried (42.6 us vs
-// 47.7 us best case at 8192x4096 f32); AXS6_FQ_NT selects the latter.
-__device__ __forceinline__ u32x4 stream_load(const u32x4* p) {
-#ifdef AXS6_FQ_NT
-    return __builtin_nontemporal_load(p);
-#else
-    return *p;
-#endif
-}
-__device__ __forceinline__ void stream_store(u32x4 v, u32x4* p) {
-#ifdef AXS6_FQ_NT
-    __builtin_nontemporal_store(v, p);
-#else
-    *p = v;
-#endif
-}
+// Streaming loads/stores are plain (cached) accesses: nontemporal ones
+// measured slower on MI355X at every unroll depth and grid size tried
+// (42.6 us against 47.7 us best case at 8192x4096 f32).
+__device__ __forceinline__ u32x4 stream_load(const u32x4* p) { return *p; }
+__device__ __forceinline__ void stream_store(u32x4 v, u32x4* p) { *p = v; }
 
 // ---- fake-quantize kernels -----------------------------------------------
 
@@ -362,22 +349,14 @@ int num_cus() {
     return cached[dev];
 }
 
-// Workgroups per CU the grid-stride kernels are capped at (tunable through
-// AXS6_FQ_WG_PER_CU for launch-shape sweeps).  Default 1024, i.e. in effect
-// one workgroup per 256*kUnroll vectors: at 8192x4096 f32 that grid (16384
-// workgroups) beat caps of 2..16 per CU.
-int wg_per_cu() {
-    static int v = [] {
-        const char* s = getenv("AXS6_FQ_WG_PER_CU");
-        int n = s ? atoi(s) : 0;
-        return (n > 0 && n <= 1024) ? n : 1024;
-    }();
-    return v;
-}
+// Workgroups per CU the grid-stride kernels are capped at: 1024, i.e. in
+// effect one workgroup per 256*kUnroll vectors -- at 8192x4096 f32 that grid
+// (16384 workgroups) beat caps of 2..16 per CU.
+constexpr int kWgPerCu = 1024;
 
 int64_t capped_grid(int64_t work_items, int64_t per_wg) {
     int64_t need = (work_items + per_wg - 1) / per_wg;
-    int64_t cap = (int64_t)num_cus() * wg_per_cu();
+    int64_t cap = (int64_t)num_cus() * kWgPerCu;
     if (need < 1) need = 1;
     return need < cap ? need : cap;
 }

@@ -85,6 +85,9 @@ extern "C" int axs6_nf5_pack_rows(const void* x, int32_t dtype, int64_t rows, in
     if (rows < 0 || cols < 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: negative shape", fn);
     if (rows == 0) return AXS6_OK;
     if (!x || !row_shift) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    if (out_f16 && ld_out < cols_pad)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: ld_out (%lld) is smaller than cols_pad (%lld)", fn,
+                    (long long)ld_out, (long long)cols_pad);
     DeviceTables t;
     int rc = device_tables(&t);
     if (rc) return rc;
@@ -159,7 +162,7 @@ extern "C" int axs6_nf5_linear_forward(const void* x, const void* w, const float
 extern "C" size_t axs6_nf5_linear_backward_workspace(int64_t M, int64_t N, int64_t K, int32_t need_dx,
                                                      int32_t need_dw, int32_t need_db) {
     if (M < 0 || N < 0 || K < 0) return 0;
-    return bwd_layout(M, N, K, need_dx != 0, need_dw != 0, need_db != 0).total;
+    return bwd_layout(M, N, K, need_dx != 0 && K > 0, need_dw != 0 && K > 0, need_db != 0).total;
 }
 
 extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M, int64_t N, int64_t K,
@@ -170,7 +173,8 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
     const char* fn = "axs6_nf5_linear_backward";
     int rc = check_dims(fn, M, N, K, block_size, dtype);
     if (rc) return rc;
-    const bool need_dx = dx != nullptr, need_dw = dw != nullptr, need_db = db != nullptr;
+    // with K == 0, dX [M, 0] and dW [N, 0] are empty; db is still the column sums of dYq
+    const bool need_dx = dx != nullptr && K > 0, need_dw = dw != nullptr && K > 0, need_db = db != nullptr;
     if (M == 0 || N == 0 || (!need_dx && !need_dw && !need_db)) return AXS6_OK;
     if (!dy) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null dy", fn);
     if ((need_dx && (!wq_f16 || !w_shift)) || (need_dw && (!xq_f16 || !x_shift)))

@@ -862,6 +862,9 @@ int check_pack_rows(const PackRowsArgs& a, RowsShape* sh_out) {
         return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: column exponents not 16-byte aligned");
     if (a.out && (a.ld_out % 8 != 0 || (uintptr_t)a.out % 16 != 0 || a.cols_pad % 8 != 0 || a.cols_pad < a.cols))
         return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: output must be 16-byte aligned with padded width >= cols");
+    if (a.out && a.ld_out < a.cols_pad)   // rows would overlap and the last row's padding run past the buffer
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: ld_out (%lld) is smaller than cols_pad (%lld)",
+                    (long long)a.ld_out, (long long)a.cols_pad);
     const int64_t nvec = a.cols / V;
     if (nvec > kRowsMaxVec) {
         // longer than a workgroup holds in registers: statistics pass + tiled pack

@@ -534,8 +534,7 @@ def pmc_pass() -> int:
 
 def gemm_only(n: int, reps: int = 50) -> int:
     """Times the fp16 MFMA GEMM alone at n^3 (small-integer fp16 operands, so
-    the fp32 result is exact and checked), for launch-shape sweeps with
-    AXS6_GEMM_CFG=<config>.  Prints one JSON line."""
+    the fp32 result is exact and checked).  Prints one JSON line."""
     import torch
 
     from axs import _lib
@@ -564,7 +563,7 @@ def gemm_only(n: int, reps: int = 50) -> int:
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) / reps * 1e3
-    print(json.dumps({"gemm_cfg": os.environ.get("AXS6_GEMM_CFG", "default"), "n": n, "us": round(us, 1),
+    print(json.dumps({"n": n, "us": round(us, 1),
                       "TFLOPs": round(2 * n ** 3 / us / 1e6, 1), "exact": exact}), flush=True)
     return 0 if exact else 1
 

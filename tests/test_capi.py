@@ -105,3 +105,25 @@ def test_invalid_arguments_rejected_without_device():
 def test_error_raises_runtime_error():
     with pytest.raises(RuntimeError, match="block_size"):
         _lib.call("axs6_nf5_fake_quantize", 1, 1, 0, 4, 32, 17, 0, 0, 0, None, None)
+
+
+def test_backward_workspace_query_with_empty_dimensions():
+    """No rows (M = 0) or an empty contraction (K = 0) is a normal query,
+    not a division by a zero tile count."""
+    L = _lib.lib()
+    for M, N, K in ((0, 512, 256), (0, 4096, 4096), (64, 512, 0), (8192, 4096, 0), (0, 0, 0)):
+        ws = L.axs6_nf5_linear_backward_workspace(M, N, K, 1, 1, 1)
+        assert ws >= 0
+    # K = 0 still needs the bias-gradient partials, nothing for dX / dW
+    assert L.axs6_nf5_linear_backward_workspace(64, 512, 0, 1, 1, 0) <= \
+        L.axs6_nf5_linear_backward_workspace(64, 512, 0, 1, 1, 1)
+
+
+def test_leading_dimensions_checked_without_device():
+    # pack_rows: ld_out below cols_pad would overlap rows and write the last
+    # row's padding past the buffer
+    rc, msg = _status("axs6_nf5_pack_rows", 256, 0, 4, 128, 32, 1, 0, 0, None, 256, 64, 128, 256, None, None)
+    assert rc == 1 and "ld_out" in msg
+    # GEMM: ldo below N
+    rc, msg = _status("axs6_gemm_f16_nt", 256, 64, 256, 64, 64, 64, 64, None, None, None, 256, 32, 0, None)
+    assert rc == 1 and "ldo" in msg
