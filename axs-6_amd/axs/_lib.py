@@ -55,6 +55,8 @@ _SIGNATURES: dict[str, list] = {
     "axs6_multi_tensor_unscale_clip": [_vp, _vp, _vp, _i32, ctypes.c_float, ctypes.c_float, _i32, _vp, _i64, _vp, _vp],
     "axs6_nf5_linear_backward": [_vp, _i32, _i64, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _vp, _vp,
                                  _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp, _vp],
+    "axs6_nf5_linear_backward_noalloc": [_vp, _i32, _i64, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _vp,
+                                         _vp, _vp, _vp, _vp, _vp, _vp],
 }
 # entry points that return a value rather than an axs6_status
 _RESTYPES = {"axs6_linear_padded_k": _i64, "axs6_nf5_linear_backward_workspace": ctypes.c_size_t,

@@ -28,6 +28,10 @@ void host_tables(float* codebook, float* lut, uint8_t* rev, uint8_t* band);
 // Uploads tables to the current device on first use; fills *out.
 int device_tables(DeviceTables* out);
 
+// Resolves the current device's address of the allocation-free backward's
+// scratch array (nf5_linear.hip); called by axs6_init.
+int init_noalloc_scratch();
+
 // Records a message for axs6_last_error() and returns `code`.
 int fail(int code, const char* fmt, ...);
 

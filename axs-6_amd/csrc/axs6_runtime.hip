@@ -177,7 +177,8 @@ const char* axs6_last_error(void) { return axs6::g_err; }
 int axs6_init(void) {
     axs6::g_err[0] = 0;
     axs6::DeviceTables t;
-    return axs6::device_tables(&t);
+    int rc = axs6::device_tables(&t);
+    return rc ? rc : axs6::init_noalloc_scratch();
 }
 
 int axs6_get_tables(float* codebook, float* lut, uint8_t* reverse_lut, uint8_t* log2_band) {

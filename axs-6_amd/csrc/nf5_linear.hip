@@ -23,6 +23,8 @@
 //   db = reduce of the partials (fixed order).
 #include <string.h>
 
+#include <mutex>
+
 #include "linear_internal.h"
 
 namespace axs6 {
@@ -32,12 +34,16 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct BwdLayout {
+    bool dx, dw, db;   // which gradients the layout serves
     size_t gmax, t, stats, a1, wqt, a2t, xqt, partial, splitk, splitk_bytes, total;
 };
 
 BwdLayout bwd_layout(int64_t M, int64_t N, int64_t K, bool dx, bool dw, bool db) {
     const int64_t Kp = pad_to(K, kGemmK), Np = pad_to(N, kGemmK), Mp = pad_to(M, kGemmK);
     BwdLayout L{};
+    L.dx = dx;
+    L.dw = dw;
+    L.db = db;
     size_t off = 0;
     auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
     L.gmax = take(sizeof(int32_t));
@@ -165,32 +171,50 @@ extern "C" size_t axs6_nf5_linear_backward_workspace(int64_t M, int64_t N, int64
     return bwd_layout(M, N, K, need_dx != 0 && K > 0, need_dw != 0 && K > 0, need_db != 0).total;
 }
 
-extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M, int64_t N, int64_t K,
-                                        int32_t block_size, int32_t quantize_grad, uint64_t seed, uint64_t offset,
-                                        const void* xq_f16, const int32_t* x_shift, const void* wq_f16,
-                                        const int32_t* w_shift, void* dx, float* dw, float* db, void* workspace,
-                                        size_t workspace_bytes, const uint64_t* seed_dev, void* stream) {
-    const char* fn = "axs6_nf5_linear_backward";
-    int rc = check_dims(fn, M, N, K, block_size, dtype);
+namespace axs6 {
+namespace {
+
+struct BwdCall {
+    const void* dy; int32_t dtype; int64_t M, N, K; int32_t block_size, quantize_grad; uint64_t seed, offset;
+    const void* xq_f16; const int32_t* x_shift; const void* wq_f16; const int32_t* w_shift;
+    void* dx; float* dw; float* db; const uint64_t* seed_dev; void* stream;
+};
+
+// Argument checks shared by both backward entry points; *run is false when
+// there is nothing to compute (empty shapes, no gradient requested).
+int bwd_check(const char* fn, const BwdCall& c, bool* run, BwdLayout* L) {
+    *run = false;
+    int rc = check_dims(fn, c.M, c.N, c.K, c.block_size, c.dtype);
     if (rc) return rc;
     // with K == 0, dX [M, 0] and dW [N, 0] are empty; db is still the column sums of dYq
-    const bool need_dx = dx != nullptr && K > 0, need_dw = dw != nullptr && K > 0, need_db = db != nullptr;
-    if (M == 0 || N == 0 || (!need_dx && !need_dw && !need_db)) return AXS6_OK;
-    if (!dy) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null dy", fn);
-    if ((need_dx && (!wq_f16 || !w_shift)) || (need_dw && (!xq_f16 || !x_shift)))
+    const bool need_dx = c.dx != nullptr && c.K > 0, need_dw = c.dw != nullptr && c.K > 0, need_db = c.db != nullptr;
+    if (c.M == 0 || c.N == 0 || (!need_dx && !need_dw && !need_db)) return AXS6_OK;
+    if (!c.dy) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null dy", fn);
+    if ((need_dx && (!c.wq_f16 || !c.w_shift)) || (need_dw && (!c.xq_f16 || !c.x_shift)))
         return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: packed operands from the forward are required", fn);
-    const BwdLayout L = bwd_layout(M, N, K, need_dx, need_dw, need_db);
-    if (!workspace || workspace_bytes < L.total || (uintptr_t)workspace % kAlign)
-        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: workspace of %zu bytes (256-byte aligned) required, got %zu",
-                    fn, L.total, workspace_bytes);
+    *L = bwd_layout(c.M, c.N, c.K, need_dx, need_dw, need_db);
+    *run = true;
+    return AXS6_OK;
+}
+
+// The backward's launches with `workspace` laid out by L (every byte a kernel
+// reads is written earlier in the same call, so nothing needs clearing).
+int bwd_run(const BwdCall& c, const BwdLayout& L, char* ws) {
+    const void* dy = c.dy;
+    const int32_t dtype = c.dtype, block_size = c.block_size;
+    const int64_t M = c.M, N = c.N, K = c.K;
+    const int32_t* x_shift = c.x_shift;
+    const int32_t* w_shift = c.w_shift;
+    float* db = c.db;
+    const bool need_dx = L.dx, need_dw = L.dw, need_db = L.db;
+    int rc;
     DeviceTables t;
     if ((rc = device_tables(&t))) return rc;
-    hipStream_t st = (hipStream_t)stream;
-    char* ws = (char*)workspace;
+    hipStream_t st = (hipStream_t)c.stream;
     const int64_t Kp = pad_to(K, kGemmK), Np = pad_to(N, kGemmK), Mp = pad_to(M, kGemmK);
     int32_t* gmax = (int32_t*)(ws + L.gmax);
     int32_t* tshift = (int32_t*)(ws + L.t);
-    const bool fq = quantize_grad != 0;
+    const bool fq = c.quantize_grad != 0;
 
     if (need_dx || need_dw) {
         RowStatsArgs s{dy, dtype, M, N, block_size, need_dx ? w_shift : nullptr, tshift,
@@ -198,7 +222,7 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
         if ((rc = launch_row_stats(s, t, st))) return rc;
     }
     if (need_dx || need_dw || need_db) {
-        PackTArgs p{dy, dtype, M, N, block_size, fq, fq, seed, offset, seed_dev, x_shift, need_dw ? gmax : nullptr,
+        PackTArgs p{dy, dtype, M, N, block_size, fq, fq, c.seed, c.offset, c.seed_dev, x_shift, need_dw ? gmax : nullptr,
                     need_dw ? (_Float16*)(ws + L.a2t) : nullptr, Mp,
                     need_dx ? (_Float16*)(ws + L.a1) : nullptr, Np, w_shift, tshift,
                     need_db ? (float*)(ws + L.partial) : nullptr};
@@ -207,8 +231,8 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
     // contraction-contiguous copies of the forward's operands, one launch
     _Float16* wqt = need_dx ? (_Float16*)(ws + L.wqt) : nullptr;
     _Float16* xqt = need_dw ? (_Float16*)(ws + L.xqt) : nullptr;
-    const TransposeF16 tw{(const _Float16*)wq_f16, N, Kp, Kp, wqt, Kp, Np, Np};
-    const TransposeF16 tx{(const _Float16*)xq_f16, M, Kp, Kp, xqt, Kp, Mp, Mp};
+    const TransposeF16 tw{(const _Float16*)c.wq_f16, N, Kp, Kp, wqt, Kp, Np, Np};
+    const TransposeF16 tx{(const _Float16*)c.xq_f16, M, Kp, Kp, xqt, Kp, Mp, Mp};
     // the bias gradient's ordered reduction of the pack's partial sums rides in
     // the same launch (or runs alone when no operand is transposed)
     const float* partial = need_db ? (const float*)(ws + L.partial) : nullptr;
@@ -221,14 +245,91 @@ extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M
     }
     if (need_dx) {
         GemmArgs g{(const _Float16*)(ws + L.a1), Np, wqt, Np, M, K, Np, tshift, nullptr, nullptr, 0, nullptr,
-                   dx, K, dtype, L.splitk_bytes ? (float*)(ws + L.splitk) : nullptr, L.splitk_bytes};
+                   c.dx, K, dtype, L.splitk_bytes ? (float*)(ws + L.splitk) : nullptr, L.splitk_bytes};
         if ((rc = launch_gemm_f16(g, st))) return rc;
     }
     if (need_dw) {
         _Float16* a2t = (_Float16*)(ws + L.a2t);
-        GemmArgs g{a2t, Mp, xqt, Mp, N, K, Mp, nullptr, nullptr, gmax, -15, nullptr, dw, K, AXS6_F32,
+        GemmArgs g{a2t, Mp, xqt, Mp, N, K, Mp, nullptr, nullptr, gmax, -15, nullptr, c.dw, K, AXS6_F32,
                    L.splitk_bytes ? (float*)(ws + L.splitk) : nullptr, L.splitk_bytes};
         if ((rc = launch_gemm_f16(g, st))) return rc;
     }
     return AXS6_OK;
+}
+
+// Scratch of the allocation-free backward: one instance per device, resolved
+// to its device address once per device (hipGetSymbolAddress with that device
+// current).  In host code the array's name is only a host-side handle; kernels
+// receive the resolved address.  Every call on a device shares the array, so
+// calls that overlap on one device race.
+static __device__ __align__(256) unsigned char scratch[AXS6_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch[kScratchDevices];
+
+int noalloc_scratch(char** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0) return fail(AXS6_ERR_NO_DEVICE, "no current HIP device: %s", hipGetErrorString(e));
+    if (dev >= kScratchDevices) return fail(AXS6_ERR_UNSUPPORTED, "device ordinal %d beyond %d", dev, kScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        char* ptr = nullptr;
+        if ((e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch))) != hipSuccess || !ptr)
+            return fail(AXS6_ERR_HIP, "scratch address lookup on device %d failed: %s", dev, hipGetErrorString(e));
+        g_scratch[dev] = ptr;
+    }
+    *out = g_scratch[dev];
+    return AXS6_OK;
+}
+
+}  // namespace
+
+// Resolves the current device's scratch address (the library's init call).
+int init_noalloc_scratch() {
+    char* p;
+    return noalloc_scratch(&p);
+}
+
+}  // namespace axs6
+
+extern "C" int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M, int64_t N, int64_t K,
+                                        int32_t block_size, int32_t quantize_grad, uint64_t seed, uint64_t offset,
+                                        const void* xq_f16, const int32_t* x_shift, const void* wq_f16,
+                                        const int32_t* w_shift, void* dx, float* dw, float* db, void* workspace,
+                                        size_t workspace_bytes, const uint64_t* seed_dev, void* stream) {
+    const char* fn = "axs6_nf5_linear_backward";
+    const BwdCall c{dy, dtype, M, N, K, block_size, quantize_grad, seed, offset, xq_f16, x_shift, wq_f16, w_shift,
+                    dx, dw, db, seed_dev, stream};
+    bool run;
+    BwdLayout L;
+    int rc = bwd_check(fn, c, &run, &L);
+    if (rc || !run) return rc;
+    if (!workspace || workspace_bytes < L.total || (uintptr_t)workspace % kAlign)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: workspace of %zu bytes (256-byte aligned) required, got %zu",
+                    fn, L.total, workspace_bytes);
+    return bwd_run(c, L, (char*)workspace);
+}
+
+extern "C" int axs6_nf5_linear_backward_noalloc(const void* dy, int32_t dtype, int64_t M, int64_t N, int64_t K,
+                                                int32_t block_size, int32_t quantize_grad, uint64_t seed,
+                                                uint64_t offset, const void* xq_f16, const int32_t* x_shift,
+                                                const void* wq_f16, const int32_t* w_shift, void* dx, float* dw,
+                                                float* db, const uint64_t* seed_dev, void* stream) {
+    const char* fn = "axs6_nf5_linear_backward_noalloc";
+    const BwdCall c{dy, dtype, M, N, K, block_size, quantize_grad, seed, offset, xq_f16, x_shift, wq_f16, w_shift,
+                    dx, dw, db, seed_dev, stream};
+    bool run;
+    BwdLayout L;
+    int rc = bwd_check(fn, c, &run, &L);
+    if (rc || !run) return rc;
+    if (L.total > (size_t)AXS6_NOALLOC_SCRATCH_BYTES)
+        return fail(AXS6_ERR_UNSUPPORTED,
+                    "%s: this shape needs %zu bytes of scratch, beyond the library's fixed %llu bytes; "
+                    "use axs6_nf5_linear_backward with a caller workspace", fn, L.total,
+                    (unsigned long long)AXS6_NOALLOC_SCRATCH_BYTES);
+    char* ws;
+    if ((rc = noalloc_scratch(&ws))) return rc;
+    return bwd_run(c, L, ws);
 }

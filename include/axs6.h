@@ -204,6 +204,28 @@ int axs6_nf5_linear_backward(const void* dy, int32_t dtype, int64_t M, int64_t N
                              const int32_t* w_shift, void* dx, float* dw, float* db, void* workspace,
                              size_t workspace_bytes, const uint64_t* seed_dev, void* stream);
 
+/* Largest backward workspace axs6_nf5_linear_backward_noalloc serves: the size
+ * of the library's fixed per-device scratch array (64 MiB), which each device
+ * the library runs on holds until the process ends. */
+#define AXS6_NOALLOC_SCRATCH_BYTES (64ull << 20)
+
+/* axs6_nf5_linear_backward without a workspace argument and without any
+ * allocation: the workspace lives in the library's fixed per-device scratch
+ * array (its address resolved by axs6_init or on the first call on a device).
+ * Same arguments, kernels and results as axs6_nf5_linear_backward; shapes whose
+ * workspace (axs6_nf5_linear_backward_workspace) exceeds
+ * AXS6_NOALLOC_SCRATCH_BYTES return AXS6_ERR_UNSUPPORTED.  Every call on a
+ * device shares that device's array: calls that overlap on one device (two
+ * streams, two host threads) race and must be serialised by the caller.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+int axs6_nf5_linear_backward_noalloc(const void* dy, int32_t dtype, int64_t M, int64_t N, int64_t K,
+                                     int32_t block_size, int32_t quantize_grad, uint64_t seed, uint64_t offset,
+                                     const void* xq_f16, const int32_t* x_shift, const void* wq_f16,
+                                     const int32_t* w_shift, void* dx, float* dw, float* db,
+                                     const uint64_t* seed_dev, void* stream);
+
 /* ---- training-step glue ----------------------------------------------------
  * Gradient unscale + overflow check + global-norm clip over a list of
  * gradient tensors: replaces the per-parameter `grad.div_(loss_scale)`, the

@@ -127,3 +127,28 @@ def test_leading_dimensions_checked_without_device():
     # GEMM: ldo below N
     rc, msg = _status("axs6_gemm_f16_nt", 256, 64, 256, 64, 64, 64, 64, None, None, None, 256, 32, 0, None)
     assert rc == 1 and "ldo" in msg
+
+
+def test_noalloc_backward_rejects_shapes_beyond_its_scratch_without_device():
+    """The allocation-free backward refuses a shape whose workspace exceeds
+    its fixed scratch before it looks up a device or launches anything."""
+    L = _lib.lib()
+    limit = 64 << 20
+    M, N, K = 8192, 4096, 11008
+    assert L.axs6_nf5_linear_backward_workspace(M, N, K, 1, 1, 1) > limit
+    p = 256   # never dereferenced: the size check comes first
+    rc, msg = _status("axs6_nf5_linear_backward_noalloc", p, 0, M, N, K, 32, 1, 0, 0, p, p, p, p, p, p, p,
+                      None, None)
+    assert rc == 2 and "scratch" in msg
+    # dX alone at this shape still exceeds it
+    rc, msg = _status("axs6_nf5_linear_backward_noalloc", p, 0, M, N, K, 32, 0, 0, 0, p, p, p, p, p, None,
+                      None, None, None)
+    assert rc == 2 and "scratch" in msg
+    # argument checks are the workspace entry point's
+    rc, msg = _status("axs6_nf5_linear_backward_noalloc", p, 0, 64, 48, 64, 32, 0, 0, 0, p, p, p, p, p, p, p,
+                      None, None)
+    assert rc == 1 and "multiples of block_size" in msg
+    # nothing requested, or no rows: a no-op
+    rc, _ = _status("axs6_nf5_linear_backward_noalloc", p, 0, 0, 64, 64, 32, 0, 0, 0, p, p, p, p, p, p, p,
+                    None, None)
+    assert rc == 0
