@@ -3,10 +3,20 @@
 Mirrors ``axs/unified/mixed_precision.py`` of the reference
 (``_AXSLinearBF16Function`` :65-155, ``axs_linear_mixed_precision`` :158,
 ``AXSLinearMixedPrecision`` :193-269, ``convert_to_axs_mixed_precision``
-:277-349, ``estimate_memory_savings`` :357-401): fp32 master weights, input
-and weight rounded to bf16 *before* fake-quantization, bf16 output, dX in
-bf16, dW in fp32, and db from the unquantized output gradient.  The GEMMs are
-the fp16-MFMA quantized-linear kernels fed with the bf16 values.
+:277-349, ``estimate_memory_savings`` :357-401), with its arithmetic:
+
+* forward (:96-108): input and weight cast to bf16, fake-quantized (fp32
+  arithmetic, result rounded to bf16), contracted with fp32 accumulation,
+  plus the bias rounded to bf16, output rounded to bf16;
+* backward (:128-153): dY cast to bf16 and stochastically fake-quantized
+  (rounded to bf16); dX = dYq . FQ(W) rounded to bf16; dW = dYq^T . FQ(X) in
+  fp32 from the bf16 operands; db = the column sums of the *unquantized*
+  dY in fp32.
+
+The contractions run on the fp16-MFMA quantized-linear kernels: the packing
+rounds bf16 inputs' FQ values to bf16, and a bf16 value times a power of two
+is exact in fp16, so the MFMAs see the reference's bf16 operands and
+accumulate in fp32 like its bf16 GEMM.
 """
 from __future__ import annotations
 
@@ -24,8 +34,11 @@ from axs.unified import hip_linear
 class _AXSLinearBF16Function(torch.autograd.Function):
     @staticmethod
     def forward(ctx, input, weight, bias, block_size, quantize_input, quantize_grad):  # type: ignore[override]
-        out, saved = hip_linear.forward_train(input.to(torch.bfloat16), weight.to(torch.bfloat16), bias,
+        # the reference adds the bias as bf16 (F.linear(input_q, weight_q, bias.to(bf16)))
+        b16 = bias.to(torch.bfloat16) if bias is not None else None
+        out, saved = hip_linear.forward_train(input.to(torch.bfloat16), weight.to(torch.bfloat16), b16,
                                               block_size, quantize_input)
+        saved.w_dtype = torch.float32     # dW stays fp32 for the fp32 master weight
         ctx.save_for_backward(*saved.tensors())
         ctx.meta = saved.meta()
         ctx.block_size = block_size
@@ -42,8 +55,6 @@ class _AXSLinearBF16Function(torch.autograd.Function):
         db = None
         if ctx.has_bias and ctx.needs_input_grad[2]:
             db = grad_output.float().sum(dim=tuple(range(grad_output.ndim - 1)))
-        if dw is not None:
-            dw = dw.float()
         return dx, dw, db, None, None, None
 
 

@@ -245,6 +245,22 @@ __device__ __forceinline__ void fq_vector(float (&f)[V], const FqScale& s, const
     }
 }
 
+// FQ values rounded to the element type's precision, as the reference's
+// fake-quantize returns them for a bf16 or f16 tensor (the output is cast back
+// to the input dtype, quantize_unified.py:201-204) before its F.linear or
+// matmul contracts them: bf16 to nearest even (NaN stays NaN), f16 through the
+// hardware conversion (values past 65504 become inf, as in torch); f32 as is.
+template <int DT, int V>
+__device__ __forceinline__ void round_to_elem(float (&f)[V]) {
+    if constexpr (DT == AXS6_BF16) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) f[e] = Elem<AXS6_BF16>::to_f(f32_to_bf16_rne(f[e]));
+    } else if constexpr (DT == AXS6_F16) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) f[e] = (float)(_Float16)f[e];
+    }
+}
+
 // Dither stream of the stochastic mode.  A call's 64-bit seed is turned into
 // a key once (the splitmix64 finaliser); the draw for element counter i is a
 // 32-bit multiply-xorshift hash (the "lowbias32" constants published by

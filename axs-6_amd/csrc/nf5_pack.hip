@@ -9,6 +9,11 @@
 // the GEMM within rel-L2 ~3e-4 of the fp32 product -- bf16 operands (8 bits)
 // land at ~2.5e-3.
 //
+// With bf16 or f16 inputs the FQ values are first rounded to that type, as
+// the reference's fake-quantize returns them before its 16-bit F.linear; a
+// bf16 or f16 value times a power of two is exact in fp16 (down to its
+// subnormal range), so the contraction then sees the reference's operands.
+//
 // Kernels:
 //   pack_rows_kernel    one workgroup per row, the row held in registers:
 //                       FQ + row scale in a single HBM pass (forward X, W;
@@ -190,6 +195,7 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
 #pragma unroll
                 for (int e = 0; e < V; ++e) d[e] = (MODE == kStochastic) ? dither_step(dv, e) : 0.0f;
                 fq_vector<V>(f[j], s, lut_s, MODE == kStochastic, d);
+                round_to_elem<DT>(f[j]);
             }
             const bool finite_block = !(s.nan_block || s.inf_scale || m == 0u);
             const int eb = (vi < nvec && finite_block) ? s.e1 : INT_MIN;
@@ -365,6 +371,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
                     for (int e = 0; e < V; ++e) d[e] = 0.0f;
                 }
                 fq_vector<V>(f, s, lut_s, MODE == kStochastic, d);
+                round_to_elem<DT>(f);
             }
             const bool live = FULL || (cin && r < k.rows);
             if (k.partial) {

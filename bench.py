@@ -441,66 +441,99 @@ def bench_pipeline(minigpt, x, y, steps: int = 100, warmup: int = 5):
     return res
 
 
-def cpu_baseline_fq(budget_s: float = 12.0):
+def cpu_threads():
+    """Host threads for the CPU baseline: every core this process may run on
+    (len(os.sched_getaffinity(0))), capped by OMP_NUM_THREADS when the
+    environment sets it (the GPU box sets it to its CPU share).  Sets torch's
+    intra-op pool to that count and returns the figures to report."""
+    import torch
+
+    torch_default = torch.get_num_threads()
+    affinity = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = affinity
+    if omp and omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))
+    torch.set_num_threads(threads)
+    return {"threads": torch.get_num_threads(), "affinity_cores": affinity, "omp_num_threads": omp,
+            "torch_default_threads": torch_default, "cpu_model": cpu_model()}
+
+
+def time_cpu(fn, warmup: int = 3, calls: int = 10, budget_s: float = 30.0):
+    """warmup untimed calls, then `calls` timed ones (fewer if budget_s runs
+    out first): (median, min, max, count) in seconds."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < calls and (not times or time.perf_counter() - t_start < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), min(times), max(times), len(times)
+
+
+def cpu_baseline_fq():
+    """The reference's CPU eager fused_fake_quantize (oracle/eager_torch.py,
+    restating quantize_unified.py:121-204) on the full 8192x4096 fp32 tensor:
+    3 warm-ups, median of 10 calls, on every host core and on one."""
     import torch
 
     from oracle import eager_torch
 
-    torch.set_num_threads(torch.get_num_threads())
-    threads = torch.get_num_threads()
+    info = cpu_threads()
     g = torch.Generator().manual_seed(3)
     x = torch.randn(*FQ_SHAPE, generator=g)
     m = torch.rand(*FQ_SHAPE, generator=g) < 0.01
     x[m] *= 100.0
-    eager_torch.fake_quantize(x, 32)  # warm-up
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 10 and (time.perf_counter() - t_start) < budget_s:
-        t0 = time.perf_counter()
-        eager_torch.fake_quantize(x, 32)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    nbytes = 8 * x.numel()
+    med, lo, hi, n = time_cpu(lambda: eager_torch.fake_quantize(x, 32))
+    torch.set_num_threads(1)
+    med1, _, _, n1 = time_cpu(lambda: eager_torch.fake_quantize(x, 32), warmup=1, calls=3, budget_s=10.0)
+    torch.set_num_threads(info["threads"])
     return {
-        "value": round(8 * x.numel() / med / 1e9, 3),
+        "value": round(nbytes / med / 1e9, 3),
         "unit": "GB/s",
-        "cores": threads,
+        "cores": info["threads"],
         "kind": "port",
+        "min_max_gbs": [round(nbytes / hi / 1e9, 3), round(nbytes / lo / 1e9, 3)],
+        "one_thread_gbs": round(nbytes / med1 / 1e9, 3),
+        "host": info,
         "sample": (f"torch-eager restatement of the reference's fused_fake_quantize "
-                   f"(oracle/eager_torch.py) on the full 8192x4096 fp32 tensor, median of "
-                   f"{len(times)} calls after 1 warm-up, {threads} threads, {cpu_model()}; "
-                   f"{med * 1e3:.1f} ms/call"),
+                   f"(oracle/eager_torch.py) on the full 8192x4096 fp32 tensor: 3 warm-ups, median of "
+                   f"{n} calls ({med * 1e3:.1f} ms/call, min {lo * 1e3:.1f}, max {hi * 1e3:.1f}) on "
+                   f"{info['threads']} threads ({info['affinity_cores']} cores in the affinity mask, "
+                   f"OMP_NUM_THREADS={info['omp_num_threads']}, torch default {info['torch_default_threads']}), "
+                   f"{info['cpu_model']}; one thread: median of {n1} calls, {med1 * 1e3:.1f} ms/call"),
     }
 
 
-def cpu_baseline_linear(budget_s: float = 15.0):
+def cpu_baseline_linear():
     """The reference's CPU eager linear forward at 4096^3 (FQ(W), FQ(X) with
     the eager fused_fake_quantize, fp32 F.linear -- oracle/eager_torch.py
-    restating functional_unified.py:116-123) on the host cores: median of up
-    to 5 calls after a warm-up, bounded by budget_s."""
+    restating functional_unified.py:116-123) on the host cores: 3 warm-ups,
+    median of 10 calls."""
     import torch
 
     from oracle import eager_torch
 
-    threads = torch.get_num_threads()
+    info = cpu_threads()
     g = torch.Generator().manual_seed(7)
     x = torch.randn(4096, 4096, generator=g)
     w = torch.randn(4096, 4096, generator=g) * 4096 ** -0.5
-    eager_torch.linear_fwd(x, w, None)  # warm-up
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
-        t0 = time.perf_counter()
-        eager_torch.linear_fwd(x, w, None)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    flops = 2 * 4096 ** 3
+    med, lo, hi, n = time_cpu(lambda: eager_torch.linear_fwd(x, w, None))
     return {
-        "value": round(2 * 4096 ** 3 / med / 1e12, 4),
+        "value": round(flops / med / 1e12, 4),
         "unit": "TFLOP/s",
-        "cores": threads,
+        "cores": info["threads"],
         "kind": "port",
+        "min_max_tflops": [round(flops / hi / 1e12, 4), round(flops / lo / 1e12, 4)],
+        "host": info,
         "sample": (f"torch-eager restatement of the reference's CPU linear forward (FQ(W), FQ(X), fp32 F.linear; "
-                   f"oracle/eager_torch.py) at 4096^3, median of {len(times)} calls after 1 warm-up, "
-                   f"{threads} threads, {cpu_model()}; {med * 1e3:.1f} ms/call"),
+                   f"oracle/eager_torch.py) at 4096^3: 3 warm-ups, median of {n} calls ({med * 1e3:.1f} ms/call, "
+                   f"min {lo * 1e3:.1f}, max {hi * 1e3:.1f}) on {info['threads']} threads "
+                   f"({info['affinity_cores']} cores in the affinity mask), {info['cpu_model']}"),
     }
 
 
@@ -640,6 +673,8 @@ def main() -> int:
             log(f"linear 4096^3 fwd: {lin['wall_ms']*1e3:.1f} us/step, {tflops:.0f} TFLOP/s")
             k = lin["kernels"]
             gemm_tf = lin["flops"] / (k["gemm_ms"] * 1e-3) / 1e12 if k.get("gemm_ms") else None
+            # the whole forward (packing of X and W + GEMM) on the device, per step
+            fwd_tf = lin["flops"] / (lin["gpu_ms"] * 1e-3) / 1e12
             out["linear"] = {
                 "metric": "AXS-6 linear forward TFLOP/s @4096^3",
                 "value": round(tflops, 1), "unit": "TFLOP/s",
@@ -648,11 +683,14 @@ def main() -> int:
                 "eager_ms_per_step": round(lin["eager_ms"], 5),
                 "dtype": k.get("compute_dtype"),
                 "kernels_ms": {kk: round(v, 5) for kk, v in k.items() if kk.endswith("_ms")},
-                "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1) if gemm_tf else None,
+                "roofline": {"bound": "mfma", "scope": "whole forward: FQ + packing of X and W, then the GEMM",
+                             "achieved": round(fwd_tf, 1),
                              "peak": BF16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
-                             "frac": round(gemm_tf / BF16_DENSE_PEAK_TFLOPS, 4) if gemm_tf else None,
-                             "end_to_end_frac": round(tflops / BF16_DENSE_PEAK_TFLOPS, 4),
-                             "traffic": load_traffic("linear_4096_traffic.json")},
+                             "frac": round(fwd_tf / BF16_DENSE_PEAK_TFLOPS, 4),
+                             "gemm_only": {"achieved": round(gemm_tf, 1) if gemm_tf else None,
+                                           "frac": round(gemm_tf / BF16_DENSE_PEAK_TFLOPS, 4) if gemm_tf else None,
+                                           "traffic": load_traffic("linear_4096_traffic.json")},
+                             "traffic": None},
             }
             lb = bench_linear(max(a.steps // 2, 10), max(a.warmup // 2, 3), dtype=torch.bfloat16)
             tb = lb["flops"] / (lb["wall_ms"] * 1e-3) / 1e12

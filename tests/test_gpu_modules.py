@@ -110,24 +110,6 @@ def test_attention_module_runs_and_backprops():
     assert torch.isfinite(x.grad).all() and mha.q_proj.weight.grad is not None
 
 
-def test_mixed_precision_linear():
-    import axs.unified as u
-
-    torch.manual_seed(4)
-    lin = u.AXSLinearMixedPrecision(128, 64, quantize_grad=False).to(DEV)
-    x = gauss((32, 128), 41).to(DEV).requires_grad_(True)
-    y = lin(x)
-    assert y.dtype == torch.bfloat16 and y.shape == (32, 64)
-    xb = x.detach().bfloat16().float().cpu().numpy()
-    wb = lin.weight.detach().bfloat16().float().cpu().numpy()
-    ref = oracle.linear_reference(oracle.fake_quantize(xb, 32), oracle.fake_quantize(wb, 32),
-                                  lin.bias.detach().cpu().numpy())
-    assert oracle.rel_l2(y.float().detach().cpu().numpy(), ref) < 5e-3
-    y.float().sum().backward()
-    assert lin.weight.grad.dtype == torch.float32 and x.grad is not None
-    assert torch.allclose(lin.bias.grad, torch.full_like(lin.bias.grad, 32.0))
-
-
 def test_convert_model_and_train_step():
     import axs.unified as u
 

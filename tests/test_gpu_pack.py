@@ -45,11 +45,15 @@ def _data(rows: int, cols: int, seed: int) -> np.ndarray:
 
 
 def _expected(x: np.ndarray, mode: int, cols_pad: int, colx: np.ndarray | None = None,
-              u: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray]:
+              u: np.ndarray | None = None, elem=None) -> tuple[np.ndarray, np.ndarray]:
     """Packed bits and row shifts; mode 1 FQ with nearest rounding, 2 with the
-    dither u, 0 raw; colx optional per-column exponents."""
+    dither u, 0 raw; colx optional per-column exponents.  `elem` (torch.bfloat16
+    or torch.float16) is the input's element type: the FQ values are rounded to
+    it first, as the reference's fake-quantize returns them for such a tensor."""
     rows, cols = x.shape
     v = oracle.fake_quantize(x, BS, u if mode == 2 else None) if mode else x.astype(np.float32)
+    if mode and elem is not None:
+        v = torch.from_numpy(v).to(elem).float().numpy()
     a = np.abs(x).reshape(rows, cols // BS, BS)
     with np.errstate(invalid="ignore"):
         amax = a.max(axis=2)                        # NaN where the block holds a NaN
@@ -114,9 +118,42 @@ def test_pack_rows_bf16_bitexact(cols):
     x = xb.float().numpy()
     cols_pad = (cols + 63) // 64 * 64
     got, shift = _pack(xb.to(DEV), 1, cols_pad)
-    want, wshift = _expected(x, 1, cols_pad)
+    want, wshift = _expected(x, 1, cols_pad, elem=torch.bfloat16)
     assert np.array_equal(shift, wshift)
     _assert_bits(got, want, f"bf16 37x{cols}")
+
+
+# f16 inputs: FQ values rounded to f16 first (past 65504 -> inf, as torch's
+# cast of the reference's fp32 FQ result), in registers and past them
+@pytest.mark.parametrize("cols", [256, 4096, 32800])
+def test_pack_rows_f16_bitexact(cols):
+    print(f"[pack_rows f16 37x{cols}]", flush=True)
+    x = _data(37, cols, 7 + cols)
+    x = np.clip(x, -6e4, 6e4)
+    x[8, :32] = 65000.0                         # FQ: lut[1014..] * 2^16 = 65536 -> inf in f16
+    x[9, :32] = np.float32(3e-5)                # FQ values in the f16 subnormal range
+    xh = torch.from_numpy(x).to(torch.float16)
+    cols_pad = (cols + 63) // 64 * 64
+    got, shift = _pack(xh.to(DEV), 1, cols_pad)
+    want, wshift = _expected(xh.float().numpy(), 1, cols_pad, elem=torch.float16)
+    assert np.array_equal(shift, wshift)
+    assert np.isinf(want[8, :32].astype(np.float32)).any()
+    _assert_bits(got, want, f"f16 37x{cols}")
+
+
+def test_pack_rows_bf16_stochastic_bitexact():
+    """Stochastic FQ of bf16 rows (the backward's dY in bf16): dither, then
+    the bf16 rounding of the FQ value, then the fp16 packing."""
+    cols = 4096
+    xb = torch.from_numpy(_data(37, cols, 77)).to(torch.bfloat16)
+    seed, offset = 0xABCDEF, 99
+    cols_pad = cols
+    got, shift = _pack(xb.to(DEV), 2, cols_pad, None, seed, offset)
+    x = xb.float().numpy()
+    want, wshift = _expected(x, 2, cols_pad, None, oracle.uniform(seed, offset, x.size).reshape(x.shape),
+                             elem=torch.bfloat16)
+    assert np.array_equal(shift, wshift)
+    _assert_bits(got, want, "bf16 stochastic")
 
 
 @pytest.mark.parametrize("cols", [256, 11008])
