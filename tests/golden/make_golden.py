@@ -16,6 +16,13 @@ Outputs (data only: inputs and expected outputs) go next to this script:
   edge_cases.npz  -- hand-built edge blocks, nearest rounding, bs 8/16/32
   ragged.npz      -- odd shapes needing padding, fp32 / bf16 / fp16 inputs
   config1.npz     -- BASELINE config 1: randn(1024,1024, seed 0) * 0.02
+  stochastic.npz  -- rounding="stochastic" of fused_fake_quantize and
+                     quantize_unified with torch.rand_like replaced by a saved
+                     array U (the draws, in the reference's padded
+                     (rows, blocks, block) layout, are part of the fixture):
+                     the edge suite, ragged rows, bf16 input
+
+    python tests/golden/make_golden.py /root/reference [--only stochastic]
 """
 from __future__ import annotations
 
@@ -110,6 +117,120 @@ def ragged_inputs():
     return out
 
 
+def draws(rng, shape) -> np.ndarray:
+    """U[0,1) with torch.rand's 24-bit resolution, with the extreme and
+    midpoint draws (0, 2^-24, 0.5 - 2^-24, 0.5, 0.5 + 2^-24, 1 - 2^-24)
+    planted at every 7th position."""
+    k = rng.integers(0, 1 << 24, size=shape, dtype=np.int64)
+    special = np.array([0, 1, (1 << 23) - 1, 1 << 23, (1 << 23) + 1, (1 << 24) - 1], np.int64)
+    flat = k.reshape(-1)
+    flat[::7] = special[np.arange(flat[::7].size) % special.size]
+    return (flat.reshape(shape).astype(np.float64) * 2.0 ** -24).astype(np.float32)
+
+
+def dither_boundary_inputs(rng) -> tuple[np.ndarray, np.ndarray]:
+    """Blocks whose dithered index (n + (U - 0.5)/1023) * 1023 lands within a
+    few float32 ulps of an integer, for draws U picked so that float32
+    restatements equal to it in exact arithmetic (n*1023 + (U - 0.5), ...)
+    truncate to a different index: these pin the reference's order of
+    operations.  Each row is one 32-block whose element 0 is 0.99999994
+    (scale 1, so n = |x|); the rest are signed candidates n with their U.
+    Returns x (rows, 32) and U (rows, 1, 32)."""
+    f32 = np.float32
+    n = (rng.random(40000) * 0.999).astype(f32)
+    j = np.round(n.astype(np.float64) * 1023)
+    k0 = np.round((0.5 + j - n.astype(np.float64) * 1023) * 2 ** 24).astype(np.int64)
+    ks = np.clip(k0[:, None] + np.arange(-64, 65)[None, :], 0, (1 << 24) - 1)
+    U = (ks.astype(np.float64) * 2.0 ** -24).astype(f32)
+    nn = np.broadcast_to(n[:, None], U.shape)
+    t_ref = (nn + (U - f32(0.5)) / f32(1023)) * f32(1023)
+    t_alt = nn * f32(1023) + (U - f32(0.5))
+    hit = np.argwhere(np.trunc(t_ref) != np.trunc(t_alt))
+    rows = 64
+    pick = hit[rng.choice(hit.shape[0], rows * 31, replace=False)]
+    x = np.zeros((rows, 32), f32)
+    u = draws(rng, (rows, 1, 32))
+    x[:, 0] = f32(0.99999994)
+    sign = np.where(rng.random(rows * 31) < 0.5, f32(-1), f32(1))
+    x[:, 1:] = (n[pick[:, 0]] * sign).reshape(rows, 31)
+    u[:, 0, 1:] = U[pick[:, 0], pick[:, 1]].reshape(rows, 31)
+    return x, u
+
+
+class fixed_rand:
+    """Replaces torch.rand_like for one call with a saved array of the same shape."""
+
+    def __init__(self, u: np.ndarray):
+        self.u = torch.from_numpy(u)
+        self.calls = 0
+
+    def __enter__(self):
+        self.orig = torch.rand_like
+
+        def fake(t, *a, **k):
+            assert tuple(t.shape) == tuple(self.u.shape), (tuple(t.shape), tuple(self.u.shape))
+            self.calls += 1
+            return self.u.clone().to(t.dtype)
+
+        torch.rand_like = fake
+        return self
+
+    def __exit__(self, *exc):
+        torch.rand_like = self.orig
+        assert self.calls == 1, "the reference drew rand_like a different number of times"
+
+
+def stochastic(ref_root: str) -> None:
+    sys.path.insert(0, ref_root)
+    from axs.unified.quantize_unified import (  # noqa: E402  (reference)
+        dequantize_unified,
+        fused_fake_quantize,
+        quantize_unified,
+    )
+
+    rng = np.random.default_rng(4321)
+    res = {}
+    g = np.random.default_rng(77)
+    xr = (g.standard_normal((32, 1000)) * 10.0 ** g.uniform(-3, 3, (32, 1))).astype(np.float32)
+    xr[g.random(xr.shape) < 0.01] *= 100.0
+    cases = {"edge": (edge_inputs(), (8, 16, 32)), "ragged": (xr, (8, 32))}
+    for name, (x, sizes) in cases.items():
+        res[f"x_{name}"] = x
+        R, C = x.shape
+        for bs in sizes:
+            nblk = (C + bs - 1) // bs
+            u = draws(rng, (R, nblk, bs))      # the same draws for both functions
+            res[f"u_{name}_bs{bs}"] = u
+            with fixed_rand(u):
+                res[f"fq_{name}_bs{bs}"] = fused_fake_quantize(torch.from_numpy(x), bs, "stochastic").numpy()
+            with fixed_rand(u):
+                q = quantize_unified(torch.from_numpy(x), bs, "stochastic")
+            res[f"exp_{name}_bs{bs}"] = q.shared_exponents.numpy()
+            res[f"code_{name}_bs{bs}"] = q.magnitudes.numpy()
+            res[f"sign_{name}_bs{bs}"] = q.signs.numpy()
+            res[f"deq_{name}_bs{bs}"] = dequantize_unified(q).numpy()
+    # draws at the index boundaries (block 32)
+    xd, ud = dither_boundary_inputs(rng)
+    res["x_dither"], res["u_dither"] = xd, ud
+    with fixed_rand(ud):
+        res["fq_dither"] = fused_fake_quantize(torch.from_numpy(xd), 32, "stochastic").numpy()
+    with fixed_rand(ud):
+        q = quantize_unified(torch.from_numpy(xd), 32, "stochastic")
+    res["exp_dither"] = q.shared_exponents.numpy()
+    res["code_dither"] = q.magnitudes.numpy()
+    # bf16 input: FQ in float32 of the bf16 values, result cast back to bf16
+    xb = torch.from_numpy(xr).to(torch.bfloat16)
+    u = draws(rng, (32, 32, 32))
+    res["x_bf16"] = xb.view(torch.int16).numpy()
+    res["u_bf16"] = u
+    with fixed_rand(u):
+        yb = fused_fake_quantize(xb, 32, "stochastic")
+    assert yb.dtype == torch.bfloat16
+    res["fq_bf16"] = yb.view(torch.int16).numpy()
+    np.savez_compressed(os.path.join(HERE, "stochastic.npz"), **res)
+    print("wrote stochastic.npz")
+
+
 def main(ref_root: str) -> None:
     sys.path.insert(0, ref_root)
     from axs.unified.quantize_unified import (  # noqa: E402  (reference)
@@ -168,4 +289,12 @@ def main(ref_root: str) -> None:
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    root = args[0] if args else "/root/reference"
+    if "--only" in sys.argv:
+        what = sys.argv[sys.argv.index("--only") + 1]
+        assert what == "stochastic", what
+        stochastic(root)
+    else:
+        main(root)
+        stochastic(root)

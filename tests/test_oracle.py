@@ -237,3 +237,80 @@ def test_stochastic_dither_is_unbiased():
         y = oracle.fake_quantize(x, 32, oracle.uniform(1000 + s, 0, x.size))
         errs.append(float((x - y).mean()))
     assert abs(np.mean(errs)) < 0.01
+
+
+def _unpad(u: np.ndarray, cols: int) -> np.ndarray:
+    """The reference's draws in its padded (rows, blocks, block) layout ->
+    the oracle's one draw per (row, col) element."""
+    return np.ascontiguousarray(u.reshape(u.shape[0], -1)[:, :cols])
+
+
+def test_stochastic_matches_reference_fixture():
+    """rounding="stochastic" of the reference's fused_fake_quantize and
+    quantize_unified with torch.rand_like replaced by saved draws
+    (tests/golden/stochastic.npz): the oracle, given the same draws, gives
+    the same bits, codes, exponents and signs."""
+    g = load_golden("stochastic.npz")
+    for name, sizes in (("edge", (8, 16, 32)), ("ragged", (8, 32))):
+        x = g[f"x_{name}"]
+        for bs in sizes:
+            u = _unpad(g[f"u_{name}_bs{bs}"], x.shape[1])
+            fq = oracle.fake_quantize(x, bs, u)
+            want = g[f"fq_{name}_bs{bs}"]
+            assert bits_equal(fq, want), f"{name} bs{bs}: {first_mismatch(fq, want)}"
+            e, c, s = oracle.quantize(x, bs, u)
+            assert np.array_equal(e, g[f"exp_{name}_bs{bs}"]), f"{name} bs{bs} exponents"
+            assert np.array_equal(c.reshape(-1), g[f"code_{name}_bs{bs}"].reshape(-1)), f"{name} bs{bs} codes"
+            assert np.array_equal(s.reshape(-1), g[f"sign_{name}_bs{bs}"].reshape(-1)), f"{name} bs{bs} signs"
+            deq = oracle.dequantize(e, c, s, x.shape[1], bs)
+            assert bits_equal(deq, g[f"deq_{name}_bs{bs}"]), f"{name} bs{bs} dequantize"
+    # draws planted at the index boundaries
+    x = g["x_dither"]
+    u = _unpad(g["u_dither"], 32)
+    fq = oracle.fake_quantize(x, 32, u)
+    assert bits_equal(fq, g["fq_dither"]), first_mismatch(fq, g["fq_dither"])
+    e, c, _ = oracle.quantize(x, 32, u)
+    assert np.array_equal(e, g["exp_dither"]) and np.array_equal(c.reshape(-1), g["code_dither"].reshape(-1))
+    # bf16 input: FQ of the bf16 values in float32, cast back to bf16
+    xb = torch.from_numpy(g["x_bf16"]).view(torch.bfloat16)
+    u = _unpad(g["u_bf16"], xb.shape[1])
+    fq = torch.from_numpy(oracle.fake_quantize(xb.float().numpy(), 32, u)).to(torch.bfloat16)
+    assert np.array_equal(fq.view(torch.int16).numpy(), g["fq_bf16"])
+
+
+def _fq_stochastic_numpy(x: np.ndarray, u: np.ndarray, variant: str) -> np.ndarray:
+    """fused_fake_quantize (block 32, rows of whole blocks, finite data) with
+    the dither index computed in float32 numpy, per `variant`: "reference"
+    the reference's order of operations (quantize_unified.py:186-189), the
+    others plausible restatements that are equal in exact arithmetic."""
+    f32 = np.float32
+    _, lut, _ = oracle.tables()
+    R, C = x.shape
+    b = x.reshape(R, C // 32, 32)
+    amax = np.abs(b).max(axis=2, keepdims=True)
+    scale = np.ldexp(f32(1), (oracle.floor_log2(np.maximum(amax, f32(1e-45))) + 1).astype(np.int32)).astype(f32)
+    scale = np.where(amax == 0, f32(1), scale)
+    n = np.clip(np.abs(b) / scale, f32(0), f32(1)).astype(f32)
+    uu = u.reshape(n.shape).astype(f32)
+    if variant == "reference":
+        t = (n + (uu - f32(0.5)) / f32(1023)) * f32(1023)
+    elif variant == "expanded":          # n*1023 + (u - 0.5)
+        t = n * f32(1023) + (uu - f32(0.5))
+    elif variant == "no_centering":      # the dither drawn in [0, 1) steps
+        t = (n + uu / f32(1023)) * f32(1023)
+    else:                                # the dither added after the scaling to 1023
+        t = (n * f32(1023) + uu) - f32(0.5)
+    idx = np.clip(np.trunc(t).astype(np.int64), 0, 1023)
+    return ((np.sign(b) * lut[idx]) * scale).astype(f32).reshape(R, C)
+
+
+def test_stochastic_fixture_rejects_reordered_dither():
+    """The fixture pins the operation order: the reference's order reproduces
+    it, and each algebraically equal reordering of the dither fails it."""
+    g = load_golden("stochastic.npz")
+    x = g["x_dither"]
+    u = _unpad(g["u_dither"], 32)
+    want = g["fq_dither"]
+    assert bits_equal(_fq_stochastic_numpy(x, u, "reference"), want)
+    for variant in ("expanded", "no_centering", "after_scaling"):
+        assert not bits_equal(_fq_stochastic_numpy(x, u, variant), want), variant
