@@ -88,24 +88,19 @@ def time_steps(step, launches, steps: int, warmup: int):
 
     `step` is the full step through the public API (autograd included);
     `launches` issues exactly the kernels of one step (the STE backward of
-    the fake-quantize launches none).  After `warmup` eager steps, `steps`
-    eager steps are timed for reference; then GRAPH_STEPS steps' launches
-    are captured into one HIP graph on a side stream and the graph is
-    replayed until `steps` steps have run, between device synchronisations
-    (wall clock) and HIP events on the launch stream (device time).  Every
-    kernel runs every step; the graph only takes the per-launch host cost
-    out of the loop, which otherwise exceeds the 40 us kernel.
+    the fake-quantize launches none).  After `warmup` eager steps,
+    GRAPH_STEPS steps' launches are captured into one HIP graph on a side
+    stream and the graph is replayed until `steps` steps have run, between
+    device synchronisations (wall clock) and HIP events on the launch stream
+    (device time).  Every kernel runs every step; the graph only takes the
+    per-launch host cost out of the loop.  Then `steps` eager steps are
+    timed for reference.
     Returns (wall ms/step, device ms/step, eager wall ms/step)."""
     import torch
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / steps
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -131,6 +126,17 @@ def time_steps(step, launches, steps: int, warmup: int):
     ev1.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / (replays * GRAPH_STEPS)
+    # the eager steps are timed last, with the GPU's clocks already settled by
+    # the replays (timed first, right after the data was made, they read up
+    # to 25% slower than the same steps a moment later)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / steps
     return wall_ms, ev0.elapsed_time(ev1) / (replays * GRAPH_STEPS), eager_ms
 
 
@@ -372,6 +378,11 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
     import minigpt
 
     x, y = minigpt.batch(1)
+    # settle the GPU and host clocks on both models before anything is timed
+    # (the first timed loop otherwise reads 10-20% slow, whichever model it is)
+    for build in (lambda: minigpt.build_axs(0, "cuda"), lambda: minigpt.base_model(0).cuda()):
+        minigpt.train(build(), x.cuda(), y.cuda(), 30)
+    torch.cuda.synchronize()
     torch.manual_seed(5)
     model = minigpt.build_axs(0, "cuda")
     losses, ms = minigpt.train(model, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize)

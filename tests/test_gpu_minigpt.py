@@ -2,19 +2,23 @@
 context 128, batch 64) trained with AdamW (lr 3e-4, fp32 master weights), every
 nn.Linear replaced by the AXS-6 linear through convert_to_axs_unified.
 
-The loss curve of the product path on the GPU is compared with
+The 200-step loss curve of the product path on the GPU is compared with
   * the same model, initial weights and batch trained on the CPU through the
     reference's eager NF5 operations (tests/minigpt.py ``build_reference``),
-    step by step over the first REF_STEPS steps;
+    whose 200-step curves tests/golden/make_minigpt_curve.py wrote to
+    tests/golden/minigpt_curve.npz: with dY taken as given (nearest) step by
+    step, and with stochastically rounded dY within an envelope (the two
+    sides draw different dither streams);
+  * a live CPU run of the restatement over the first REF_STEPS steps (the
+    fixture's path on this host);
   * the unquantized fp32 model on the GPU over the full 200 steps (the
     reference's claim: AXS-6 training tracks fp32, README.md:238-243).
-Over the first steps the gradient dither (stochastic FQ of dY) moves a loss
-by < 1e-4 between dither streams, so the step-by-step bound there is mostly
-the fp16-MFMA product's rounding (rel-L2 ~3e-4 per linear output); over tens
-of steps two dither streams drift apart by up to ~1% of the loss.
 """
 from __future__ import annotations
 
+import os
+
+import numpy as np
 import pytest
 import torch
 
@@ -24,20 +28,62 @@ pytestmark = pytest.mark.gpu
 
 STEPS = 200
 REF_STEPS = 8
-STEP_TOL = 2e-3        # relative, per step, GPU product path vs CPU reference
-CURVE_TOL = 0.03       # x initial loss, |AXS - fp32| at every step of the 200-step
-                       # curve (measured max 0.079 nats = 0.014 x 5.6, mid-descent)
-FINAL_TOL = 0.005      # nats, final loss vs the fp32 model (both near 0.02: the
-                       # batch is memorised, so a relative bound would be ill-posed)
+STEP_TOL = 2e-3        # relative, per step, GPU product path vs CPU reference (first REF_STEPS)
+NEAR_STEPS = 10        # nearest dY: steps compared step by step at STEP_TOL (the
+                       # runs then drift: 2.4e-3 relative at step 19, max 0.062 nats at
+                       # step ~50, back to 1e-4 once the batch is memorised)
+CURVE_TOL = 0.03       # x initial loss, |a - b| at every step of two curves with different
+                       # dither streams (GPU vs CPU reference; AXS vs fp32)
+FINAL_TOL = 0.005      # nats, final loss (both near 0.02: the batch is memorised, so a
+                       # relative bound would be ill-posed)
+
+FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "minigpt_curve.npz")
+
+
+def _nearest_dy(model):
+    from axs.unified import AXSLinearUnified
+
+    for m in model.modules():
+        if isinstance(m, AXSLinearUnified):
+            m.quantize_grad = False
+    return model
+
+
+def _max_gap(a, b):
+    return max(abs(u - v) for u, v in zip(a, b))
 
 
 def test_minigpt_loss_curve_matches_reference_and_fp32():
+    ref_curves = np.load(FIXTURE, allow_pickle=False)
+    assert int(ref_curves["steps"]) == STEPS
     x, y = minigpt.batch(1)
-    print("[minigpt: GPU product path, 200 steps]", flush=True)
+
+    print("[minigpt: GPU product path, nearest dY, 200 steps]", flush=True)
+    near, _ = minigpt.train(_nearest_dy(minigpt.build_axs(0, "cuda")), x.cuda(), y.cuda(), STEPS)
+    ref_near = ref_curves["nearest"].tolist()
+    gap = _max_gap(near, ref_near)
+    windows = [round(_max_gap(near[i:i + 20], ref_near[i:i + 20]), 4) for i in range(0, STEPS, 20)]
+    print(f"  loss {near[0]:.4f} -> {near[-1]:.4f}; CPU reference {ref_near[0]:.4f} -> {ref_near[-1]:.4f}; "
+          f"max gap {gap:.4f}; per 20 steps {windows}", flush=True)
+    # step by step while the two runs have not yet diverged (fp16 rounding of
+    # the products vs fp32, amplified by NF5's quantization steps and the
+    # training dynamics), then within the envelope of two dither streams
+    rel = [abs(near[i] - ref_near[i]) / ref_near[i] for i in range(NEAR_STEPS)]
+    print(f"  first {NEAR_STEPS} steps: max relative gap {max(rel):.2e}", flush=True)
+    assert max(rel) < STEP_TOL
+    assert gap < CURVE_TOL * ref_near[0]
+    assert abs(near[-1] - ref_near[-1]) < FINAL_TOL
+
+    print("[minigpt: GPU product path, stochastic dY, 200 steps]", flush=True)
     torch.manual_seed(5)
     model = minigpt.build_axs(0, "cuda")
     gpu_losses, ms = minigpt.train(model, x.cuda(), y.cuda(), STEPS, warmup=5, sync=torch.cuda.synchronize)
-    print(f"  {ms:.2f} ms/step, loss {gpu_losses[0]:.4f} -> {gpu_losses[-1]:.4f}", flush=True)
+    ref_st = ref_curves["stochastic"].tolist()
+    gap = _max_gap(gpu_losses, ref_st)
+    print(f"  {ms:.2f} ms/step, loss {gpu_losses[0]:.4f} -> {gpu_losses[-1]:.4f}; CPU reference "
+          f"{ref_st[0]:.4f} -> {ref_st[-1]:.4f}; max gap {gap:.4f}", flush=True)
+    assert gap < CURVE_TOL * ref_st[0]
+    assert abs(gpu_losses[-1] - ref_st[-1]) < FINAL_TOL
 
     print("[minigpt: fp32 GPU model, 200 steps]", flush=True)
     fp32 = minigpt.base_model(0).cuda()
@@ -50,12 +96,16 @@ def test_minigpt_loss_curve_matches_reference_and_fp32():
     ref_losses, ref_ms = minigpt.train(ref, x, y, REF_STEPS, warmup=1)
     print(f"  {ref_ms:.0f} ms/step, losses {[round(v, 4) for v in ref_losses]}", flush=True)
     print(f"  gpu losses {[round(v, 4) for v in gpu_losses[:REF_STEPS]]}", flush=True)
+    # the fixture was written by the same restatement (same seeds and draws) on
+    # another host, whose thread count orders the fp32 reductions differently:
+    # measured 1.6e-4 relative by step 3
+    assert np.allclose(ref_losses, ref_st[:REF_STEPS], rtol=1e-3, atol=0)
 
     for i in range(REF_STEPS):
         rel = abs(gpu_losses[i] - ref_losses[i]) / ref_losses[i]
         assert rel < STEP_TOL, (i, gpu_losses[i], ref_losses[i])
     assert gpu_losses[-1] < gpu_losses[0] - 1.0, "training did not make progress"
-    gap = max(abs(a - b) for a, b in zip(gpu_losses, fp32_losses))
+    gap = _max_gap(gpu_losses, fp32_losses)
     print(f"  final loss axs {gpu_losses[-1]:.4f} fp32 {fp32_losses[-1]:.4f}; max curve gap {gap:.4f}", flush=True)
     assert gap < CURVE_TOL * fp32_losses[0]
     assert abs(gpu_losses[-1] - fp32_losses[-1]) < FINAL_TOL
@@ -71,15 +121,6 @@ def test_minigpt_every_linear_converted():
     assert isinstance(model.token_embed, AXSEmbeddingUnified)
 
 
-def _no_grad_quant(model):
-    from axs.unified import AXSLinearUnified
-
-    for m in model.modules():
-        if isinstance(m, AXSLinearUnified):
-            m.quantize_grad = False
-    return model
-
-
 def test_minigpt_graph_replay_matches_eager_training():
     """The whole training step (forward, loss, backward, AdamW) recorded in one
     HIP graph and replayed trains like the eager loop.  With nearest-rounded
@@ -93,8 +134,8 @@ def test_minigpt_graph_replay_matches_eager_training():
     x, y = minigpt.batch(1)
     xd, yd = x.cuda(), y.cuda()
     print("[minigpt: eager vs graph-replayed, nearest dY, 30 steps]", flush=True)
-    eager, _ = minigpt.train(_no_grad_quant(minigpt.build_axs(0, "cuda")), xd, yd, 30, capturable=True)
-    graphed, _ = minigpt.train_graphed(_no_grad_quant(minigpt.build_axs(0, "cuda")), xd, yd, 30, warmup=3)
+    eager, _ = minigpt.train(_nearest_dy(minigpt.build_axs(0, "cuda")), xd, yd, 30, capturable=True)
+    graphed, _ = minigpt.train_graphed(_nearest_dy(minigpt.build_axs(0, "cuda")), xd, yd, 30, warmup=3)
     print(f"  losses {eager[0]:.5f} -> {eager[-1]:.5f}", flush=True)
     assert graphed == eager
 
