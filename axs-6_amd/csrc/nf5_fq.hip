@@ -224,17 +224,18 @@ __global__ __launch_bounds__(kThreads) void quantize_vec_kernel(
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
     __shared__ uint8_t rev_s[kLutSize];
-    reinterpret_cast<uint32_t*>(rev_s)[threadIdx.x] = reinterpret_cast<const uint32_t*>(rev_g)[threadIdx.x];
-    stage_tables(lut_s, band_w, lut_g, band_g);
-    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
     const int64_t step = (int64_t)gridDim.x * kThreads;
     // the bound is rounded up to whole waves so every lane of a block's DPP
     // group runs every iteration
     const int64_t span = (n_vec + 63) / 64 * 64;
     int64_t vi = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    // the next iteration's vector is loaded before this one is processed
+    // the first vector's HBM load goes out before the tables are staged (the
+    // two latencies overlap); later ones one iteration ahead
     u32x4 cur = vi < n_vec ? xv[vi] : u32x4{0u, 0u, 0u, 0u};
+    reinterpret_cast<uint32_t*>(rev_s)[threadIdx.x] = reinterpret_cast<const uint32_t*>(rev_g)[threadIdx.x];
+    stage_tables(lut_s, band_w, lut_g, band_g);
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
     for (; vi < span; vi += step) {
         const bool live = vi < n_vec;
         const u32x4 nxt = vi + step < n_vec ? xv[vi + step] : u32x4{0u, 0u, 0u, 0u};
