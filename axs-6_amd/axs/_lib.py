@@ -46,6 +46,7 @@ _SIGNATURES: dict[str, list] = {
     "axs6_nf5_linear_forward": [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp,
                                 _vp, _vp],
     "axs6_nf5_linear_backward_workspace": [_i64, _i64, _i64, _i32, _i32, _i32],
+    "axs6_nf5_fused_linear": [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp],
     "axs6_nf5_wire_bytes": [_i64, _i64, _i32],
     "axs6_nf5_pack_wire": [_vp, _i32, _i64, _i64, _i32, _vp, _vp],
     "axs6_nf5_unpack_wire": [_vp, _i64, _i64, _i32, _vp, _vp],

@@ -118,8 +118,49 @@ def forward_train(input, weight, bias, block_size=32, quantize_input=True):
     return _forward(input, weight, bias, block_size, quantize_input)
 
 
+# Outputs up to this many elements take the single-launch fused kernel (the
+# reference's _FUSED_SIZE_THRESHOLD, triton_kernels.py:382, applied the same
+# way by its accelerated_linear, backend.py:577-590).
+FUSED_SIZE_THRESHOLD = 128 * 1024
+
+
+def fused_forward(input, weight, bias=None, quantize_input=True):
+    """``FQ(input) FQ(weight)^T + bias`` with block size 32 in one launch of
+    the fused kernel (FQ in the tile loads, fp32 contraction): the
+    reference's ``triton_fused_linear`` (``triton_kernels.py:385-482``).
+    Returns the input's dtype (float32 for other dtypes)."""
+    fn = "axs_fused_linear"
+    _require_device(input, fn)
+    _require_device(weight, fn)
+    K = input.shape[-1]
+    N, Kw = weight.shape
+    if Kw != K:
+        raise RuntimeError(f"{fn}: input has {K} features but weight expects {Kw}")
+    dtype = input.dtype if input.dtype in _SUPPORTED else torch.float32
+    x2 = _dense(_pad_last(input.reshape(-1, K).to(dtype), 32))
+    w2 = _dense(_pad_last(weight.to(dtype), 32))
+    M, Kb = x2.shape
+    dev = x2.device
+    y = torch.empty((M, N), dtype=dtype, device=dev)
+    b = None if bias is None else bias.to(torch.float32).contiguous()
+    if M and N and not Kb:
+        y.copy_(b.to(dtype).expand(M, N) if b is not None else torch.zeros((), dtype=dtype, device=dev).expand(M, N))
+    elif M and N:
+        with _on_device(x2):
+            _lib.call("axs6_nf5_fused_linear", x2.data_ptr(), w2.data_ptr(), _lib.ptr(b), y.data_ptr(),
+                      _lib.DTYPE_CODE[dtype], M, N, Kb, 32, int(bool(quantize_input)), _lib.stream_of(x2))
+    return y.reshape(*input.shape[:-1], N)
+
+
 def linear_forward(input, weight, bias=None, block_size=32, quantize_input=True):
-    """Y = FQ(input) FQ(weight)^T + bias (no autograd bookkeeping)."""
+    """Y = FQ(input) FQ(weight)^T + bias (no autograd bookkeeping): the fused
+    single-launch kernel for block size 32 and at most FUSED_SIZE_THRESHOLD
+    outputs, else the packing kernels and the fp16-MFMA GEMM."""
+    if block_size == 32 and input.shape[-1] == weight.shape[-1]:
+        rows = input.numel() // input.shape[-1] if input.shape[-1] else 0
+        if rows * weight.shape[0] <= FUSED_SIZE_THRESHOLD:
+            out = fused_forward(input, weight, bias, quantize_input)
+            return out if input.dtype == out.dtype or input.dtype not in _SUPPORTED else out.to(input.dtype)
     out, _ = _forward(input, weight, bias, block_size, quantize_input)
     return out if input.dtype == out.dtype or input.dtype not in _SUPPORTED else out.to(input.dtype)
 

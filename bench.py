@@ -20,6 +20,8 @@ linear TFLOP/s @4096^3 bf16"):
     dequantize at 8192x4096, GB/s.
   * "configs": the smaller config-1/2 shapes (FQ at 256^2 and 4096^2,
     quantize/dequantize at 1024^2), device time per launch.
+  * "fused": the single-launch fused linear at small outputs (decode-like
+    shapes), beside the packing + GEMM path.
   * "minigpt": config 5, the MiniGPT training step with every nn.Linear
     converted (ms/step and the loss curve, beside the fp32 model).
 Inputs are synthetic, resident in HBM before the timed region.  K steps are
@@ -312,6 +314,55 @@ def bench_configs(steps: int = 200, warmup: int = 20):
 
 
 LIN_TRAIN_SHAPES = [(8192, 4096, 11008), (8192, 11008, 4096), (2048, 768, 3072), (2048, 3072, 768)]
+
+
+def bench_fused(reps: int = 100, warmup: int = 10):
+    """The single-launch fused linear (FQ in the tile loads, fp32 MFMA) at
+    outputs <= 128K elements, where accelerated_linear / triton_fused_linear
+    dispatch to it: decode-like M against a 4096 x 4096 weight and a small
+    square layer, device time per call (HIP events), beside the packing +
+    fp16-GEMM path on the same inputs."""
+    import torch
+
+    from axs import _lib
+    from axs.unified import hip_linear
+
+    def ev(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    g = torch.Generator(device="cuda").manual_seed(9)
+    out = {"metric": "fused FQ + linear (M*N <= 128K outputs), device us per call",
+           "note": "fused: one launch, FQ of each 32-wide K tile as it is loaded, fp32 MFMA; "
+                   "packed: FQ + fp16 packing of X and W, then the fp16-MFMA GEMM"}
+    for M, K, N in ((1, 4096, 4096), (32, 4096, 4096), (128, 1024, 1024), (256, 512, 512)):
+        X = torch.randn(M, K, device="cuda", generator=g)
+        W = torch.randn(N, K, device="cuda", generator=g) * K ** -0.5
+        b = torch.zeros(N, device="cuda")
+        y = torch.empty(M, N, device="cuda")
+        st = _lib.stream_of(X)
+        fused = ev(lambda: _lib.call("axs6_nf5_fused_linear", X.data_ptr(), W.data_ptr(), b.data_ptr(), y.data_ptr(),
+                                     _lib.F32, M, N, K, 32, 1, st))
+        Kp = hip_linear.padded_k(K)
+        xq = torch.empty(M, Kp, dtype=torch.float16, device="cuda")
+        wq = torch.empty(N, Kp, dtype=torch.float16, device="cuda")
+        sx = torch.empty(M, dtype=torch.int32, device="cuda")
+        sw = torch.empty(N, dtype=torch.int32, device="cuda")
+        packed = ev(lambda: _lib.call("axs6_nf5_linear_forward", X.data_ptr(), W.data_ptr(), b.data_ptr(),
+                                      y.data_ptr(), _lib.F32, M, N, K, 32, 1, xq.data_ptr(), sx.data_ptr(),
+                                      wq.data_ptr(), sw.data_ptr(), st))
+        out[f"{M}x{K}x{N}"] = {"fused_us": round(fused * 1e3, 1), "packed_us": round(packed * 1e3, 1),
+                               "weight_gbs": round(N * K * 4 / (fused * 1e-3) / 1e9, 1)}
+    return out
 
 
 def bench_linear_train(reps: int = 5, warmup: int = 2):
@@ -739,6 +790,8 @@ def main() -> int:
             f"dequantize {out['codec']['dequantize_gbs']} GB/s")
 
     if not a.no_linear:
+        if leg(out, "fused", bench_fused):
+            log(f"fused small-output linear: {out['fused']}")
         log("linear fwd+bwd (config 4) ...")
         leg(out, "linear_train", bench_linear_train)
 

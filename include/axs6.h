@@ -185,6 +185,26 @@ int axs6_nf5_linear_forward(const void* x, const void* w, const float* bias, voi
                             int64_t M, int64_t N, int64_t K, int32_t block_size, int32_t quantize_input,
                             void* xq_f16, int32_t* x_shift, void* wq_f16, int32_t* w_shift, void* stream);
 
+/* Y[M, N] = FQ(X)[M, K] . FQ(W)[N, K]^T + bias in one launch, for small
+ * outputs: each 32-wide K tile of X and W is NF5 fake-quantized as it is
+ * loaded (the block scale and LUT step of axs6_nf5_fake_quantize, nearest
+ * rounding) and contracted in fp32 (fp32 MFMA: the products of the fp32 FQ
+ * values, no fp16 packing), so no quantized operand is written to memory.
+ * block_size must be 32, K a multiple of 32 (zero-pad a ragged K first), x
+ * and w 16-byte aligned and row-major; bias f32 (may be NULL); Y in `dtype`.
+ * With quantize_input = 0, X enters the contraction as given.  For 16-bit
+ * inputs the FQ values stay fp32 and only Y is rounded to `dtype`.  Meant for
+ * M * N <= 131072 outputs (the Python layer dispatches there); larger
+ * problems run correctly but repeat the FQ of each operand tile for every
+ * output tile that reads it.
+ * Replaces: triton_fused_linear / _nf5_fq_linear_kernel
+ *           (axs/unified/triton_kernels.py:185-282,385-482), selected by
+ *           accelerated_linear for M * N <= _FUSED_SIZE_THRESHOLD
+ *           (axs/unified/backend.py:567-590, triton_kernels.py:382). */
+int axs6_nf5_fused_linear(const void* x, const void* w, const float* bias, void* y, int32_t dtype,
+                          int64_t M, int64_t N, int64_t K, int32_t block_size, int32_t quantize_input,
+                          void* stream);
+
 /* Device workspace (bytes) axs6_nf5_linear_backward needs for the requested
  * gradients. */
 size_t axs6_nf5_linear_backward_workspace(int64_t M, int64_t N, int64_t K, int32_t need_dx,

@@ -1,0 +1,144 @@
+"""The single-launch fused linear (``axs6_nf5_fused_linear``): NF5 FQ of
+each 32-wide K tile as it is loaded and an fp32 contraction, the
+reference's ``triton_fused_linear`` / ``_nf5_fq_linear_kernel``
+(triton_kernels.py:185-282,385-482 in the reference), which its
+``accelerated_linear`` selects for M*N <= 128K outputs.
+
+Bar: the products are those of the fp32 FQ values, so against the fp64
+product of the C oracle's FQ operands rel-L2 <= 1e-5 (fp32 accumulation;
+measured ~1e-7).  16-bit inputs: the FQ of the 16-bit values stays fp32 and
+only Y is rounded, as in the reference's fused kernel: >= 99% of Y
+bit-identical to the exact result rounded to the dtype, the rest one ulp
+(fp32 accumulation order)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+TOL = 1e-5
+
+
+def _inputs(lead, K, N, seed, outliers=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*lead, K, generator=g)
+    if outliers:
+        x[torch.rand(*lead, K, generator=g) < 0.01] *= 100.0
+    w = torch.randn(N, K, generator=g) * K ** -0.5
+    b = torch.randn(N, generator=g)
+    return x, w, b
+
+
+def _exact(x, w, b, quantize_input=True):
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).float().numpy()
+    xq = oracle.fake_quantize(x2, 32) if quantize_input else x2
+    wq = oracle.fake_quantize(w.float().numpy(), 32)
+    y = oracle.linear_reference(xq, wq, None if b is None else b.float().numpy())
+    return y.reshape(*x.shape[:-1], w.shape[0])
+
+
+# decode-like (M 1..32, K = N = 4096), square-ish, wide/short, ragged N and K
+@pytest.mark.parametrize("lead,K,N", [((1,), 4096, 4096), ((7,), 4096, 4096), ((32,), 4096, 4096),
+                                      ((128,), 1024, 1024), ((256,), 512, 512), ((362,), 4096, 362),
+                                      ((64,), 256, 2048), ((512,), 4096, 256), ((5,), 96, 13), ((3, 7), 160, 33),
+                                      ((2, 4, 8), 32, 64)])
+def test_fused_linear_f32_vs_fp64(lead, K, N):
+    from axs.unified import hip_linear
+
+    print(f"[fused linear {lead} K={K} N={N}]", flush=True)
+    x, w, b = _inputs(lead, K, N, K + N)
+    y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), b.to(DEV))
+    assert y.shape == (*lead, N) and y.dtype == torch.float32
+    err = oracle.rel_l2(y.cpu().numpy(), _exact(x, w, b))
+    print(f"  rel-L2 {err:.2e}", flush=True)
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("K", [33, 50, 100, 127, 255])
+def test_fused_linear_ragged_k(K):
+    from axs.unified import hip_linear
+
+    x, w, b = _inputs((64,), K, 32, K)
+    y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), None)
+    assert oracle.rel_l2(y.cpu().numpy(), _exact(x, w, None)) <= TOL
+
+
+def test_fused_linear_raw_input_and_no_bias():
+    from axs.unified import hip_linear
+
+    x, w, b = _inputs((96,), 1024, 768, 9)
+    y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), None, quantize_input=False)
+    assert oracle.rel_l2(y.cpu().numpy(), _exact(x, w, None, quantize_input=False)) <= TOL
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_fused_linear_16bit(dt):
+    from axs.unified import hip_linear
+
+    x, w, b = _inputs((48,), 2048, 1024, 11, outliers=False)
+    x, w = x.to(dt), w.to(dt)
+    y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), b.to(DEV))
+    assert y.dtype == dt
+    exact = _exact(x.float(), w.float(), b)
+    want = torch.from_numpy(exact.astype(np.float32)).to(dt)
+    got = y.cpu()
+    same = (got.view(torch.int16) == want.view(torch.int16)).float().mean().item()
+    print(f"  {dt}: {same:.5f} bit-identical to the rounded exact product", flush=True)
+    assert same >= 0.99
+    assert oracle.rel_l2(got.float().numpy(), exact) <= (4e-3 if dt == torch.bfloat16 else 5e-4)
+
+
+def test_fused_linear_fq_is_bit_exact_with_the_fq_kernel():
+    """With W = c I, c = 0.99999994 (the largest float below 1: its block
+    scale is 1 and its LUT cell the top code, so FQ(W) = I exactly), Y is
+    FQ(X) itself: the fused kernel's FQ of X must equal the oracle's bit for
+    bit."""
+    from axs.unified import hip_linear
+
+    K = 256
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(40, K, generator=g) * torch.exp2(torch.randint(-30, 30, (40, 1), generator=g).float())
+    eye = torch.eye(K) * 0.99999994
+    assert np.array_equal(oracle.fake_quantize(eye.numpy(), 32), np.eye(K, dtype=np.float32))
+    y = hip_linear.fused_forward(x.to(DEV), eye.to(DEV), None)
+    want = oracle.fake_quantize(x.numpy(), 32)
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_linear_forward_dispatches_small_outputs_to_the_fused_kernel(monkeypatch):
+    from axs.unified import hip_linear
+
+    calls = []
+    real = hip_linear.fused_forward
+    monkeypatch.setattr(hip_linear, "fused_forward", lambda *a, **k: calls.append(1) or real(*a, **k))
+    x, w, b = _inputs((32,), 4096, 4096, 1)
+    y = hip_linear.linear_forward(x.to(DEV), w.to(DEV), b.to(DEV), 32, True)        # 131072 outputs: fused
+    assert calls == [1]
+    assert oracle.rel_l2(y.cpu().numpy(), _exact(x, w, b)) <= TOL
+    x2, w2, _ = _inputs((33,), 256, 4096, 2)
+    hip_linear.linear_forward(x2.to(DEV), w2.to(DEV), None, 32, True)                # 135168: packed path
+    hip_linear.linear_forward(x.to(DEV), w.to(DEV), None, 16, True)                  # block 16: packed path
+    assert calls == [1]
+
+
+def test_fused_linear_errors():
+    from axs import _lib
+    from axs.unified import hip_linear
+
+    with pytest.raises(RuntimeError, match="CUDA"):
+        hip_linear.fused_forward(torch.randn(4, 32), torch.randn(8, 32))
+    x = torch.randn(4, 64, device=DEV)
+    w = torch.randn(8, 64, device=DEV)
+    y = torch.empty(4, 8, device=DEV)
+    with pytest.raises(_lib.LibraryError, match="block_size=32"):
+        _lib.call("axs6_nf5_fused_linear", x.data_ptr(), w.data_ptr(), None, y.data_ptr(), 0, 4, 8, 64, 16, 1,
+                  _lib.stream_of(x))
+    with pytest.raises(_lib.LibraryError, match="multiple of 32"):
+        _lib.call("axs6_nf5_fused_linear", x.data_ptr(), w.data_ptr(), None, y.data_ptr(), 0, 4, 8, 48, 32, 1,
+                  _lib.stream_of(x))
