@@ -175,3 +175,57 @@ def test_pipeline_warmup_and_stats():
     assert [a["warmup"] for a in ours] == [True, True, False, False]
     for a, b in zip(ours, ref):
         assert abs(a["loss"] - b["loss"]) <= 1e-3 * b["loss"]
+
+
+def test_pipeline_matches_the_reference_fixture_on_gpu():
+    """AXSTrainingPipelineUnified on the GPU against tests/golden/pipeline.npz,
+    written by the reference's own pipeline on the CPU with the same model,
+    data, schedule and two forced overflows: the overflow flags, loss scales
+    and step counters identical; losses, gradient norms and final parameters
+    within 1e-5 relative (GPU fp32 matmuls order their sums differently from
+    the CPU's)."""
+    import sys
+
+    import numpy as np
+
+    from axs.unified import AXSTrainingPipelineUnified
+    from conftest import GOLDEN, load_golden
+
+    sys.path.insert(0, GOLDEN)
+    import make_pipeline_golden as mk
+
+    want = load_golden("pipeline.npz")
+    model, opt, sched, x, loss_fn = mk.setup()
+    model = model.to(DEV)
+    # the optimiser was built on the CPU parameters: rebuild it on the moved ones
+    opt = torch.optim.SGD(model.parameters(), lr=0.1, momentum=0.9)
+    sched = torch.optim.lr_scheduler.LambdaLR(opt, lambda s: 1.0 / (1.0 + 0.1 * s))
+    p = AXSTrainingPipelineUnified(model, opt, scheduler=sched, **mk.PIPELINE_ARGS)
+    rows = []
+    xd = x.to(DEV)
+    ystate = {}
+
+    def loss_dev(out, inputs):
+        # the fixture's loss (mean squared error against its fixed targets, scaled
+        # at the forced-overflow calls) evaluated on the device
+        ystate.setdefault("n", 0)
+        ystate["n"] += 1
+        g = torch.Generator().manual_seed(1)
+        torch.randn(8, 16, generator=g)
+        t = torch.randn(8, 4, generator=g).to(DEV)
+        loss = ((out - t) ** 2).mean()
+        return loss * 1e35 if ystate["n"] in mk.OVERFLOW_AT else loss
+
+    for _ in range(mk.STEPS):
+        r = p.training_step(xd, loss_dev)
+        rows.append([r["loss"], r["loss_scale"], r["grad_norm"], float(r["overflow"]), float(r["step"]),
+                     float(r["warmup"])])
+    rows = np.array(rows, np.float64)
+    ref = want["steps"]
+    assert np.array_equal(rows[:, [1, 3, 4, 5]], ref[:, [1, 3, 4, 5]])
+    ok = ref[:, 3] == 0
+    assert np.allclose(rows[ok, 0], ref[ok, 0], rtol=1e-5, atol=0)
+    assert np.allclose(rows[ok, 2], ref[ok, 2], rtol=1e-5, atol=0)
+    for i, t in enumerate(model.parameters()):
+        a = t.detach().cpu().numpy()
+        assert np.allclose(a, want[f"param{i}"], rtol=1e-5, atol=1e-6), i

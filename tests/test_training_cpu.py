@@ -79,3 +79,30 @@ def test_unscale_rejects_cpu_gradients():
     w.grad = torch.ones(4)
     with pytest.raises(RuntimeError, match="CUDA"):
         unscale_and_clip_([w], 2.0, 1.0)
+
+
+def test_reference_style_pipeline_matches_the_reference_fixture():
+    """tests/ref_pipeline.py (the checker of AXSTrainingPipelineUnified and the
+    bench's reference-style timing) against tests/golden/pipeline.npz, which
+    the reference's own AXSTrainingPipelineUnified wrote on the same model,
+    data and schedule (make_pipeline_golden.py): loss-scale growth, two
+    forced overflows with back-off, clipping, SGD with momentum and a
+    LambdaLR scheduler -- every returned value and the final parameters
+    bit for bit."""
+    import os
+    import sys
+
+    import numpy as np
+
+    from conftest import GOLDEN, load_golden
+
+    sys.path.insert(0, GOLDEN)
+    import make_pipeline_golden as mk
+    from ref_pipeline import RefPipeline
+
+    want = load_golden("pipeline.npz")
+    rows, params = mk.run(RefPipeline)
+    assert np.array_equal(rows, want["steps"]), (rows, want["steps"])
+    assert rows[:, 3].tolist().count(1.0) == len(mk.OVERFLOW_AT)
+    for i, a in enumerate(params):
+        assert np.array_equal(a.view(np.uint32), want[f"param{i}"].view(np.uint32)), i
