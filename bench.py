@@ -601,9 +601,10 @@ def cpu_baseline_linear():
 
 def pmc_pass() -> int:
     """A short run for rocprofv3 counter collection: 5 NF5 fake-quantize
-    launches at 8192x4096 f32, 3 linear forwards at 4096^3 and, as the
-    calibration reference for HBM byte counters, 5 plain device copies of a
-    known 128 MiB (torch's copy kernel: 128 MiB read + 128 MiB written)."""
+    launches at 8192x4096 f32, 3 linear forwards at 4096^3, 5 fused
+    small-output linears at M=1, K=N=4096 and, as the calibration reference
+    for HBM byte counters, 5 plain device copies of a known 128 MiB (torch's
+    copy kernel: 128 MiB read + 128 MiB written)."""
     import torch
 
     from axs.unified import hip_linear
@@ -618,6 +619,9 @@ def pmc_pass() -> int:
     W = torch.randn(N, K, device="cuda", generator=g) * K ** -0.5
     for _ in range(3):
         hip_linear.linear_forward(X, W, None, 32, True)
+    x1 = torch.randn(1, K, device="cuda", generator=g)
+    for _ in range(5):
+        hip_linear.fused_forward(x1, W, None)
     src = torch.randn(32 * 1024 * 1024, device="cuda", generator=g)
     dst = torch.empty_like(src)
     for _ in range(5):
