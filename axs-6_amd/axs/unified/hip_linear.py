@@ -13,6 +13,8 @@ device first -- NF5 pads the last block with zeros, so this changes nothing.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 import torch.nn.functional as F
 
@@ -39,6 +41,12 @@ def _pad_last(t: torch.Tensor, mult: int) -> torch.Tensor:
 def _pad_rows(t: torch.Tensor, mult: int) -> torch.Tensor:
     pad = (-t.shape[0]) % mult
     return F.pad(t, (0, 0, 0, pad)) if pad else t
+
+
+def _rows(t: torch.Tensor, cols: int) -> torch.Tensor:
+    """t viewed as (rows, cols) over its last dim; unlike reshape(-1, cols)
+    this also works when cols is 0 (an empty contraction or output)."""
+    return t.reshape(math.prod(t.shape[:-1]), cols)
 
 
 def _dense(t: torch.Tensor) -> torch.Tensor:
@@ -78,7 +86,7 @@ def _forward(input, weight, bias, block_size, quantize_input):
     if Kw != K:
         raise RuntimeError(f"{fn}: input has {K} features but weight expects {Kw}")
     dtype = input.dtype if input.dtype in _SUPPORTED else torch.float32
-    x2 = input.reshape(-1, K).to(dtype)
+    x2 = _rows(input, K).to(dtype)
     w2 = weight.to(dtype)
     k_true, n_true = K, N
     x2 = _dense(_pad_last(x2, block_size))
@@ -137,7 +145,7 @@ def fused_forward(input, weight, bias=None, quantize_input=True):
     if Kw != K:
         raise RuntimeError(f"{fn}: input has {K} features but weight expects {Kw}")
     dtype = input.dtype if input.dtype in _SUPPORTED else torch.float32
-    x2 = _dense(_pad_last(input.reshape(-1, K).to(dtype), 32))
+    x2 = _dense(_pad_last(_rows(input, K).to(dtype), 32))
     w2 = _dense(_pad_last(weight.to(dtype), 32))
     M, Kb = x2.shape
     dev = x2.device
@@ -171,7 +179,7 @@ def backward(grad_output, saved: Saved, block_size: int, quantize_grad: bool,
     ``seed`` fixes the stochastic rounding of dY (default: a fresh draw)."""
     M, N, K = saved.M, saved.N, saved.K
     dev = saved.xq.device
-    dy = grad_output.reshape(-1, saved.n_true).to(saved.dtype)
+    dy = _rows(grad_output, saved.n_true).to(saved.dtype)
     if N != saved.n_true:
         dy = _pad_last(dy, block_size)
     dy = _dense(dy)
@@ -222,7 +230,7 @@ def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     if b.shape[0] != K:
         raise RuntimeError(f"{fn}: shapes {tuple(a.shape)} and {tuple(b.shape)} do not contract")
     N = b.shape[1]
-    a2 = _dense(_pad_last(a.reshape(-1, K).float(), 32))
+    a2 = _dense(_pad_last(_rows(a, K).float(), 32))
     bt = _dense(_pad_last(b.float().t(), 32))               # [N, K'] rows along the contraction
     M, Kb = a2.shape
     Kp = padded_k(Kb)

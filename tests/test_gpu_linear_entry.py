@@ -195,3 +195,27 @@ def test_triton_fused_linear_config3_full_size():
     wq = oracle.fake_quantize(w.numpy())
     want = oracle.linear_reference(xq, wq, b.numpy())
     _check(out[torch.from_numpy(rows).to(DEV)], want, "config 3 sampled rows")
+
+
+def test_empty_dimensions_follow_f_linear():
+    """K = 0 (an empty contraction gives the bias), N = 0 and M = 0, through the
+    fused path, the packed path and autograd, as F.linear would."""
+    from axs.unified import hip_linear
+    from axs.unified.functional_unified import axs_linear_unified
+
+    b = torch.randn(3, device=DEV)
+    x0 = torch.randn(4, 0, device=DEV)
+    w0 = torch.randn(3, 0, device=DEV)
+    for y in (hip_linear.linear_forward(x0, w0, b), hip_linear.forward_train(x0, w0, b)[0]):
+        assert y.shape == (4, 3) and torch.equal(y, b.expand(4, 3))
+    assert torch.equal(hip_linear.linear_forward(x0, w0, None), torch.zeros(4, 3, device=DEV))
+    y = hip_linear.linear_forward(torch.randn(2, 5, 32, device=DEV), torch.randn(0, 32, device=DEV), None)
+    assert y.shape == (2, 5, 0)
+    xe = torch.randn(0, 32, device=DEV, requires_grad=True)
+    we = torch.randn(16, 32, device=DEV, requires_grad=True)
+    be = torch.randn(16, device=DEV, requires_grad=True)
+    out = axs_linear_unified(xe, we, be)
+    assert out.shape == (0, 16)
+    out.sum().backward()
+    assert torch.count_nonzero(we.grad).item() == 0 and torch.count_nonzero(be.grad).item() == 0
+    assert xe.grad.shape == (0, 32)
