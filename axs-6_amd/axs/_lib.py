@@ -52,6 +52,11 @@ _SIGNATURES: dict[str, list] = {
     "axs6_nf5_unpack_wire": [_vp, _i64, _i64, _i32, _vp, _vp],
     "axs6_nf5_wire_from_codes": [_vp, _vp, _vp, _i64, _i64, _i32, _vp, _vp],
     "axs6_nf5_wire_to_codes": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp],
+    "axs6_nf5_block_bytes": [_i64, _i64, _i32],
+    "axs6_nf5_pack_blocks": [_vp, _i32, _i64, _i64, _i32, _vp, _vp],
+    "axs6_nf5_unpack_blocks": [_vp, _i64, _i64, _i32, _vp, _vp],
+    "axs6_nf5_blocks_from_codes": [_vp, _vp, _vp, _i64, _i64, _i32, _vp, _vp],
+    "axs6_nf5_blocks_to_codes": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp],
     "axs6_multi_tensor_workspace": [_vp, _i32],
     "axs6_multi_tensor_unscale_clip": [_vp, _vp, _vp, _i32, ctypes.c_float, ctypes.c_float, _i32, _vp, _i64, _vp, _vp],
     "axs6_nf5_linear_backward": [_vp, _i32, _i64, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _vp, _vp,
@@ -61,7 +66,7 @@ _SIGNATURES: dict[str, list] = {
 }
 # entry points that return a value rather than an axs6_status
 _RESTYPES = {"axs6_linear_padded_k": _i64, "axs6_nf5_linear_backward_workspace": ctypes.c_size_t,
-             "axs6_nf5_wire_bytes": _i64, "axs6_multi_tensor_workspace": _i64,
+             "axs6_nf5_wire_bytes": _i64, "axs6_nf5_block_bytes": _i64, "axs6_multi_tensor_workspace": _i64,
              "axs6_nf5_row_stats_workspace": _i64}
 
 

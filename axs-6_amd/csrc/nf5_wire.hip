@@ -11,6 +11,13 @@
 // (axs/unified/distributed.py:147-198); the codes are those of
 // _pack_gradient (:70-115), i.e. quantize_unified with nearest rounding.
 //
+// The AXSBlock byte form (AXSBlock.to_bytes / from_bytes, axs/core.py:97-152)
+// differs only in its header: two bytes, the little-endian word
+// e << 2 | config (config DENSE = 0 when written, ignored when decoded, as
+// the reference's decoder ignores it), then the same 6-bit little-endian
+// stream, so a 32-value block takes 26 bytes.  Every kernel below takes the
+// header size HB (1 wire, 2 AXSBlock) as a template parameter.
+//
 // One thread handles one group of four values (three bytes); a block is
 // bs/4 neighbouring lanes, whose amax is a DPP reduction.
 //
@@ -39,6 +46,25 @@ __device__ __forceinline__ void unpack3(const uint8_t* in, int (&q)[4]) {
     q[1] = ((b0 >> 6) & 0x03) | ((b1 & 0x0F) << 2);
     q[2] = ((b1 >> 4) & 0x0F) | ((b2 & 0x03) << 4);
     q[3] = (b2 >> 2) & 0x3F;
+}
+
+// Record header of HB bytes.  HB = 1 (wire): the exponent byte.  HB = 2
+// (AXSBlock): the little-endian 16-bit word e << 2 | config, written with
+// config DENSE (0); bits 10..15 are padding, read as zero.
+template <int HB>
+__device__ __forceinline__ void put_header(uint8_t* rec, int e8) {
+    if constexpr (HB == 1) {
+        rec[0] = (uint8_t)e8;
+    } else {
+        rec[0] = (uint8_t)(e8 << 2);
+        rec[1] = (uint8_t)(e8 >> 6);
+    }
+}
+
+template <int HB>
+__device__ __forceinline__ int get_exponent(const uint8_t* rec) {
+    if constexpr (HB == 1) return rec[0];
+    else return (rec[0] >> 2) | ((rec[1] & 0x03) << 6);
 }
 
 struct WireGeom {
@@ -70,14 +96,14 @@ __device__ __forceinline__ int wire_codes(const float (&f)[4], uint32_t m, const
 }
 
 // x [rows, cols] -> records (general path), one group per thread.
-template <int DT, int BS>
+template <int HB, int DT, int BS>
 __global__ __launch_bounds__(kThreads) void wire_pack_kernel(const typename Elem<DT>::S* __restrict__ x, WireGeom g,
                                                              const uint8_t* __restrict__ band_g,
                                                              const uint8_t* __restrict__ rev_g,
                                                              uint8_t* __restrict__ buf) {
     using E = Elem<DT>;
     constexpr int GPB = BS / 4;                 // groups (lanes) per block
-    constexpr int REC = 1 + BS * 3 / 4;         // bytes per block record
+    constexpr int REC = HB + BS * 3 / 4;        // bytes per block record
     __shared__ uint32_t band_w[kBandSize / 4];
     __shared__ uint8_t rev_s[kLutSize];
     const int tid = threadIdx.x;
@@ -110,17 +136,18 @@ __global__ __launch_bounds__(kThreads) void wire_pack_kernel(const typename Elem
         const int e8 = wire_codes(f, m, band_s, rev_s, qv);
         if (vq) {
             uint8_t* rec = buf + blk * REC;
-            if (j4 == 0) rec[0] = (uint8_t)e8;
-            pack3(qv, rec + 1 + 3 * j4);
+            if (j4 == 0) put_header<HB>(rec, e8);
+            pack3(qv, rec + HB + 3 * j4);
         }
     }
 }
 
 // Fast-path geometry: kWireTiles tiles of kThreads groups per workgroup
-// iteration; a tile's records take wire_tile_bytes<BS>() bytes.
+// iteration; a tile's records take wire_tile_bytes<HB, BS>() bytes
+// (800, 832, 896 for wire blocks of 32, 16, 8; 832, 896, 1024 for AXSBlocks).
 constexpr int kWireTiles = 4;
-template <int BS>
-constexpr int wire_tile_bytes() { return kThreads / (BS / 4) * (1 + BS * 3 / 4); }
+template <int HB, int BS>
+constexpr int wire_tile_bytes() { return kThreads / (BS / 4) * (HB + BS * 3 / 4); }
 
 // The four values of group q (flat index 4q), as floats.
 template <int DT>
@@ -143,14 +170,14 @@ __device__ __forceinline__ void load_group(const typename Elem<DT>::S* x, int64_
 
 // Fast-path pack: groups = rows * cols / 4 with cols % BS == 0; x aligned to
 // its 4-value group, buf to 16 bytes.  Same record bytes as wire_pack_kernel.
-template <int DT, int BS>
+template <int HB, int DT, int BS>
 __global__ __launch_bounds__(kThreads) void wire_pack_vec_kernel(const typename Elem<DT>::S* __restrict__ x,
                                                                  int64_t groups, const uint8_t* __restrict__ band_g,
                                                                  const uint8_t* __restrict__ rev_g,
                                                                  uint8_t* __restrict__ buf) {
     constexpr int GPB = BS / 4;
-    constexpr int REC = 1 + BS * 3 / 4;
-    constexpr int TB = wire_tile_bytes<BS>();
+    constexpr int REC = HB + BS * 3 / 4;
+    constexpr int TB = wire_tile_bytes<HB, BS>();
     constexpr int U = kWireTiles;
     static_assert(TB % 16 == 0 && kThreads % GPB == 0, "tiles of whole blocks and 16-byte chunks");
     __shared__ uint32_t band_w[kBandSize / 4];
@@ -186,8 +213,8 @@ __global__ __launch_bounds__(kThreads) void wire_pack_vec_kernel(const typename 
             m = group_umax<GPB>(m);
             int qv[4];
             const int e8 = wire_codes(f[u], m, band_s, rev_s, qv);
-            if (j4 == 0) rec[u * TB] = (uint8_t)e8;
-            pack3(qv, rec + u * TB + 1 + 3 * j4);
+            if (j4 == 0) put_header<HB>(rec + u * TB, e8);
+            pack3(qv, rec + u * TB + HB + 3 * j4);
         }
         __syncthreads();
         // the U tiles' records are contiguous in buf from t0 * TB
@@ -206,13 +233,13 @@ __global__ __launch_bounds__(kThreads) void wire_pack_vec_kernel(const typename 
 }
 
 // Fast-path unpack, the inverse geometry: y [groups * 4] f32 (16-byte aligned), buf 16-byte aligned.
-template <int BS>
+template <int HB, int BS>
 __global__ __launch_bounds__(kThreads) void wire_unpack_vec_kernel(const uint8_t* __restrict__ buf, int64_t groups,
                                                                    const float* __restrict__ cb_g,
                                                                    float* __restrict__ y) {
     constexpr int GPB = BS / 4;
-    constexpr int REC = 1 + BS * 3 / 4;
-    constexpr int TB = wire_tile_bytes<BS>();
+    constexpr int REC = HB + BS * 3 / 4;
+    constexpr int TB = wire_tile_bytes<HB, BS>();
     constexpr int U = kWireTiles;
     static_assert(TB % 16 == 0 && kThreads % GPB == 0, "tiles of whole blocks and 16-byte chunks");
     __shared__ float cb[kLevels];
@@ -241,9 +268,9 @@ __global__ __launch_bounds__(kThreads) void wire_unpack_vec_kernel(const uint8_t
             const int64_t q = (t0 + u) * kThreads + tid;
             if (q < groups) {
                 const uint8_t* r = rec + u * TB;
-                const float scale = pow2_float((int)r[0] - kExpBias);
+                const float scale = pow2_float(get_exponent<HB>(r) - kExpBias);
                 int qv[4];
-                unpack3(r + 1 + 3 * j4, qv);
+                unpack3(r + HB + 3 * j4, qv);
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -269,11 +296,11 @@ unsigned wire_vec_grid(int64_t groups) {
 // records -> y [rows, cols] f32: codebook[code] * 2^(e-127), negated where the
 // sign bit is set (_unpack_from_flat_buffer + _unpack_gradient, :118-144,201-232).
 // General path, one group per thread.
-template <int BS>
+template <int HB, int BS>
 __global__ __launch_bounds__(kThreads) void wire_unpack_kernel(const uint8_t* __restrict__ buf, WireGeom g,
                                                                const float* __restrict__ cb_g, float* __restrict__ y) {
     constexpr int GPB = BS / 4;
-    constexpr int REC = 1 + BS * 3 / 4;
+    constexpr int REC = HB + BS * 3 / 4;
     __shared__ float cb[kLevels];
     if (threadIdx.x < kLevels) cb[threadIdx.x] = cb_g[threadIdx.x];
     __syncthreads();
@@ -284,9 +311,9 @@ __global__ __launch_bounds__(kThreads) void wire_unpack_kernel(const uint8_t* __
         const int64_t r = blk / g.nblk;
         const int64_t c0 = (blk - r * g.nblk) * BS + j4 * 4;
         const uint8_t* rec = buf + blk * REC;
-        const float scale = pow2_float((int)rec[0] - kExpBias);
+        const float scale = pow2_float(get_exponent<HB>(rec) - kExpBias);
         int qv[4];
-        unpack3(rec + 1 + 3 * j4, qv);
+        unpack3(rec + HB + 3 * j4, qv);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int64_t c = c0 + e;
@@ -301,11 +328,12 @@ __global__ __launch_bounds__(kThreads) void wire_unpack_kernel(const uint8_t* __
 // AXSTensor components (exponents [rows, nblk], codes and signs [rows, nblk, bs])
 // <-> records, for the component-level API (_pack_to_flat_buffer /
 // _unpack_from_flat_buffer).
+template <int HB>
 __global__ __launch_bounds__(kThreads) void wire_from_codes_kernel(const uint8_t* __restrict__ exps,
                                                                    const uint8_t* __restrict__ codes,
                                                                    const uint8_t* __restrict__ signs, int bs,
                                                                    int64_t groups, uint8_t* __restrict__ buf) {
-    const int gpb = bs / 4, rec_bytes = 1 + bs * 3 / 4;
+    const int gpb = bs / 4, rec_bytes = HB + bs * 3 / 4;
     const int64_t step = (int64_t)gridDim.x * kThreads;
     for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < groups; q += step) {
         const int64_t blk = q / gpb;
@@ -317,24 +345,25 @@ __global__ __launch_bounds__(kThreads) void wire_from_codes_kernel(const uint8_t
             qv[e] = (codes[o] & 0x1F) | ((signs && signs[o]) ? 0x20 : 0);
         }
         uint8_t* rec = buf + blk * rec_bytes;
-        if (j4 == 0) rec[0] = exps[blk];
-        pack3(qv, rec + 1 + 3 * j4);
+        if (j4 == 0) put_header<HB>(rec, exps[blk]);
+        pack3(qv, rec + HB + 3 * j4);
     }
 }
 
+template <int HB>
 __global__ __launch_bounds__(kThreads) void wire_to_codes_kernel(const uint8_t* __restrict__ buf, int bs,
                                                                  int64_t groups, uint8_t* __restrict__ exps,
                                                                  uint8_t* __restrict__ codes,
                                                                  uint8_t* __restrict__ signs) {
-    const int gpb = bs / 4, rec_bytes = 1 + bs * 3 / 4;
+    const int gpb = bs / 4, rec_bytes = HB + bs * 3 / 4;
     const int64_t step = (int64_t)gridDim.x * kThreads;
     for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < groups; q += step) {
         const int64_t blk = q / gpb;
         const int j4 = (int)(q % gpb);
         const uint8_t* rec = buf + blk * rec_bytes;
         int qv[4];
-        unpack3(rec + 1 + 3 * j4, qv);
-        if (j4 == 0) exps[blk] = rec[0];
+        unpack3(rec + HB + 3 * j4, qv);
+        if (j4 == 0) exps[blk] = (uint8_t)get_exponent<HB>(rec);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int64_t o = q * 4 + e;
@@ -356,110 +385,160 @@ int check_wire(const char* fn, int64_t rows, int64_t cols, int bs) {
     return AXS6_OK;
 }
 
+int64_t record_bytes(int hb, int64_t rows, int64_t cols, int bs) {
+    if (rows < 0 || cols < 0 || !valid_block(bs)) return -1;
+    const int64_t nblk = (cols + bs - 1) / bs;
+    return rows * nblk * (hb + bs * 3 / 4);
+}
+
+template <int HB, int DT>
+void launch_pack(const void* x, const WireGeom& g, int bs, bool vec, const DeviceTables& t, uint8_t* buf,
+                 hipStream_t st) {
+    using S = typename Elem<DT>::S;
+    const S* xs = (const S*)x;
+    if (vec) {
+        const dim3 grid(wire_vec_grid(g.groups));
+        if (bs == 8) wire_pack_vec_kernel<HB, DT, 8><<<grid, kThreads, 0, st>>>(xs, g.groups, t.band, t.rev, buf);
+        else if (bs == 16) wire_pack_vec_kernel<HB, DT, 16><<<grid, kThreads, 0, st>>>(xs, g.groups, t.band, t.rev, buf);
+        else wire_pack_vec_kernel<HB, DT, 32><<<grid, kThreads, 0, st>>>(xs, g.groups, t.band, t.rev, buf);
+    } else {
+        const dim3 grid(wire_grid(g.groups));
+        if (bs == 8) wire_pack_kernel<HB, DT, 8><<<grid, kThreads, 0, st>>>(xs, g, t.band, t.rev, buf);
+        else if (bs == 16) wire_pack_kernel<HB, DT, 16><<<grid, kThreads, 0, st>>>(xs, g, t.band, t.rev, buf);
+        else wire_pack_kernel<HB, DT, 32><<<grid, kThreads, 0, st>>>(xs, g, t.band, t.rev, buf);
+    }
+}
+
+// x [rows, cols] -> records with HB-byte headers.
+template <int HB>
+int pack_records(const char* fn, const void* x, int dtype, int64_t rows, int64_t cols, int bs, uint8_t* buffer,
+                 void* stream) {
+    if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
+    int rc = check_wire(fn, rows, cols, bs);
+    if (rc) return rc;
+    if (rows == 0 || cols == 0) return AXS6_OK;
+    if (!x || !buffer) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    DeviceTables t;
+    if ((rc = device_tables(&t))) return rc;
+    const int64_t nblk = (cols + bs - 1) / bs;
+    const WireGeom g{rows, cols, nblk, rows * nblk * (bs / 4)};
+    const int esize = dtype == AXS6_F32 ? 4 : 2;
+    const bool vec = cols % bs == 0 && (uintptr_t)x % (4 * esize) == 0 && (uintptr_t)buffer % 16 == 0;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == AXS6_F32) launch_pack<HB, AXS6_F32>(x, g, bs, vec, t, buffer, st);
+    else if (dtype == AXS6_BF16) launch_pack<HB, AXS6_BF16>(x, g, bs, vec, t, buffer, st);
+    else launch_pack<HB, AXS6_F16>(x, g, bs, vec, t, buffer, st);
+    return check_launch(fn);
+}
+
+// records -> y [rows, cols] f32.
+template <int HB>
+int unpack_records(const char* fn, const uint8_t* buffer, int64_t rows, int64_t cols, int bs, float* y,
+                   void* stream) {
+    int rc = check_wire(fn, rows, cols, bs);
+    if (rc) return rc;
+    if (rows == 0 || cols == 0) return AXS6_OK;
+    if (!buffer || !y) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    DeviceTables t;
+    if ((rc = device_tables(&t))) return rc;
+    const int64_t nblk = (cols + bs - 1) / bs;
+    const WireGeom g{rows, cols, nblk, rows * nblk * (bs / 4)};
+    hipStream_t st = (hipStream_t)stream;
+    if (cols % bs == 0 && (uintptr_t)y % 16 == 0 && (uintptr_t)buffer % 16 == 0) {
+        const dim3 grid(wire_vec_grid(g.groups));
+        if (bs == 8) wire_unpack_vec_kernel<HB, 8><<<grid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
+        else if (bs == 16) wire_unpack_vec_kernel<HB, 16><<<grid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
+        else wire_unpack_vec_kernel<HB, 32><<<grid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
+        return check_launch(fn);
+    }
+    const dim3 grid(wire_grid(g.groups));
+    if (bs == 8) wire_unpack_kernel<HB, 8><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);
+    else if (bs == 16) wire_unpack_kernel<HB, 16><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);
+    else wire_unpack_kernel<HB, 32><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);
+    return check_launch(fn);
+}
+
+template <int HB>
+int records_from_codes(const char* fn, const uint8_t* exponents, const uint8_t* codes, const uint8_t* signs,
+                       int64_t rows, int64_t nblk, int bs, uint8_t* buffer, void* stream) {
+    int rc = check_wire(fn, rows, nblk * (int64_t)bs, bs);
+    if (rc) return rc;
+    if (rows == 0 || nblk == 0) return AXS6_OK;
+    if (!exponents || !codes || !buffer) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    const int64_t groups = rows * nblk * (bs / 4);
+    wire_from_codes_kernel<HB><<<dim3(wire_grid(groups)), kThreads, 0, (hipStream_t)stream>>>(exponents, codes, signs,
+                                                                                              bs, groups, buffer);
+    return check_launch(fn);
+}
+
+template <int HB>
+int records_to_codes(const char* fn, const uint8_t* buffer, int64_t rows, int64_t nblk, int bs, uint8_t* exponents,
+                     uint8_t* codes, uint8_t* signs, void* stream) {
+    int rc = check_wire(fn, rows, nblk * (int64_t)bs, bs);
+    if (rc) return rc;
+    if (rows == 0 || nblk == 0) return AXS6_OK;
+    if (!buffer || !exponents || !codes) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    const int64_t groups = rows * nblk * (bs / 4);
+    wire_to_codes_kernel<HB><<<dim3(wire_grid(groups)), kThreads, 0, (hipStream_t)stream>>>(buffer, bs, groups,
+                                                                                            exponents, codes, signs);
+    return check_launch(fn);
+}
+
 }  // namespace
 }  // namespace axs6
 
 using namespace axs6;
 
 extern "C" int64_t axs6_nf5_wire_bytes(int64_t rows, int64_t cols, int32_t block_size) {
-    if (rows < 0 || cols < 0 || !valid_block(block_size)) return -1;
-    const int64_t nblk = (cols + block_size - 1) / block_size;
-    return rows * nblk * (1 + block_size * 3 / 4);
+    return record_bytes(1, rows, cols, block_size);
 }
 
 extern "C" int axs6_nf5_pack_wire(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
                                   uint8_t* buffer, void* stream) {
-    const char* fn = "axs6_nf5_pack_wire";
-    if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
-    int rc = check_wire(fn, rows, cols, block_size);
-    if (rc) return rc;
-    if (rows == 0 || cols == 0) return AXS6_OK;
-    if (!x || !buffer) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
-    DeviceTables t;
-    if ((rc = device_tables(&t))) return rc;
-    const int64_t nblk = (cols + block_size - 1) / block_size;
-    const WireGeom g{rows, cols, nblk, rows * nblk * (block_size / 4)};
-    hipStream_t st = (hipStream_t)stream;
-    const int esize = dtype == AXS6_F32 ? 4 : 2;
-    if (cols % block_size == 0 && (uintptr_t)x % (4 * esize) == 0 && (uintptr_t)buffer % 16 == 0) {
-        const dim3 vgrid(wire_vec_grid(g.groups));
-#define AXS6_WIRE_VEC(DT_)                                                                                     \
-    do {                                                                                                       \
-        using S_ = typename Elem<DT_>::S;                                                                      \
-        if (block_size == 8) wire_pack_vec_kernel<DT_, 8><<<vgrid, kThreads, 0, st>>>((const S_*)x, g.groups, t.band, t.rev, buffer);   \
-        else if (block_size == 16) wire_pack_vec_kernel<DT_, 16><<<vgrid, kThreads, 0, st>>>((const S_*)x, g.groups, t.band, t.rev, buffer); \
-        else wire_pack_vec_kernel<DT_, 32><<<vgrid, kThreads, 0, st>>>((const S_*)x, g.groups, t.band, t.rev, buffer);     \
-    } while (0)
-        if (dtype == AXS6_F32) AXS6_WIRE_VEC(AXS6_F32);
-        else if (dtype == AXS6_BF16) AXS6_WIRE_VEC(AXS6_BF16);
-        else AXS6_WIRE_VEC(AXS6_F16);
-#undef AXS6_WIRE_VEC
-        return check_launch(fn);
-    }
-    const dim3 grid(wire_grid(g.groups));
-#define AXS6_WIRE(DT_)                                                                                         \
-    do {                                                                                                       \
-        using S_ = typename Elem<DT_>::S;                                                                      \
-        if (block_size == 8) wire_pack_kernel<DT_, 8><<<grid, kThreads, 0, st>>>((const S_*)x, g, t.band, t.rev, buffer);   \
-        else if (block_size == 16) wire_pack_kernel<DT_, 16><<<grid, kThreads, 0, st>>>((const S_*)x, g, t.band, t.rev, buffer); \
-        else wire_pack_kernel<DT_, 32><<<grid, kThreads, 0, st>>>((const S_*)x, g, t.band, t.rev, buffer);     \
-    } while (0)
-    if (dtype == AXS6_F32) AXS6_WIRE(AXS6_F32);
-    else if (dtype == AXS6_BF16) AXS6_WIRE(AXS6_BF16);
-    else AXS6_WIRE(AXS6_F16);
-#undef AXS6_WIRE
-    return check_launch(fn);
+    return pack_records<1>("axs6_nf5_pack_wire", x, dtype, rows, cols, block_size, buffer, stream);
 }
 
 extern "C" int axs6_nf5_unpack_wire(const uint8_t* buffer, int64_t rows, int64_t cols, int32_t block_size, float* y,
                                     void* stream) {
-    const char* fn = "axs6_nf5_unpack_wire";
-    int rc = check_wire(fn, rows, cols, block_size);
-    if (rc) return rc;
-    if (rows == 0 || cols == 0) return AXS6_OK;
-    if (!buffer || !y) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
-    DeviceTables t;
-    if ((rc = device_tables(&t))) return rc;
-    const int64_t nblk = (cols + block_size - 1) / block_size;
-    const WireGeom g{rows, cols, nblk, rows * nblk * (block_size / 4)};
-    hipStream_t st = (hipStream_t)stream;
-    if (cols % block_size == 0 && (uintptr_t)y % 16 == 0 && (uintptr_t)buffer % 16 == 0) {
-        const dim3 vgrid(wire_vec_grid(g.groups));
-        if (block_size == 8) wire_unpack_vec_kernel<8><<<vgrid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
-        else if (block_size == 16) wire_unpack_vec_kernel<16><<<vgrid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
-        else wire_unpack_vec_kernel<32><<<vgrid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
-        return check_launch(fn);
-    }
-    const dim3 grid(wire_grid(g.groups));
-    if (block_size == 8) wire_unpack_kernel<8><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);
-    else if (block_size == 16) wire_unpack_kernel<16><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);
-    else wire_unpack_kernel<32><<<grid, kThreads, 0, st>>>(buffer, g, t.codebook, y);
-    return check_launch(fn);
+    return unpack_records<1>("axs6_nf5_unpack_wire", buffer, rows, cols, block_size, y, stream);
 }
 
 extern "C" int axs6_nf5_wire_from_codes(const uint8_t* exponents, const uint8_t* codes, const uint8_t* signs,
                                         int64_t rows, int64_t nblk, int32_t block_size, uint8_t* buffer,
                                         void* stream) {
-    const char* fn = "axs6_nf5_wire_from_codes";
-    int rc = check_wire(fn, rows, nblk * (int64_t)block_size, block_size);
-    if (rc) return rc;
-    if (rows == 0 || nblk == 0) return AXS6_OK;
-    if (!exponents || !codes || !buffer) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
-    const int64_t groups = rows * nblk * (block_size / 4);
-    wire_from_codes_kernel<<<dim3(wire_grid(groups)), kThreads, 0, (hipStream_t)stream>>>(exponents, codes, signs,
-                                                                                          block_size, groups, buffer);
-    return check_launch(fn);
+    return records_from_codes<1>("axs6_nf5_wire_from_codes", exponents, codes, signs, rows, nblk, block_size, buffer,
+                                 stream);
 }
 
 extern "C" int axs6_nf5_wire_to_codes(const uint8_t* buffer, int64_t rows, int64_t nblk, int32_t block_size,
                                       uint8_t* exponents, uint8_t* codes, uint8_t* signs, void* stream) {
-    const char* fn = "axs6_nf5_wire_to_codes";
-    int rc = check_wire(fn, rows, nblk * (int64_t)block_size, block_size);
-    if (rc) return rc;
-    if (rows == 0 || nblk == 0) return AXS6_OK;
-    if (!buffer || !exponents || !codes) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
-    const int64_t groups = rows * nblk * (block_size / 4);
-    wire_to_codes_kernel<<<dim3(wire_grid(groups)), kThreads, 0, (hipStream_t)stream>>>(buffer, block_size, groups,
-                                                                                        exponents, codes, signs);
-    return check_launch(fn);
+    return records_to_codes<1>("axs6_nf5_wire_to_codes", buffer, rows, nblk, block_size, exponents, codes, signs,
+                               stream);
+}
+
+extern "C" int64_t axs6_nf5_block_bytes(int64_t rows, int64_t cols, int32_t block_size) {
+    return record_bytes(2, rows, cols, block_size);
+}
+
+extern "C" int axs6_nf5_pack_blocks(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
+                                    uint8_t* buffer, void* stream) {
+    return pack_records<2>("axs6_nf5_pack_blocks", x, dtype, rows, cols, block_size, buffer, stream);
+}
+
+extern "C" int axs6_nf5_unpack_blocks(const uint8_t* buffer, int64_t rows, int64_t cols, int32_t block_size, float* y,
+                                      void* stream) {
+    return unpack_records<2>("axs6_nf5_unpack_blocks", buffer, rows, cols, block_size, y, stream);
+}
+
+extern "C" int axs6_nf5_blocks_from_codes(const uint8_t* exponents, const uint8_t* codes, const uint8_t* signs,
+                                          int64_t rows, int64_t nblk, int32_t block_size, uint8_t* buffer,
+                                          void* stream) {
+    return records_from_codes<2>("axs6_nf5_blocks_from_codes", exponents, codes, signs, rows, nblk, block_size,
+                                 buffer, stream);
+}
+
+extern "C" int axs6_nf5_blocks_to_codes(const uint8_t* buffer, int64_t rows, int64_t nblk, int32_t block_size,
+                                        uint8_t* exponents, uint8_t* codes, uint8_t* signs, void* stream) {
+    return records_to_codes<2>("axs6_nf5_blocks_to_codes", buffer, rows, nblk, block_size, exponents, codes, signs,
+                               stream);
 }

@@ -15,7 +15,7 @@ linear TFLOP/s @4096^3 bf16"):
   * "linear_train": config 4, forward + backward at its four shapes
     (6*M*N*K FLOPs per step).
   * "wire": the 6.25-bit gradient wire format (quantize+pack, unpack) at
-    8192x4096, GB/s.
+    8192x4096, GB/s, and the AXSBlock record stream (26 B per 32 values).
   * "codec": quantize (exponents, codes, signs and the FQ output) and
     dequantize at 8192x4096, GB/s.
   * "configs": the smaller config-1/2 shapes (FQ at 256^2 and 4096^2,
@@ -208,9 +208,11 @@ def bench_wire(reps: int = 20, warmup: int = 3):
     """NF5 wire format (the reference's 6.25-bit gradient buffer) of one
     8192x4096 f32 tensor: quantize+pack and unpack+dequantize, one kernel each.
     Algorithmic bytes: pack 4 B read + 25/32 B written per value; unpack the
-    reverse.  HIP-event device time per call."""
+    reverse.  The same for the AXSBlock record stream (26/32 B per value).
+    HIP-event device time per call."""
     import torch
 
+    from axs import blocks
     from axs.unified import distributed as d
 
     g = torch.Generator(device="cuda").manual_seed(3)
@@ -232,11 +234,20 @@ def bench_wire(reps: int = 20, warmup: int = 3):
     pack_ms = timed(lambda: d.pack_gradient_to_buffer(x, 32))
     unpack_ms = timed(lambda: d.unpack_buffer_to_gradient(buf, x.shape, 32))
     nbytes = x.numel() * 4 + buf.numel()
+    # the AXSBlock record stream (2-byte header, 26 B per 32 values): same kernels
+    recs = blocks.encode_blocks(x, 32)
+    bpack_ms = timed(lambda: blocks.encode_blocks(x, 32))
+    bunpack_ms = timed(lambda: blocks.decode_blocks(recs, x.shape, 32))
+    bbytes = x.numel() * 4 + recs.numel()
     return {"metric": "NF5 wire format GB/s @8192x4096 fp32 (quantize+pack, unpack+dequantize)",
             "buffer_bytes": buf.numel(), "bits_per_value": round(buf.numel() * 8 / x.numel(), 4),
             "pack_ms": round(pack_ms, 5), "unpack_ms": round(unpack_ms, 5),
             "pack_gbs": round(nbytes / (pack_ms * 1e-3) / 1e9, 1),
-            "unpack_gbs": round(nbytes / (unpack_ms * 1e-3) / 1e9, 1)}
+            "unpack_gbs": round(nbytes / (unpack_ms * 1e-3) / 1e9, 1),
+            "axs_blocks": {"buffer_bytes": recs.numel(),
+                           "encode_ms": round(bpack_ms, 5), "decode_ms": round(bunpack_ms, 5),
+                           "encode_gbs": round(bbytes / (bpack_ms * 1e-3) / 1e9, 1),
+                           "decode_gbs": round(bbytes / (bunpack_ms * 1e-3) / 1e9, 1)}}
 
 
 def bench_codec(reps: int = 20, warmup: int = 3):
@@ -786,7 +797,8 @@ def main() -> int:
             return False
 
     if leg(out, "wire", bench_wire):
-        log(f"wire 8192x4096: pack {out['wire']['pack_gbs']} GB/s, unpack {out['wire']['unpack_gbs']} GB/s")
+        log(f"wire 8192x4096: pack {out['wire']['pack_gbs']} GB/s, unpack {out['wire']['unpack_gbs']} GB/s; "
+            f"AXSBlock records {out['wire']['axs_blocks']}")
     if leg(out, "configs", bench_configs):
         log(f"configs: {out['configs']}")
     if leg(out, "codec", bench_codec):

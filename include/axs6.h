@@ -124,6 +124,39 @@ int axs6_nf5_wire_from_codes(const uint8_t* exponents, const uint8_t* codes, con
 int axs6_nf5_wire_to_codes(const uint8_t* buffer, int64_t rows, int64_t nblk, int32_t block_size,
                            uint8_t* exponents, uint8_t* codes, uint8_t* signs, void* stream);
 
+/* ---- AXSBlock byte form ------------------------------------------------------
+ * The concatenation of AXSBlock.to_bytes() over a tensor's blocks (blocks in
+ * row-major order, the last block of a row zero-padded): per block a 2-byte
+ * little-endian header e << 2 | config (config written as DENSE = 0 and
+ * ignored when decoding; bits 10..15 zero), then the 6-bit codes as above,
+ * four per three bytes, low bits first.  A 32-value block takes 26 bytes.
+ * The same kernels as the wire format with the wider header. */
+
+/* Bytes of the block stream of a rows x cols tensor (-1 on bad arguments). */
+int64_t axs6_nf5_block_bytes(int64_t rows, int64_t cols, int32_t block_size);
+
+/* Quantize x [rows, cols] (nearest rounding) straight into AXSBlock records.
+ * Replaces: quantize_unified then AXSBlock(...).to_bytes() per block
+ *           (axs/unified/quantize_unified.py:211-282, axs/core.py:97-119). */
+int axs6_nf5_pack_blocks(const void* x, int32_t dtype, int64_t rows, int64_t cols, int32_t block_size,
+                         uint8_t* buffer, void* stream);
+
+/* AXSBlock records -> y [rows, cols] f32: +-codebook[code] * 2^(e-127).
+ * Replaces: AXSBlock.from_bytes per block then dequantize_unified
+ *           (axs/core.py:121-152, axs/unified/quantize_unified.py:285-308). */
+int axs6_nf5_unpack_blocks(const uint8_t* buffer, int64_t rows, int64_t cols, int32_t block_size, float* y,
+                           void* stream);
+
+/* AXSTensor components -> AXSBlock records (signs may be NULL).
+ * Replaces: AXSBlock(...).to_bytes() per block (axs/core.py:97-119). */
+int axs6_nf5_blocks_from_codes(const uint8_t* exponents, const uint8_t* codes, const uint8_t* signs,
+                               int64_t rows, int64_t nblk, int32_t block_size, uint8_t* buffer, void* stream);
+
+/* AXSBlock records -> AXSTensor components (signs may be NULL).
+ * Replaces: AXSBlock.from_bytes per block (axs/core.py:121-152). */
+int axs6_nf5_blocks_to_codes(const uint8_t* buffer, int64_t rows, int64_t nblk, int32_t block_size,
+                             uint8_t* exponents, uint8_t* codes, uint8_t* signs, void* stream);
+
 /* ---- quantized linear ------------------------------------------------------
  * The linear contracts NF5 fake-quantized operands on fp16 MFMA.  Operands are
  * packed as fp16 rows scaled by an exact power of two (2^-shift per row, so

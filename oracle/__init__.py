@@ -11,6 +11,8 @@ Contents:
     (``axs/unified/quantize_unified.py:50-308``), wrapped below for numpy.
   * :func:`wire_pack` / :func:`wire_unpack`: the reference's 6.25-bit gradient
     buffer layout (``axs/unified/distributed.py:147-232``).
+  * :func:`block_pack` / :func:`block_unpack`: the concatenated
+    ``AXSBlock.to_bytes`` / ``from_bytes`` records (``axs/core.py:97-152``).
   * :func:`linear_reference`: the fp64 product of fake-quantized operands
     that the quantized-linear kernels are compared to
     (``axs/unified/functional_unified.py:107-170``).
@@ -172,6 +174,41 @@ def wire_unpack(buf: np.ndarray, rows: int, nblk: int, bs: int):
     c3 = (b2 >> 2) & 0x3F
     q = np.stack([c0, c1, c2, c3], axis=-1).reshape(rows, nblk, bs)
     return exps, (q & 0x1F).astype(np.uint8), ((q >> 5) & 1).astype(bool)
+
+
+def block_pack(exps: np.ndarray, codes: np.ndarray, signs: np.ndarray,
+               configs: np.ndarray | None = None) -> np.ndarray:
+    """AXSBlock.to_bytes (axs/core.py:97-119) of every block, concatenated:
+    the 2-byte little-endian header ``e << 2 | config`` then the 6-bit values
+    ``sign << 5 | code`` emitted low bit first (the reference's bit
+    accumulator, here as unpackbits/packbits in little bit order) and padded
+    to whole bytes.  uint8 [R * nblk * (2 + ceil(6 bs / 8))]."""
+    R, nblk, bs = codes.shape
+    q = (codes.astype(np.uint8) & 0x1F) | (np.asarray(signs).astype(np.uint8) << 5)
+    bits = np.unpackbits(q.reshape(R, nblk, bs, 1), axis=-1, bitorder="little")[..., :6]
+    bits = bits.reshape(R, nblk, bs * 6)
+    pad = (-bits.shape[-1]) % 8
+    if pad:
+        bits = np.concatenate([bits, np.zeros((R, nblk, pad), np.uint8)], axis=-1)
+    payload = np.packbits(bits, axis=-1, bitorder="little")
+    cfg = np.zeros((R, nblk), np.int64) if configs is None else np.asarray(configs, np.int64)
+    header = (np.asarray(exps, np.int64) << 2) | cfg
+    out = np.empty((R, nblk, 2 + payload.shape[-1]), np.uint8)
+    out[:, :, 0] = header & 0xFF
+    out[:, :, 1] = header >> 8
+    out[:, :, 2:] = payload
+    return out.reshape(-1)
+
+
+def block_unpack(buf: np.ndarray, rows: int, nblk: int, bs: int):
+    """AXSBlock.from_bytes (axs/core.py:121-152) of every record:
+    (exps, codes, signs, configs), exps = header >> 2."""
+    nb = (6 * bs + 7) // 8
+    b = np.asarray(buf).view(np.uint8).reshape(rows, nblk, 2 + nb)
+    header = b[:, :, 0].astype(np.int64) | (b[:, :, 1].astype(np.int64) << 8)
+    bits = np.unpackbits(b[:, :, 2:], axis=-1, bitorder="little")[..., :6 * bs]
+    q = np.packbits(bits.reshape(rows, nblk, bs, 6), axis=-1, bitorder="little")[..., 0]
+    return header >> 2, (q & 0x1F).astype(np.uint8), ((q >> 5) & 1).astype(bool), (header & 3).astype(np.uint8)
 
 
 def linear_reference(xq: np.ndarray, wq: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
