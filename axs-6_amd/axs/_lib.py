@@ -1,8 +1,10 @@
-"""ctypes binding of libaxs6.so (C ABI declared in include/axs6.h).
+"""ctypes binding of libaxs6.so (C ABI declared in include/axs6.h), and the
+loader of the torch extension ``axs._C`` built over the same C ABI.
 
 The library is built in-tree by ``python axs-6_amd/build.py`` into
-``axs-6_amd/axs/_lib/libaxs6.so``.  There is no fallback: if the library is
-missing or fails to load, every entry point raises.
+``axs-6_amd/axs/_lib/libaxs6.so`` (the extension into ``axs-6_amd/axs/_C.so``).
+There is no fallback: if either is missing or fails to load, every entry
+point that needs it raises.
 
 torch is imported first so that the HIP runtime torch ships
 (libamdhip64.so.7) is the one the library binds to; device pointers and
@@ -99,6 +101,31 @@ def lib() -> ctypes.CDLL:
                     fn.restype = _RESTYPES.get(name, ctypes.c_int)
             _lib = L
     return _lib
+
+
+_ext = None
+EXT_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_C.so")
+
+
+def ext():
+    """The torch extension ``axs._C`` (the linear's host logic and autograd
+    node in C++), loaded after libaxs6.so so both share the one library."""
+    global _ext
+    if _ext is not None:
+        return _ext
+    lib()
+    with _lock:
+        if _ext is None:
+            if not os.path.exists(EXT_PATH):
+                raise LibraryError(
+                    f"torch extension not found at {EXT_PATH}; build it with "
+                    "`python axs-6_amd/build.py`")
+            try:
+                from axs import _C
+            except ImportError as e:  # pragma: no cover - environment problem
+                raise LibraryError(f"failed to load {EXT_PATH}: {e}") from e
+            _ext = _C
+    return _ext
 
 
 def has(name: str) -> bool:

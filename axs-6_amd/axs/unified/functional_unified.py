@@ -78,8 +78,11 @@ def axs_linear_unified(
     quantize_input: bool = True,
     quantize_grad: bool = True,
 ) -> torch.Tensor:
-    """AXS-6 quantized linear: ``input (*, in) -> (*, out)``."""
-    return _AXSLinearUnifiedFunction.apply(input, weight, bias, block_size, quantize_input, quantize_grad)
+    """AXS-6 quantized linear: ``input (*, in) -> (*, out)``.  Runs as one C++
+    autograd node (the same forward and backward as
+    ``_AXSLinearUnifiedFunction``, whose Python class is kept for callers
+    that use it directly)."""
+    return hip_linear.linear_autograd(input, weight, bias, block_size, quantize_input, quantize_grad)
 
 
 def axs_matmul_unified(

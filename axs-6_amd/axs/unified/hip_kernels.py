@@ -80,15 +80,13 @@ _graph_counters: dict[int, torch.Tensor] = {}
 
 
 def _graph_counter(device: torch.device) -> torch.Tensor:
+    """The device's counter, shared with the linear's C++ backward (which
+    keeps the registry: axs._C.graph_counter); created on first use, which
+    raises while the current stream records a graph."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     ctr = _graph_counters.get(idx)
     if ctr is None:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError(
-                "a stochastic AXS-6 call is being recorded in a HIP graph before any stochastic call ran "
-                "eagerly on this device; run one warm-up step before capture (or call "
-                "axs.unified.hip_kernels.prepare_graph_capture())")
-        ctr = torch.zeros(1, dtype=torch.int64, device=torch.device("cuda", idx))
+        ctr = _lib.ext().graph_counter(idx)
         _graph_counters[idx] = ctr
     return ctr
 

@@ -10,6 +10,11 @@ rows (see include/axs6.h); results are float32-accumulated and land within
 rel-L2 ~3e-4 of the fp32 product of the fake-quantized operands.
 Ragged K or N (not a multiple of the block size) are zero-padded on the
 device first -- NF5 pads the last block with zeros, so this changes nothing.
+
+The training forward and backward (shape handling, allocation, the dither
+seed and the library calls) live in the torch extension ``axs._C``
+(csrc/torch_ext.cpp); ``linear_autograd`` is the same pair as one C++
+autograd node, which ``axs_linear_unified`` uses.
 """
 from __future__ import annotations
 
@@ -20,7 +25,7 @@ import torch.nn.functional as F
 
 from axs import _lib
 from axs.core import VALID_BLOCK_SIZES
-from axs.unified.hip_kernels import _on_device, _require_device, stochastic_seed
+from axs.unified.hip_kernels import _on_device, _require_device
 
 _SUPPORTED = (torch.float32, torch.bfloat16, torch.float16)
 
@@ -36,11 +41,6 @@ def padded_k(k: int) -> int:
 def _pad_last(t: torch.Tensor, mult: int) -> torch.Tensor:
     pad = (-t.shape[-1]) % mult
     return F.pad(t, (0, pad)) if pad else t
-
-
-def _pad_rows(t: torch.Tensor, mult: int) -> torch.Tensor:
-    pad = (-t.shape[0]) % mult
-    return F.pad(t, (0, 0, 0, pad)) if pad else t
 
 
 def _rows(t: torch.Tensor, cols: int) -> torch.Tensor:
@@ -77,48 +77,15 @@ class Saved:
 
 
 def _forward(input, weight, bias, block_size, quantize_input):
+    """(Y, Saved) through the extension's forward (axs._C.linear_fwd: shape
+    handling, allocation and the axs6_nf5_linear_forward call in C++)."""
     fn = "axs_linear"
     _require_device(input, fn)
     _require_device(weight, fn)
     assert block_size in VALID_BLOCK_SIZES, f"block_size must be one of {VALID_BLOCK_SIZES}"
-    K = input.shape[-1]
-    N, Kw = weight.shape
-    if Kw != K:
-        raise RuntimeError(f"{fn}: input has {K} features but weight expects {Kw}")
-    dtype = input.dtype if input.dtype in _SUPPORTED else torch.float32
-    x2 = _rows(input, K).to(dtype)
-    w2 = weight.to(dtype)
-    k_true, n_true = K, N
-    x2 = _dense(_pad_last(x2, block_size))
-    w2 = _dense(_pad_rows(_pad_last(w2, block_size), block_size))
-    M, Kb = x2.shape
-    Nb = w2.shape[0]
-    b = None
-    if bias is not None:
-        b = bias.to(torch.float32)
-        if Nb != N:
-            b = F.pad(b, (0, Nb - N))
-        b = b.contiguous()
-    Kp = padded_k(Kb)
-    dev = x2.device
-    xq = torch.empty((M, Kp), dtype=torch.float16, device=dev)
-    wq = torch.empty((Nb, Kp), dtype=torch.float16, device=dev)
-    sx = torch.empty((M,), dtype=torch.int32, device=dev)
-    sw = torch.empty((Nb,), dtype=torch.int32, device=dev)
-    y = torch.empty((M, Nb), dtype=dtype, device=dev)
-    if M and Nb and not Kb:
-        # an empty contraction: F.linear gives the bias (or zeros)
-        y.copy_(b.to(dtype).expand(M, Nb) if b is not None else torch.zeros((), dtype=dtype, device=dev).expand(M, Nb))
-    elif M and Nb:
-        with _on_device(x2):
-            _lib.call("axs6_nf5_linear_forward", x2.data_ptr(), w2.data_ptr(), _lib.ptr(b), y.data_ptr(),
-                      _lib.DTYPE_CODE[dtype], M, Nb, Kb, block_size, int(bool(quantize_input)),
-                      xq.data_ptr(), sx.data_ptr(), wq.data_ptr(), sw.data_ptr(), _lib.stream_of(x2))
-    if Nb != N:
-        y = y[:, :N]
-    out = y.reshape(*input.shape[:-1], N)
-    saved = Saved(xq, sx, wq, sw, M, Nb, Kb, n_true, k_true, dtype, tuple(input.shape), weight.dtype)
-    return out, saved
+    out, xq, sx, wq, sw, M, N, K, n_true, k_true, dtype = _lib.ext().linear_fwd(
+        input, weight, bias, block_size, bool(quantize_input))
+    return out, Saved(xq, sx, wq, sw, M, N, K, n_true, k_true, dtype, tuple(input.shape), weight.dtype)
 
 
 def forward_train(input, weight, bias, block_size=32, quantize_input=True):
@@ -175,47 +142,25 @@ def linear_forward(input, weight, bias=None, block_size=32, quantize_input=True)
 
 def backward(grad_output, saved: Saved, block_size: int, quantize_grad: bool,
              need_x: bool, need_w: bool, need_b: bool, seed: int | None = None):
-    """(dX, dW, db) of the quantized linear, each None when not needed.
-    ``seed`` fixes the stochastic rounding of dY (default: a fresh draw)."""
-    M, N, K = saved.M, saved.N, saved.K
-    dev = saved.xq.device
-    dy = _rows(grad_output, saved.n_true).to(saved.dtype)
-    if N != saved.n_true:
-        dy = _pad_last(dy, block_size)
-    dy = _dense(dy)
-    dx = torch.empty((M, K), dtype=saved.dtype, device=dev) if need_x else None
-    dw = torch.empty((N, K), dtype=torch.float32, device=dev) if need_w else None
-    db = torch.empty((N,), dtype=torch.float32, device=dev) if need_b else None
-    if M and N and (need_x or need_w or need_b):
-        L = _lib_sigs()
-        ws_bytes = int(L.axs6_nf5_linear_backward_workspace(M, N, K, int(need_x), int(need_w), int(need_b)))
-        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
-        s, sdev, ctr = stochastic_seed(dev, seed) if quantize_grad else (0, None, None)
-        with _on_device(dy):
-            _lib.call("axs6_nf5_linear_backward", dy.data_ptr(), _lib.DTYPE_CODE[saved.dtype], M, N, K,
-                      block_size, int(bool(quantize_grad)), s, 0,
-                      saved.xq.data_ptr(), saved.sx.data_ptr(), saved.wq.data_ptr(), saved.sw.data_ptr(),
-                      _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), ws.data_ptr(), ws_bytes, sdev,
-                      _lib.stream_of(dy))
-            if ctr is not None:
-                ctr.add_(1)
-    else:
-        # no rows (M == 0): the reference's dYq^T X and sum over rows give zeros
-        if dw is not None:
-            dw.zero_()
-        if db is not None:
-            db.zero_()
-    if dx is not None:
-        if K != saved.k_true:
-            dx = dx[:, :saved.k_true]
-        dx = dx.reshape(*saved.x_shape[:-1], saved.k_true)
-    if dw is not None:
-        dw = dw[:saved.n_true, :saved.k_true]
-        if saved.w_dtype != torch.float32:
-            dw = dw.to(saved.w_dtype)
-    if db is not None:
-        db = db[:saved.n_true]
-    return dx, dw, db
+    """(dX, dW, db) of the quantized linear, each None when not needed, through
+    the extension's backward (axs._C.linear_bwd).  ``seed`` fixes the
+    stochastic rounding of dY (default: a fresh draw from torch's CPU
+    generator; while a graph is recorded, plus the device's replay counter)."""
+    return _lib.ext().linear_bwd(
+        grad_output, saved.xq, saved.sx, saved.wq, saved.sw, saved.M, saved.N, saved.K, saved.n_true,
+        saved.k_true, saved.dtype, list(saved.x_shape), saved.w_dtype, block_size, bool(quantize_grad),
+        bool(need_x), bool(need_w), bool(need_b), seed)
+
+
+def linear_autograd(input, weight, bias, block_size=32, quantize_input=True, quantize_grad=True):
+    """``axs_linear_unified`` as one C++ autograd node (axs._C.linear): the
+    same forward and backward as forward_train / backward, with no Python on
+    either side of the engine."""
+    fn = "axs_linear"
+    _require_device(input, fn)
+    _require_device(weight, fn)
+    assert block_size in VALID_BLOCK_SIZES, f"block_size must be one of {VALID_BLOCK_SIZES}"
+    return _lib.ext().linear(input, weight, bias, block_size, bool(quantize_input), bool(quantize_grad))
 
 
 def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
