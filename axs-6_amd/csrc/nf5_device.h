@@ -112,24 +112,46 @@ template <> struct Elem<AXS6_F16> {
 
 // ---- block arithmetic ------------------------------------------------------
 
+// v and the value DPP control `ctrl` brings to this lane, unsigned max.  Every
+// control used here reads a lane inside the same row, so bound_ctrl (zero for
+// lanes without a source) never applies; written this way (old value 0, the
+// identity of the max) the compiler fuses the move into one v_max_u32_dpp.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_umax(uint32_t v) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+    return v > o ? v : o;
+}
+
 // Unsigned max across a group of G neighbouring lanes (G in {1,2,4,8}) with
 // DPP: quad_perm [1,0,3,2], quad_perm [2,3,0,1], then row_half_mirror pairs
 // each quad with the other quad of its 8-lane half-row.
 template <int G>
 __device__ __forceinline__ uint32_t group_umax(uint32_t v) {
-    if constexpr (G >= 2) {
-        uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false);
-        v = v > o ? v : o;
-    }
-    if constexpr (G >= 4) {
-        uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false);
-        v = v > o ? v : o;
-    }
-    if constexpr (G >= 8) {
-        uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false);
-        v = v > o ? v : o;
-    }
+    if constexpr (G >= 2) v = dpp_umax<0xB1>(v);
+    if constexpr (G >= 4) v = dpp_umax<0x4E>(v);
+    if constexpr (G >= 8) v = dpp_umax<0x141>(v);
     return v;
+}
+
+// Unsigned max over the whole wave, returned in every lane (a scalar): an
+// inclusive max-scan over each row of 16 lanes (row_shr 1, 2, 4, 8; lanes
+// without a source read 0), rows folded with row_bcast:15 and row_bcast:31,
+// then lane 63 read out.
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+    v = dpp_umax<0x111>(v);
+    v = dpp_umax<0x112>(v);
+    v = dpp_umax<0x114>(v);
+    v = dpp_umax<0x118>(v);
+    uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);
+    v = v > o ? v : o;
+    o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);
+    v = v > o ? v : o;
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Signed max over the whole wave (same reduction, signed order).
+__device__ __forceinline__ int wave_imax(int v) {
+    return (int)(wave_umax((uint32_t)v ^ 0x80000000u) ^ 0x80000000u);
 }
 
 // Same reduction for groups of up to 32 lanes through cross-lane shuffles
@@ -163,24 +185,30 @@ __device__ __forceinline__ float pow2_float(int e) {
 }
 
 // The per-block scale of fused_fake_quantize (quantize_unified.py:172-179).
+// The scale itself (torch's `scales` entry: 2^e1, 1 for a zero block, inf,
+// NaN) is only formed on the general path (scale_of); the short sequences
+// use e1.
 struct FqScale {
-    float scale;    // torch's `scales` entry: 2^e1, 1 (zero block), inf, NaN
-    int e1;         // exponent used to normalise when scale is finite
+    int e1;         // exponent used to normalise when scale is finite (0 for a zero block)
     bool inf_scale;
     bool nan_block;
+    bool zero;
 };
 
 __device__ __forceinline__ FqScale fq_scale(uint32_t amax, const uint8_t* band) {
     FqScale s;
     s.nan_block = amax > kInfBits;
-    bool zero = amax == 0u;
+    s.zero = amax == 0u;
     bool inf_amax = amax == kInfBits;
-    int e1 = (zero || amax >= kInfBits) ? 0 : floor_log2_torch(amax, band) + 1;
+    int e1 = (s.zero || amax >= kInfBits) ? 0 : floor_log2_torch(amax, band) + 1;
     s.inf_scale = inf_amax || e1 >= 128;
     s.e1 = s.inf_scale ? 0 : e1;
-    s.scale = s.nan_block ? __uint_as_float(kNanBits)
-                          : (s.inf_scale ? __uint_as_float(kInfBits) : (zero ? 1.0f : pow2_float(e1)));
     return s;
+}
+
+__device__ __forceinline__ float scale_of(const FqScale& s) {
+    return s.nan_block ? __uint_as_float(kNanBits)
+                       : (s.inf_scale ? __uint_as_float(kInfBits) : (s.zero ? 1.0f : pow2_float(s.e1)));
 }
 
 // |x| / scale exactly, for power-of-two scales.
@@ -205,37 +233,49 @@ __device__ __forceinline__ float fq_value(float x, const FqScale& s, const float
     uint32_t ab = __float_as_uint(x) & 0x7fffffffu;
     float n = normalise(ab, s);
     float rec = lut[lut_index(n, stochastic, d)];
-    float r = (torch_sign(x) * rec) * s.scale;
+    float r = (torch_sign(x) * rec) * scale_of(s);
     return s.nan_block ? __uint_as_float(kNanBits) : r;
 }
 
+// Lowest block exponent e1 of the short FQ sequences below: from it up to 127
+// the factor 1023 * 2^-e1 is a finite normal float and lut * 2^e1 is normal.
+constexpr int kFastMinE1 = -100;
+
+// |x| * 1023 * 2^-e1 as the reference computes it, (|x| * 2^-e1) * 1023,
+// for e1 >= kFastMinE1, as one product with c = 1023 * 2^-e1 (exact): when
+// |x| * 2^-e1 is a normal float it is exact, so both are the one rounding of
+// the same real number; when it is subnormal both are below 1023 * 2^-126
+// and truncate to the same index 0.
+__device__ __forceinline__ float lut_pos(uint32_t abits, float c) { return __uint_as_float(abits) * c; }
+
 // fused_fake_quantize of the V elements of one 16-byte vector whose block
 // scale is s; d[e] is element e's dither (U - 0.5) / 1023 (unused in nearest
-// mode).  Blocks with a NaN or an infinite scale take the per-element general
-// path (fq_value).  When no lane of the wave holds such a block -- the normal
-// case, tested with one ballot so the branch is uniform -- a shorter sequence
-// gives the same bits: the scale 2^e1 exceeds every |x| of the block, so
-// n = |x| 2^-e1 < 1 is finite, (n + d) * 1023 lies in (-0.51, 1023.5) and
-// truncates into [0, 1023], and (sign(x) * lut) * scale equals lut * scale
-// with x's sign bit (rounding to nearest is symmetric), or +0 where x is +-0
-// (torch.sign(-0.0) is +0).
+// mode).  Blocks with a NaN or an infinite scale, or an exponent below
+// kFastMinE1, take the per-element general path (fq_value).  When no lane of
+// the wave holds such a block -- the normal case, tested with one ballot so
+// the branch is uniform -- a shorter sequence gives the same bits: the scale
+// 2^e1 exceeds every |x| of the block, so n = |x| 2^-e1 < 1 is finite,
+// n * 1023 lies in [0, 1023) and (n + d) * 1023 in (-0.51, 1023.5), so the
+// truncated index is in [0, 1023] without a clamp, and (sign(x) * lut) * scale
+// equals lut * scale with x's sign bit (rounding to nearest is symmetric), or
+// +0 where x is +-0 (torch.sign(-0.0) is +0).
 template <int V>
 __device__ __forceinline__ void fq_vector(float (&f)[V], const FqScale& s, const float* lut, bool stochastic,
                                           const float (&d)[V]) {
-    const bool special = s.nan_block || s.inf_scale;
+    const bool special = s.nan_block || s.inf_scale || s.e1 < kFastMinE1;
     if (__builtin_amdgcn_ballot_w64(special) != 0) {
 #pragma unroll
         for (int e = 0; e < V; ++e) f[e] = fq_value(f[e], s, lut, stochastic, d[e]);
     } else {
+        const float c = __builtin_amdgcn_ldexpf(1023.0f, -s.e1);
 #pragma unroll
         for (int e = 0; e < V; ++e) {
             const uint32_t xb = __float_as_uint(f[e]);
             const uint32_t ab = xb & 0x7fffffffu;
-            const float n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -s.e1);
-            const float t = stochastic ? (n + d[e]) * 1023.0f : n * 1023.0f;
-            int i = (int)t;
-            i = i < 0 ? 0 : (i > kLutMax ? kLutMax : i);   // in range already; keeps the LDS index bounded
-            const float mag = lut[i] * s.scale;
+            float t;
+            if (stochastic) t = (__builtin_amdgcn_ldexpf(__uint_as_float(ab), -s.e1) + d[e]) * 1023.0f;
+            else t = lut_pos(ab, c);
+            const float mag = __builtin_amdgcn_ldexpf(lut[(int)t], s.e1);   // lut * 2^e1, exact (normal)
             // +0 where x is +-0, else mag with x's sign -- as a mask, not a
             // select, so the compiler does not branch around the LUT read per
             // element: (ab + 0x7fffffff) has bit 31 set exactly when ab != 0
@@ -243,6 +283,36 @@ __device__ __forceinline__ void fq_vector(float (&f)[V], const FqScale& s, const
             f[e] = __uint_as_float((__float_as_uint(mag) ^ (xb & 0x80000000u)) & nz);
         }
     }
+}
+
+// Nearest-mode FQ of one 16-byte vector without the block scale, for callers
+// that fold 2^e1 into a power-of-two scaling of their own: f[e] becomes
+// +-lut_fast[i] (+0 where x is +-0), with i the index fq_vector computes.
+// lut_fast is the LUT, or the LUT rounded to the input type when the caller
+// must round FQ values to it (rounding commutes with 2^e1 while lut * 2^e1
+// is normal, which e1 >= kFastMinE1 guarantees).  When any lane of the wave
+// holds a block the fast sequence does not cover, every lane writes its full
+// FQ values instead (fq_value, from the unrounded lut) and the call returns
+// true -- wave-uniform, so the caller's branch on it is too.
+template <int V>
+__device__ __forceinline__ bool fq_vector_unscaled(float (&f)[V], const FqScale& s, const float* lut,
+                                                   const float* lut_fast) {
+    const bool special = s.nan_block || s.inf_scale || s.e1 < kFastMinE1;
+    if (__builtin_amdgcn_ballot_w64(special) != 0) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) f[e] = fq_value(f[e], s, lut, false, 0.0f);
+        return true;
+    }
+    const float c = __builtin_amdgcn_ldexpf(1023.0f, -s.e1);
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+        const uint32_t xb = __float_as_uint(f[e]);
+        const uint32_t ab = xb & 0x7fffffffu;
+        const float mag = lut_fast[(int)lut_pos(ab, c)];
+        const uint32_t nz = (uint32_t)((int32_t)(ab + 0x7fffffffu) >> 31);
+        f[e] = __uint_as_float((__float_as_uint(mag) ^ (xb & 0x80000000u)) & nz);
+    }
+    return false;
 }
 
 // FQ values rounded to the element type's precision, as the reference's

@@ -51,15 +51,9 @@ enum PackMode { kRaw = 0, kNearest = 1, kStochastic = 2 };
 
 // Unsigned max over groups of g neighbouring lanes (g uniform at runtime).
 __device__ __forceinline__ uint32_t group_umax_rt(uint32_t v, int g) {
-    if (g >= 2) v = group_umax<2>(v) ;
-    if (g >= 4) {
-        uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false);
-        v = v > o ? v : o;
-    }
-    if (g >= 8) {
-        uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false);
-        v = v > o ? v : o;
-    }
+    if (g >= 2) v = dpp_umax<0xB1>(v);
+    if (g >= 4) v = dpp_umax<0x4E>(v);
+    if (g >= 8) v = dpp_umax<0x141>(v);
     return v;
 }
 
@@ -71,14 +65,7 @@ __device__ __forceinline__ uint32_t group_umax_shfl_rt(uint32_t v, int bs) {
     return v;
 }
 
-__device__ __forceinline__ int wave_max_i32(int v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        int o = __shfl_xor(v, off, 64);
-        v = v > o ? v : o;
-    }
-    return v;
-}
+__device__ __forceinline__ int wave_max_i32(int v) { return wave_imax(v); }
 
 template <int V>
 __device__ __forceinline__ void store_f16(_Float16* p, const float* v, int sh_base, const int* sh_col) {
@@ -100,6 +87,24 @@ __device__ __forceinline__ void store_f16(_Float16* p, const float* v, int sh_ba
     }
 }
 
+// fp16 of v[e] * factor (factor a power of two), V halves stored as one vector.
+template <int V>
+__device__ __forceinline__ void store_f16_mul(_Float16* p, const float* v, float factor) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    uint32_t w[V / 2];
+#pragma unroll
+    for (int i = 0; i < V / 2; ++i) {
+        const f32x2 x = {v[2 * i] * factor, v[2 * i + 1] * factor};
+        w[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, f16x2));
+    }
+    if constexpr (V == 8) {
+        *reinterpret_cast<u32x4*>(p) = u32x4{w[0], w[1], w[2], w[3]};
+    } else {
+        *reinterpret_cast<u32x2*>(p) = u32x2{w[0], w[1]};
+    }
+}
+
 struct PackRowsK {
     const void* x; int64_t rows; int64_t cols; int block;
     uint64_t seed; const uint64_t* seed_dev; uint64_t offset;   // dither seed (+ *seed_dev when set)
@@ -118,6 +123,18 @@ struct PackRowsK {
 // reductions need no barrier, so short rows run several to a workgroup
 // (RPW > 1 requires NT == 64).  The LUT and band table are staged once per
 // workgroup (NT * RPW >= 256 threads).
+//
+// The row index is wave-uniform (taken from the block index, or read from the
+// first lane), so row addresses and the choice between k and k2 are scalar.
+//
+// DEFER (nearest FQ without column exponents, f32 or bf16 input -- the
+// forward's packing): the FQ leaves +-lut[i] per element and the block
+// exponent e1 per vector (fq_vector_unscaled), and the store multiplies by
+// 2^(e1 - S_row) -- the block scale and the row shift in one exact product
+// instead of a product and an ldexp.  For bf16 input the LUT is read rounded
+// to bf16 (the reference's FQ output rounding, which commutes with 2^e1 on
+// this path).  Vectors whose wave met a special block keep full FQ values
+// and the ldexp store.
 template <int DT, int MODE, bool COLX, int NV, int NT, int RPW>
 __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRowsK k2, int64_t total) {
     using E = Elem<DT>;
@@ -125,30 +142,34 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
     constexpr int V = E::V;
     constexpr int NW = NT / 64;
     constexpr bool WAVE_ROW = NT == 64;
+    constexpr bool DEFER = MODE == kNearest && !COLX && DT != AXS6_F16;
+    constexpr bool ROUNDED_LUT = DEFER && DT == AXS6_BF16;
     static_assert(RPW == 1 || WAVE_ROW, "several rows per workgroup need one wave per row");
     static_assert(NT * RPW >= kLutSize / 4 && NT * RPW >= kBandSize / 4, "table staging takes one thread per word");
     __shared__ float lut_s[kLutSize];
+    __shared__ float lutr_s[ROUNDED_LUT ? kLutSize : 1];
     __shared__ uint32_t band_w[kBandSize / 4];
     __shared__ int red[2][2][NW];         // [row parity][tmax, rmax][wave]
     const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
     const int tid = threadIdx.x % NT;     // thread within the row group
-    stage_tables(lut_s, band_w, k.lut, k.band);
-
-    auto load_row = [&](int64_t RR, u32x4 (&dst)[NV]) {
-        const bool sec = RR >= k.rows;
-        const int64_t cols = sec ? k2.cols : k.cols;
-        const S* xr = reinterpret_cast<const S*>(sec ? k2.x : k.x) + (sec ? RR - k.rows : RR) * cols;
-        const int64_t nv = cols / V;
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const int64_t vi = tid + (int64_t)NT * j;
-            dst[j] = vi < nv ? *(reinterpret_cast<const u32x4*>(xr) + vi) : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (ROUNDED_LUT) {
+        if (threadIdx.x < kLutSize / 4) {
+            const float4 v = reinterpret_cast<const float4*>(k.lut)[threadIdx.x];
+            float4 r;
+            r.x = Elem<AXS6_BF16>::to_f(f32_to_bf16_rne(v.x)); r.y = Elem<AXS6_BF16>::to_f(f32_to_bf16_rne(v.y));
+            r.z = Elem<AXS6_BF16>::to_f(f32_to_bf16_rne(v.z)); r.w = Elem<AXS6_BF16>::to_f(f32_to_bf16_rne(v.w));
+            reinterpret_cast<float4*>(lutr_s)[threadIdx.x] = r;
         }
-    };
+    }
+    stage_tables(lut_s, band_w, k.lut, k.band);
+    const float* lut_fast = ROUNDED_LUT ? lutr_s : lut_s;
+
+    // wave-uniform row group index within the workgroup
+    const int64_t g0 = RPW == 1 ? 0 : (int64_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x / NT));
     const int64_t stride = (int64_t)gridDim.x * RPW;
 
     int parity = 0;
-    for (int64_t R = (int64_t)blockIdx.x * RPW + threadIdx.x / NT; R < total; R += stride, parity ^= 1) {
+    for (int64_t R = (int64_t)blockIdx.x * RPW + g0; R < total; R += stride, parity ^= 1) {
         const bool second = R >= k.rows;
         const PackRowsK q = second ? k2 : k;      // by value: field-wise selects, no stack copy
         const uint64_t key = MODE == kStochastic ? dither_key(q.seed + (q.seed_dev ? *q.seed_dev : 0ull)) : 0ull;
@@ -159,9 +180,13 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
 
         float f[NV][V];
         int cx[NV][V];
+        int e1v[NV];          // DEFER: the vector's block exponent, or INT_MIN when f holds full FQ values
         u32x4 raw[NV];
-        load_row(R, raw);
-        (void)xr;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int64_t vi = tid + (int64_t)NT * j;
+            raw[j] = vi < nvec ? *(reinterpret_cast<const u32x4*>(xr) + vi) : u32x4{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int64_t vi = tid + (int64_t)NT * j;
@@ -189,7 +214,11 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
             }
             m = group_umax_rt(m, g);
             const FqScale s = fq_scale(m, band_s);
-            if constexpr (MODE != kRaw) {
+            if constexpr (DEFER) {
+                const bool full = fq_vector_unscaled<V>(f[j], s, lut_s, lut_fast);
+                if (full) round_to_elem<DT>(f[j]);
+                e1v[j] = full ? INT_MIN : s.e1;
+            } else if constexpr (MODE != kRaw) {
                 const DitherVec dv = dither_vec(key, q.offset + (uint64_t)(r * q.cols + vi * V));
                 float d[V];
 #pragma unroll
@@ -215,7 +244,7 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
         // row max of (tmax, rmax); across waves, the parity buffer lets the
         // next row's writes proceed while slower waves still read this row's
         tmax = wave_max_i32(tmax);
-        rmax = wave_max_i32(rmax);
+        rmax = COLX ? wave_max_i32(rmax) : tmax;
         if constexpr (!WAVE_ROW) {
             if ((tid & 63) == 0) { red[parity][0][tid >> 6] = tmax; red[parity][1][tid >> 6] = rmax; }
             __syncthreads();
@@ -233,7 +262,16 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
                 const int64_t vi = tid + (int64_t)NT * j;
-                if (vi < nvec) store_f16<V>(orow + vi * V, f[j], -S_row, COLX ? cx[j] : nullptr);
+                if (vi < nvec) {
+                    if constexpr (DEFER) {
+                        // e1v[j] <= row max, so 2^(e1 - S_row) <= 2^15: finite; below 2^-149 it is 0,
+                        // as is the fp16 value of anything that small
+                        if (e1v[j] != INT_MIN) store_f16_mul<V>(orow + vi * V, f[j], __builtin_amdgcn_ldexpf(1.0f, e1v[j] - S_row));
+                        else store_f16<V>(orow + vi * V, f[j], -S_row, nullptr);
+                    } else {
+                        store_f16<V>(orow + vi * V, f[j], -S_row, COLX ? cx[j] : nullptr);
+                    }
+                }
             }
             const int64_t zvec = (q.cols_pad - q.cols) / 8;   // 8-half zero chunks
             for (int64_t z = tid; z < zvec; z += NT)
@@ -776,18 +814,17 @@ inline RowsShape rows_shape(int64_t nvec) {
     if (nvec <= 64) return {64, 1};
     if (nvec <= 128) return {64, 2};
     if (nvec <= 256) return {64, 4};
-    // 257-512 vectors still one wave per row, 8 vectors per lane: 4-13%
-    // shorter than 256 threads x 2 (16384 rows of 1536-2048 f32 or
-    // 2560-4096 bf16 columns)
-    if (nvec <= 512) return {64, 8};
+    // one row per workgroup from here.  Measured with the forward's nearest
+    // pack (graph-free event timing, 2048-16384 rows): 257-512 vectors
+    // 256 x 2 beats one wave of 8 vectors by 0-24% (bf16 4096 columns 14.7
+    // against 19.4 us); 513-1024 256 x 4; 1025-1536 768 x 2 beats 256 x 8 by
+    // 8-15% (f32 6144 and bf16 11008-12288 columns); 1537-2048 512 x 4 beats
+    // it by 6-10%; 2049-3072 768 x 4 (1024 x 4 and 512 x 8 slower); beyond,
+    // 512 x 8.
+    if (nvec <= 512) return {256, 2};
     if (nvec <= 1024) return {256, 4};
-    // long rows, measured (one row per workgroup, 8192-16384 rows): for
-    // 1025-2048 vectors 256 x 8 beats 512 x 4 by 12-13%; for 2049-3072
-    // (e.g. 11008 fp32 columns) 768 x 4 beats 1024 x 4 (two rows per
-    // workgroup, the second's loads in flight) by 32%; for 3073-4096 512 x 8
-    // beats it by 20%.  Thread counts of 384, 704 and 1024 were slower at
-    // every length tried.
-    if (nvec <= 2048) return {256, 8};
+    if (nvec <= 1536) return {768, 2};
+    if (nvec <= 2048) return {512, 4};
     if (nvec <= 3072) return {768, 4};
     return {512, 8};
 }
@@ -803,14 +840,13 @@ void dispatch_rows_nv(const PackRowsK& k, const PackRowsK& k2, int64_t rows, Row
         const dim3 g4((unsigned)((rows + RPW - 1) / RPW));
         if (sh.nv == 1) pack_rows_kernel<DT, MODE, COLX, 1, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
         else if (sh.nv == 2) pack_rows_kernel<DT, MODE, COLX, 2, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
-        else if (sh.nv == 4) pack_rows_kernel<DT, MODE, COLX, 4, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
-        else pack_rows_kernel<DT, MODE, COLX, 8, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
+        else pack_rows_kernel<DT, MODE, COLX, 4, 64, RPW><<<g4, 64 * RPW, 0, st>>>(k, k2, rows);
     } else if (sh.nt == 768) {
-        pack_rows_kernel<DT, MODE, COLX, 4, 768, 1><<<grid, 768, 0, st>>>(k, k2, rows);
+        if (sh.nv == 2) pack_rows_kernel<DT, MODE, COLX, 2, 768, 1><<<grid, 768, 0, st>>>(k, k2, rows);
+        else pack_rows_kernel<DT, MODE, COLX, 4, 768, 1><<<grid, 768, 0, st>>>(k, k2, rows);
     } else if (sh.nt == 512) {
-        pack_rows_kernel<DT, MODE, COLX, 8, 512, 1><<<grid, 512, 0, st>>>(k, k2, rows);
-    } else if (sh.nv == 8) {
-        pack_rows_kernel<DT, MODE, COLX, 8, 256, 1><<<grid, 256, 0, st>>>(k, k2, rows);
+        if (sh.nv == 4) pack_rows_kernel<DT, MODE, COLX, 4, 512, 1><<<grid, 512, 0, st>>>(k, k2, rows);
+        else pack_rows_kernel<DT, MODE, COLX, 8, 512, 1><<<grid, 512, 0, st>>>(k, k2, rows);
     } else if (sh.nv == 2) {
         pack_rows_kernel<DT, MODE, COLX, 2, 256, 1><<<grid, 256, 0, st>>>(k, k2, rows);
     } else {

@@ -94,9 +94,10 @@ def _assert_bits(got: np.ndarray, want: np.ndarray, what: str):
     assert bad.size == 0, f"{what}: {bad.size} values differ, first {g[bad[:4]]} vs {w[bad[:4]]}"
 
 
-# row lengths cover every thread shape of the kernel (one wave per row; 256 x
-# 2/4/8, 768 x 4, 512 x 8 threads x vectors), the boundaries between them, and
-# rows past the register-resident 16384 (statistics pass + tiled pack)
+# row lengths cover every thread shape of the kernel (one wave per row with
+# 1, 2 or 4 vectors; 256 x 2/4, 768 x 2/4, 512 x 4/8 threads x vectors), the
+# boundaries between them, and rows past the register-resident 16384
+# (statistics pass + tiled pack)
 @pytest.mark.parametrize("cols", [32, 256, 512, 1024, 1056, 1536, 2048, 4096, 6144, 8192, 8224, 11008, 12288, 12320,
                                   16384, 16416, 20000, 65536])
 @pytest.mark.parametrize("rows", [37, 1])
@@ -110,8 +111,8 @@ def test_pack_rows_f32_bitexact(rows, cols):
     _assert_bits(got, want, f"f32 {rows}x{cols}")
 
 
-# bf16 widths up to the register-resident 32768 and past it
-@pytest.mark.parametrize("cols", [256, 2080, 2560, 4096, 11008, 16384, 16416, 24576, 32768, 32800, 40000])
+# bf16 widths over every thread shape, up to the register-resident 32768 and past it
+@pytest.mark.parametrize("cols", [256, 2080, 2560, 4096, 8192, 11008, 16384, 16416, 24576, 32768, 32800, 40000])
 def test_pack_rows_bf16_bitexact(cols):
     print(f"[pack_rows bf16 37x{cols}]", flush=True)
     xb = torch.from_numpy(_data(37, cols, 5 + cols)).to(torch.bfloat16)
