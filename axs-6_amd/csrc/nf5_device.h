@@ -195,7 +195,7 @@ struct FqScale {
     bool zero;
 };
 
-__device__ __forceinline__ FqScale fq_scale(uint32_t amax, const uint8_t* band) {
+__device__ __forceinline__ FqScale fq_scale_general(uint32_t amax, const uint8_t* band) {
     FqScale s;
     s.nan_block = amax > kInfBits;
     s.zero = amax == 0u;
@@ -203,6 +203,28 @@ __device__ __forceinline__ FqScale fq_scale(uint32_t amax, const uint8_t* band) 
     int e1 = (s.zero || amax >= kInfBits) ? 0 : floor_log2_torch(amax, band) + 1;
     s.inf_scale = inf_amax || e1 >= 128;
     s.e1 = s.inf_scale ? 0 : e1;
+    return s;
+}
+
+// Bits of 2^-101: a block maximum at or above it has e1 >= -100.
+constexpr uint32_t kFastMinAmaxBits = (uint32_t)(kExpBias - 101) << 23;
+
+// fq_scale_general's result.  For a normal block maximum the exponent takes a
+// short form (floor_log2_torch without its subnormal branch: f from the
+// exponent field, k = f + 1 at the power of two above); a wave with a block
+// outside [2^-101, 2^128) other than zero -- subnormal, tiny, inf, NaN or
+// rounding to e1 = 128 -- recomputes with the general form (uniform branch).
+__device__ __forceinline__ FqScale fq_scale(uint32_t amax, const uint8_t* band) {
+    const int f = (int)(amax >> 23) - kExpBias;
+    const uint32_t kb = (amax & 0x7f800000u) + 0x00800000u;     // bits of 2^(f + 1)
+    const int e1 = (kb - amax <= (uint32_t)band[f + 150]) ? f + 2 : f + 1;
+    const bool wide = amax != 0u && (amax < kFastMinAmaxBits || e1 >= 128);
+    if (__builtin_amdgcn_ballot_w64(wide) != 0) return fq_scale_general(amax, band);
+    FqScale s;
+    s.nan_block = false;
+    s.inf_scale = false;
+    s.zero = amax == 0u;
+    s.e1 = s.zero ? 0 : e1;
     return s;
 }
 
