@@ -23,7 +23,12 @@
 //     maxima, then the FQ is the streaming FQ kernel's arithmetic (bit-exact
 //     with fused_fake_quantize on the same values);
 //   * the next K tile is loaded while the current one is quantized and
-//     multiplied.
+//     multiplied;
+//   * with at most 16 rows of X (decode) whose FQ fits the LDS (XL), the
+//     workgroup first quantizes its rows of X once into LDS -- every
+//     workgroup needs all of X, and quantizing it per K tile with the 16-row
+//     block of the MFMA spent as much VALU on X (mostly rows past M) as on W
+//     -- and the K loop then reads FQ(X) from LDS and quantizes only W.
 // Unlike the packed fp16 path there is no row shift and no rounding of the
 // operands: the products are those of fp32 FQ values, as in the reference's
 // fused kernel.  For 16-bit inputs the FQ values stay fp32 too, as in the
@@ -38,6 +43,7 @@ typedef float f32x4f __attribute__((ext_vector_type(4)));
 
 constexpr int kFBK = 32;             // K per tile = one NF5 block
 constexpr int kFRed = 32 * 1024;     // bytes of LDS for the partial tiles
+constexpr int kXlBytes = 128 * 1024; // LDS for FQ(X) in the XL form: M * (K + 4) floats
 
 struct FusedK {
     const void* x; const void* w; const float* bias; void* y;
@@ -77,24 +83,66 @@ __device__ __forceinline__ void fq8(float (&f)[8], const float* lut_s, const uin
         const uint32_t a = __float_as_uint(f[e]) & 0x7fffffffu;
         m = m > a ? m : a;
     }
-    uint32_t o = (uint32_t)__shfl_xor((int)m, 16, 64);
-    m = m > o ? m : o;
-    o = (uint32_t)__shfl_xor((int)m, 32, 64);
-    m = m > o ? m : o;
+    // max with lane ^ 16, then lane ^ 32: v_permlane16_swap (v, v) leaves rows
+    // (0, 0, 2, 2) in its first result and (1, 1, 3, 3) in its second, so each
+    // lane holds its value and its partner's across the two; permlane32_swap
+    // likewise for the halves (lane layout checked on the GPU)
+    const auto p16 = __builtin_amdgcn_permlane16_swap(m, m, false, false);
+    m = p16[0] > p16[1] ? p16[0] : p16[1];
+    const auto p32 = __builtin_amdgcn_permlane32_swap(m, m, false, false);
+    m = p32[0] > p32[1] ? p32[0] : p32[1];
     const FqScale s = fq_scale(m, band_s);
     const float d[8] = {};
     fq_vector<8>(f, s, lut_s, false, d);
 }
 
-template <int DT, int WM, int TN, int NW, bool QX>
+// XL prologue: FQ(X) of rows [0, M) (M <= 16) into xl (row stride K + 4
+// floats: the 16 rows a ds_read_b128 group reads start 4 banks apart).  A
+// thread takes 8 consecutive values, so an NF5 block is 4 neighbouring lanes
+// (a DPP quad); K % 32 == 0 keeps every block's lanes together.
+template <int DT, bool QX>
+__device__ __forceinline__ void stage_x(const FusedK& k, float* xl, const float* lut_s, const uint8_t* band_s,
+                                        int nthreads) {
+    using E = Elem<DT>;
+    using S = typename E::S;
+    const int per_row = k.K / 8;
+    const int nchunk = k.M * per_row;
+    const int ld = k.K + 4;
+    for (int c = threadIdx.x; c < nchunk; c += nthreads) {
+        const int r = c / per_row, c8 = c - r * per_row;
+        u32x4 v[2];
+        load8<DT>(reinterpret_cast<const S*>(k.x) + (int64_t)r * k.K, 0, c8, true, v);
+        float f[8];
+        unpack8<DT>(v, f);
+        if constexpr (QX) {
+            uint32_t m = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t a = __float_as_uint(f[e]) & 0x7fffffffu;
+                m = m > a ? m : a;
+            }
+            m = group_umax<4>(m);
+            const FqScale s = fq_scale(m, band_s);
+            const float d[8] = {};
+            fq_vector<8>(f, s, lut_s, false, d);
+        }
+        float4* dst = reinterpret_cast<float4*>(xl + r * ld + 8 * c8);
+        dst[0] = make_float4(f[0], f[1], f[2], f[3]);
+        dst[1] = make_float4(f[4], f[5], f[6], f[7]);
+    }
+}
+
+template <int DT, int WM, int TN, int NW, bool QX, bool XL>
 __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
     using E = Elem<DT>;
     using S = typename E::S;
     constexpr int BM = 16 * WM, BN = 16 * TN;
     static_assert(NW * BM * BN * 4 <= kFRed, "partial tiles must fit the reduction LDS");
+    static_assert(!XL || WM == 1, "FQ(X) from LDS covers one 16-row block");
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
-    __shared__ __align__(16) float red[kFRed / 4];
+    __shared__ __align__(16) float red[NW * BM * BN];
+    extern __shared__ __align__(16) float xl_s[];   // XL: FQ(X), M x (K + 4)
     const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -133,14 +181,21 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
     u32x4 xv[PF + 1][WM][2], wv[PF + 1][TN][2];
     auto load_tile = [&](int kt, u32x4 (&xd)[WM][2], u32x4 (&wd)[TN][2]) {
         const bool in = kt < kt1;
+        if constexpr (!XL) {
 #pragma unroll
-        for (int i = 0; i < WM; ++i) load8<DT>(xrow[i], kt, q, in && xlive[i], xd[i]);
+            for (int i = 0; i < WM; ++i) load8<DT>(xrow[i], kt, q, in && xlive[i], xd[i]);
+        }
 #pragma unroll
         for (int j = 0; j < TN; ++j) load8<DT>(wrow[j], kt, q, in && wlive[j], wd[j]);
     };
 #pragma unroll
     for (int p = 0; p < PF; ++p) load_tile(kt0 + p, xv[p], wv[p]);
     stage_tables(lut_s, band_w, k.lut, k.band);
+    if constexpr (XL) {
+        stage_x<DT, QX>(k, xl_s, lut_s, band_s, NW * 64);
+        __syncthreads();
+    }
+    const float* xl_row = xl_s + (xlive[0] ? fr : 0) * (k.K + 4) + 8 * q;
 
     f32x4f acc[WM][TN];
 #pragma unroll
@@ -151,10 +206,19 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
     auto step = [&](int kt, u32x4 (&xc)[WM][2], u32x4 (&wc)[TN][2], u32x4 (&xl)[WM][2], u32x4 (&wl)[TN][2]) {
         load_tile(kt + PF, xl, wl);                // tiles past the range load nothing
         float xf[WM][8], wf[TN][8];
+        if constexpr (XL) {
+            // lanes of rows past M read row 0: an output row takes only its own A row, and
+            // the rows past M are not stored
+            const float4 a = *reinterpret_cast<const float4*>(xl_row + kt * kFBK);
+            const float4 b = *reinterpret_cast<const float4*>(xl_row + kt * kFBK + 4);
+            xf[0][0] = a.x; xf[0][1] = a.y; xf[0][2] = a.z; xf[0][3] = a.w;
+            xf[0][4] = b.x; xf[0][5] = b.y; xf[0][6] = b.z; xf[0][7] = b.w;
+        } else {
 #pragma unroll
-        for (int i = 0; i < WM; ++i) {
-            unpack8<DT>(xc[i], xf[i]);
-            if constexpr (QX) fq8(xf[i], lut_s, band_s);
+            for (int i = 0; i < WM; ++i) {
+                unpack8<DT>(xc[i], xf[i]);
+                if constexpr (QX) fq8(xf[i], lut_s, band_s);
+            }
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
@@ -200,11 +264,12 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
     }
 }
 
-template <int DT, int WM, int TN, int NW>
+template <int DT, int WM, int TN, int NW, bool XL = false>
 void launch_cfg(const FusedK& k, bool qx, hipStream_t st) {
     const int tiles = ((k.M + 16 * WM - 1) / (16 * WM)) * ((k.N + 16 * TN - 1) / (16 * TN));
-    if (qx) fused_linear_kernel<DT, WM, TN, NW, true><<<dim3((unsigned)tiles), NW * 64, 0, st>>>(k);
-    else fused_linear_kernel<DT, WM, TN, NW, false><<<dim3((unsigned)tiles), NW * 64, 0, st>>>(k);
+    const size_t xl_bytes = XL ? (size_t)k.M * (k.K + 4) * sizeof(float) : 0;
+    if (qx) fused_linear_kernel<DT, WM, TN, NW, true, XL><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
+    else fused_linear_kernel<DT, WM, TN, NW, false, XL><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
 }
 
 // Tile and K split by shape: one 16-row block for M <= 16 (decode), else
@@ -216,8 +281,14 @@ void launch_dt(const FusedK& k, bool qx, hipStream_t st) {
     const int64_t nkt = k.K / kFBK;
     auto tiles = [&](int bm, int bn) { return ((k.M + bm - 1) / bm) * (int64_t)((k.N + bn - 1) / bn); };
     if (k.M <= 16) {
-        if (nkt >= 16) launch_cfg<DT, 1, 1, 16>(k, qx, st);
-        else launch_cfg<DT, 1, 1, 4>(k, qx, st);
+        const bool xl = (int64_t)k.M * (k.K + 4) * (int64_t)sizeof(float) <= kXlBytes;
+        if (nkt >= 16) {
+            if (xl) launch_cfg<DT, 1, 1, 16, true>(k, qx, st);
+            else launch_cfg<DT, 1, 1, 16>(k, qx, st);
+        } else {
+            if (xl) launch_cfg<DT, 1, 1, 4, true>(k, qx, st);
+            else launch_cfg<DT, 1, 1, 4>(k, qx, st);
+        }
         return;
     }
     if (tiles(32, 64) >= 256) {

@@ -44,7 +44,8 @@ def _exact(x, w, b, quantize_input=True):
 
 
 # decode-like (M 1..32, K = N = 4096), square-ish, wide/short, ragged N and K
-@pytest.mark.parametrize("lead,K,N", [((1,), 4096, 4096), ((7,), 4096, 4096), ((32,), 4096, 4096),
+@pytest.mark.parametrize("lead,K,N", [((1,), 4096, 4096), ((7,), 4096, 4096), ((8,), 4096, 4096),
+                                      ((16,), 2048, 1024), ((16,), 8192, 512), ((32,), 4096, 4096),
                                       ((128,), 1024, 1024), ((256,), 512, 512), ((362,), 4096, 362),
                                       ((64,), 256, 2048), ((512,), 4096, 256), ((5,), 96, 13), ((3, 7), 160, 33),
                                       ((2, 4, 8), 32, 64)])
@@ -72,16 +73,18 @@ def test_fused_linear_ragged_k(K):
 def test_fused_linear_raw_input_and_no_bias():
     from axs.unified import hip_linear
 
-    x, w, b = _inputs((96,), 1024, 768, 9)
-    y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), None, quantize_input=False)
-    assert oracle.rel_l2(y.cpu().numpy(), _exact(x, w, None, quantize_input=False)) <= TOL
+    for m in (96, 3):
+        x, w, b = _inputs((m,), 1024, 768, 9)
+        y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), None, quantize_input=False)
+        assert oracle.rel_l2(y.cpu().numpy(), _exact(x, w, None, quantize_input=False)) <= TOL, m
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-def test_fused_linear_16bit(dt):
+@pytest.mark.parametrize("m", [48, 4])
+def test_fused_linear_16bit(dt, m):
     from axs.unified import hip_linear
 
-    x, w, b = _inputs((48,), 2048, 1024, 11, outliers=False)
+    x, w, b = _inputs((m,), 2048, 1024, 11, outliers=False)
     x, w = x.to(dt), w.to(dt)
     y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), b.to(DEV))
     assert y.dtype == dt
@@ -109,6 +112,10 @@ def test_fused_linear_fq_is_bit_exact_with_the_fq_kernel():
     y = hip_linear.fused_forward(x.to(DEV), eye.to(DEV), None)
     want = oracle.fake_quantize(x.numpy(), 32)
     assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    # at most 16 rows: FQ(X) staged once in LDS (decode form), same bits
+    for m in (1, 5, 16):
+        ym = hip_linear.fused_forward(x[:m].to(DEV), eye.to(DEV), None)
+        assert np.array_equal(ym.cpu().numpy().view(np.uint32), want[:m].view(np.uint32)), m
 
 
 def test_linear_forward_dispatches_small_outputs_to_the_fused_kernel(monkeypatch):
