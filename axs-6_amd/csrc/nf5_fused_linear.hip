@@ -14,11 +14,12 @@
 //     1-32 against a 4096-wide weight) thereby runs thousands of waves;
 //   * the contraction is v_mfma_f32_16x16x4_f32, which takes from lane l
 //     (row l % 16, K group q = l / 16) one value per instruction.  Lane l
-//     loads the 8 consecutive values 8q .. 8q+7 of its row's 32-block (two
-//     16-byte vectors in f32, one in bf16/f16) and feeds its t-th value to
-//     the t-th instruction: the 8 instructions together cover the block's 32
-//     K once, in a permuted order that A and B share, so no operand passes
-//     through LDS;
+//     loads 8 values of its row's 32-block (kslot: two runs of 4 in f32, so
+//     each 16-byte load instruction covers 64 contiguous bytes per row; the
+//     run 8q .. 8q+7 in bf16/f16) and feeds its t-th value to the t-th
+//     instruction: the 8 instructions together cover the block's 32 K once,
+//     in a permuted order that A and B share, so no operand passes through
+//     LDS;
 //   * a row's block is the four lanes l % 16 = r: its amax is two cross-lane
 //     maxima, then the FQ is the streaming FQ kernel's arithmetic (bit-exact
 //     with fused_fake_quantize on the same values);
@@ -51,14 +52,27 @@ struct FusedK {
     const float* lut; const uint8_t* band;
 };
 
-// The 8 values lane (row r, group q) takes of a row's 32-block: 8q .. 8q+7.
+// The 8 values lane (row r, group q) takes of a row's 32-block: in bf16/f16
+// 8q .. 8q+7 (one 16-byte load; the four groups cover the row's 64 bytes);
+// in f32 4q .. 4q+3 and 16+4q .. 16+4q+3, so each of the two 16-byte loads
+// covers one contiguous 64-byte half of the block's 128 bytes per row.
+template <int DT>
+__device__ __forceinline__ int kslot(int q, int t) {
+    return Elem<DT>::V == 4 ? (t < 4 ? 4 * q + t : 16 + 4 * q + (t - 4)) : 8 * q + t;
+}
+
 template <int DT>
 __device__ __forceinline__ void load8(const typename Elem<DT>::S* row, int kt, int q, bool live, u32x4 (&v)[2]) {
     using S = typename Elem<DT>::S;
     constexpr int V = Elem<DT>::V;
-    const S* p = row + kt * kFBK + 8 * q;
-    v[0] = live ? *reinterpret_cast<const u32x4*>(p) : u32x4{0u, 0u, 0u, 0u};
-    if constexpr (V == 4) v[1] = live ? *reinterpret_cast<const u32x4*>(p + 4) : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (V == 4) {
+        const S* p = row + kt * kFBK + 4 * q;
+        v[0] = live ? *reinterpret_cast<const u32x4*>(p) : u32x4{0u, 0u, 0u, 0u};
+        v[1] = live ? *reinterpret_cast<const u32x4*>(p + 16) : u32x4{0u, 0u, 0u, 0u};
+    } else {
+        const S* p = row + kt * kFBK + 8 * q;
+        v[0] = live ? *reinterpret_cast<const u32x4*>(p) : u32x4{0u, 0u, 0u, 0u};
+    }
 }
 
 template <int DT>
@@ -110,8 +124,10 @@ __device__ __forceinline__ void stage_x(const FusedK& k, float* xl, const float*
     const int ld = k.K + 4;
     for (int c = threadIdx.x; c < nchunk; c += nthreads) {
         const int r = c / per_row, c8 = c - r * per_row;
+        const S* p = reinterpret_cast<const S*>(k.x) + (int64_t)r * k.K + 8 * c8;
         u32x4 v[2];
-        load8<DT>(reinterpret_cast<const S*>(k.x) + (int64_t)r * k.K, 0, c8, true, v);
+        v[0] = *reinterpret_cast<const u32x4*>(p);
+        if constexpr (E::V == 4) v[1] = *reinterpret_cast<const u32x4*>(p + 4);
         float f[8];
         unpack8<DT>(v, f);
         if constexpr (QX) {
@@ -195,7 +211,7 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
         stage_x<DT, QX>(k, xl_s, lut_s, band_s, NW * 64);
         __syncthreads();
     }
-    const float* xl_row = xl_s + (xlive[0] ? fr : 0) * (k.K + 4) + 8 * q;
+    const float* xl_row = xl_s + (xlive[0] ? fr : 0) * (k.K + 4);
 
     f32x4f acc[WM][TN];
 #pragma unroll
@@ -209,8 +225,9 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
         if constexpr (XL) {
             // lanes of rows past M read row 0: an output row takes only its own A row, and
             // the rows past M are not stored
-            const float4 a = *reinterpret_cast<const float4*>(xl_row + kt * kFBK);
-            const float4 b = *reinterpret_cast<const float4*>(xl_row + kt * kFBK + 4);
+            // the K slots of W's lanes (kslot): two 4-value runs in f32, one 8-value run otherwise
+            const float4 a = *reinterpret_cast<const float4*>(xl_row + kt * kFBK + kslot<DT>(q, 0));
+            const float4 b = *reinterpret_cast<const float4*>(xl_row + kt * kFBK + kslot<DT>(q, 4));
             xf[0][0] = a.x; xf[0][1] = a.y; xf[0][2] = a.z; xf[0][3] = a.w;
             xf[0][4] = b.x; xf[0][5] = b.y; xf[0][6] = b.z; xf[0][7] = b.w;
         } else {
