@@ -92,11 +92,11 @@ def time_steps(step, launches, steps: int, warmup: int):
     `launches` issues exactly the kernels of one step (the STE backward of
     the fake-quantize launches none).  After `warmup` eager steps,
     GRAPH_STEPS steps' launches are captured into one HIP graph on a side
-    stream and the graph is replayed until `steps` steps have run, between
-    device synchronisations (wall clock) and HIP events on the launch stream
-    (device time).  Every kernel runs every step; the graph only takes the
-    per-launch host cost out of the loop.  Then `steps` eager steps are
-    timed for reference.
+    stream, replayed untimed as often as the timed run will, then replayed
+    until `steps` steps have run, between device synchronisations (wall
+    clock) and HIP events on the launch stream (device time).  Every kernel
+    runs every step; the graph only takes the per-launch host cost out of the
+    loop.  Then `steps` eager steps are timed for reference.
     Returns (wall ms/step, device ms/step, eager wall ms/step)."""
     import torch
 
@@ -118,6 +118,12 @@ def time_steps(step, launches, steps: int, warmup: int):
     g.replay()
     torch.cuda.synchronize()
     replays = max(1, (steps + GRAPH_STEPS - 1) // GRAPH_STEPS)
+    # as many untimed replays first: the power-limited GEMM reads several
+    # percent slow in the first replays after the eager warm-up, while the
+    # clocks settle (4096^3 forward: 160 against 146-152 us a moment later)
+    for _ in range(replays):
+        g.replay()
+    torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
