@@ -804,6 +804,65 @@ __global__ __launch_bounds__(256) void transpose_f16_kernel(TransposeF16 j0, Tra
     }
 }
 
+// The same transposes in 128 x 128 tiles when every row and pointer is
+// 16-byte aligned and the zero-padded width rows_pad a multiple of 8 (the
+// backward's operands): a thread loads an 8 x 8 block (eight 16-byte row
+// segments), transposes it in registers (v_perm_b32 pairs halves of two rows:
+// 32 per block), and writes its 8 columns as 16-byte LDS chunks; the output
+// rows are then stored as 16-byte chunks.  The LDS tile has no padding: the
+// 16-byte chunk k of tile row oc sits at chunk k ^ ((oc >> 3) & 15), so the
+// 16 lanes of a ds_write_b128 or ds_read_b128 group (one 8-row block each,
+// or 16 chunks of one row) reach 16 distinct bank quads.  Against the 64 x 64
+// kernel's 2-byte LDS writes: 8 LDS writes per 64 values instead of 64.
+constexpr int kT128 = 128;
+
+__device__ __forceinline__ int t128_slot(int oc, int k) { return oc * (kT128 / 8) + (k ^ ((oc >> 3) & 15)); }
+
+__global__ __launch_bounds__(256) void transpose128_f16_kernel(TransposeF16 j0, TransposeF16 j1, int ny0, int ny1,
+                                                               ReduceJob red) {
+    if ((int)blockIdx.y >= ny0 + ny1) {      // uniform per workgroup
+        const int64_t rb = (int64_t)(blockIdx.y - ny0 - ny1) * gridDim.x + blockIdx.x;
+        if (rb < red.blocks) reduce_partials_block(red.partial, red.chunks, red.cols, red.out, rb);
+        return;
+    }
+    const bool second = (int)blockIdx.y >= ny0;
+    const TransposeF16 j = second ? j1 : j0;
+    const uint16_t* __restrict__ in = reinterpret_cast<const uint16_t*>(j.in);
+    uint16_t* __restrict__ out = reinterpret_cast<uint16_t*>(j.out);
+    __shared__ __align__(16) u32x4 tile[kT128 * kT128 / 8];   // 16-byte chunks, swizzled
+    const int tid = threadIdx.x;
+    const int64_t c0 = (int64_t)blockIdx.x * kT128, r0 = (int64_t)(second ? blockIdx.y - ny0 : blockIdx.y) * kT128;
+    const int br = tid >> 4, bc = tid & 15;      // this thread's 8 x 8 block
+    const int64_t r = r0 + 8 * br, c = c0 + 8 * bc;
+    uint32_t w[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (r + i < j.rows && c < j.cols) v = *reinterpret_cast<const u32x4*>(in + (r + i) * j.ld_in + c);
+        w[i][0] = v.x; w[i][1] = v.y; w[i][2] = v.z; w[i][3] = v.w;
+    }
+    // column e of the block = rows 0..7 of input column c + e: dword d pairs rows 2d, 2d + 1
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        u32x4 o;
+        o.x = __builtin_amdgcn_perm(w[1][e >> 1], w[0][e >> 1], sel);
+        o.y = __builtin_amdgcn_perm(w[3][e >> 1], w[2][e >> 1], sel);
+        o.z = __builtin_amdgcn_perm(w[5][e >> 1], w[4][e >> 1], sel);
+        o.w = __builtin_amdgcn_perm(w[7][e >> 1], w[6][e >> 1], sel);
+        tile[t128_slot(8 * bc + e, br)] = o;
+    }
+    __syncthreads();
+    // output rows c0 + oc, chunk k = output columns r0 + 8k .. r0 + 8k + 7
+#pragma unroll
+    for (int q = tid; q < kT128 * kT128 / 8; q += 256) {
+        const int oc = q >> 4, k = q & 15;
+        const int64_t orow = c0 + oc, ocol = r0 + 8 * k;
+        if (orow < j.out_rows && ocol < j.rows_pad)
+            *reinterpret_cast<u32x4*>(out + orow * j.ld_out + ocol) = tile[t128_slot(oc, k)];
+    }
+}
+
 __global__ void init_gmax_kernel(int32_t* p) { *p = INT_MIN; }
 
 // Launch shape of the row pack for a row of nvec 16-byte vectors: NT threads,
@@ -1059,9 +1118,15 @@ int launch_transpose_f16(const TransposeF16& a, const TransposeF16* b, hipStream
                          int64_t chunks, int64_t cols, float* db) {
     const TransposeF16 none{nullptr, 0, 0, 0, nullptr, 0, 0, 0};
     const TransposeF16& bb = b ? *b : none;
-    const int64_t gx_a = a.out_rows && a.rows_pad ? (a.out_rows + 63) / 64 : 0;
-    const int64_t gx_b = bb.out_rows && bb.rows_pad ? (bb.out_rows + 63) / 64 : 0;
-    const int64_t ny0 = gx_a ? (a.rows_pad + 63) / 64 : 0, ny1 = gx_b ? (bb.rows_pad + 63) / 64 : 0;
+    auto aligned = [](const TransposeF16& x) {
+        return x.out_rows == 0 || x.rows_pad == 0 ||
+               (x.ld_in % 8 == 0 && x.ld_out % 8 == 0 && x.rows_pad % 8 == 0 && x.cols % 8 == 0 &&
+                (uintptr_t)x.in % 16 == 0 && (uintptr_t)x.out % 16 == 0);
+    };
+    const int T = aligned(a) && aligned(bb) ? kT128 : kTile;
+    const int64_t gx_a = a.out_rows && a.rows_pad ? (a.out_rows + T - 1) / T : 0;
+    const int64_t gx_b = bb.out_rows && bb.rows_pad ? (bb.out_rows + T - 1) / T : 0;
+    const int64_t ny0 = gx_a ? (a.rows_pad + T - 1) / T : 0, ny1 = gx_b ? (bb.rows_pad + T - 1) / T : 0;
     const bool red = db && partial && cols > 0;
     if (ny0 + ny1 == 0) return red ? launch_reduce_partials(partial, chunks, cols, db, st) : AXS6_OK;
     // a tile column past one job's out_rows writes nothing for it (orow >= out_rows)
@@ -1070,8 +1135,12 @@ int launch_transpose_f16(const TransposeF16& a, const TransposeF16* b, hipStream
     const int64_t nyr = (rj.blocks + gx - 1) / gx;
     const dim3 grid((unsigned)gx, (unsigned)(ny0 + ny1 + nyr));
     // the jobs in order: a (when it has tiles), then b
-    transpose_f16_kernel<<<grid, 256, 0, st>>>(ny0 ? a : bb, ny0 ? bb : a, (int)(ny0 ? ny0 : ny1),
-                                               (int)(ny0 ? ny1 : 0), rj);
+    if (T == kT128)
+        transpose128_f16_kernel<<<grid, 256, 0, st>>>(ny0 ? a : bb, ny0 ? bb : a, (int)(ny0 ? ny0 : ny1),
+                                                      (int)(ny0 ? ny1 : 0), rj);
+    else
+        transpose_f16_kernel<<<grid, 256, 0, st>>>(ny0 ? a : bb, ny0 ? bb : a, (int)(ny0 ? ny0 : ny1),
+                                                   (int)(ny0 ? ny1 : 0), rj);
     return check_launch("transpose_f16");
 }
 
