@@ -23,7 +23,7 @@ import torch
 
 from axs import _lib
 from axs.core import DEFAULT_BLOCK_SIZE, VALID_BLOCK_SIZES, AXSTensor
-from axs.unified.hip_kernels import _on_device, _require_device, as_rows
+from axs.unified.hip_kernels import _on_device, _require_device, as_rows, components
 
 __all__ = ["block_bytes", "record_bytes", "encode_blocks", "decode_blocks", "axs_tensor_to_bytes",
            "axs_tensor_from_bytes"]
@@ -87,16 +87,11 @@ def decode_blocks(data: torch.Tensor, shape, block_size: int = DEFAULT_BLOCK_SIZ
 def axs_tensor_to_bytes(t: AXSTensor) -> torch.Tensor:
     """uint8 records of an AXSTensor's blocks (``AXSBlock.to_bytes`` of each
     block, concatenated)."""
-    _require_device(t.magnitudes, "axs_tensor_to_bytes")
     bs = t.block_size
     _check_block(bs)
     nblk = t.num_blocks
     rows = t.shared_exponents.numel() // nblk if nblk else 0
-    e = t.shared_exponents.contiguous().to(torch.uint8)
-    c = t.magnitudes.contiguous().to(torch.uint8)
-    s = None if t.signs is None else t.signs.contiguous().view(torch.uint8)
-    if c.numel() != rows * nblk * bs:
-        raise ValueError(f"magnitudes hold {c.numel()} codes, expected {rows * nblk * bs}")
+    e, c, s = components(t.shared_exponents, t.magnitudes, t.signs, rows, nblk, bs, "axs_tensor_to_bytes")
     buf = torch.empty((rows * nblk * record_bytes(bs),), dtype=torch.uint8, device=c.device)
     if buf.numel():
         with _on_device(c):

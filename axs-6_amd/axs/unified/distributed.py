@@ -20,7 +20,7 @@ import torch
 
 from axs import _lib
 from axs.core import DEFAULT_BLOCK_SIZE, VALID_BLOCK_SIZES
-from axs.unified.hip_kernels import _on_device, _require_device, as_rows, hip_dequantize, hip_quantize
+from axs.unified.hip_kernels import _on_device, _require_device, as_rows, components, hip_dequantize, hip_quantize
 
 __all__ = [
     "_pack_gradient",
@@ -63,9 +63,7 @@ def _pack_to_flat_buffer(shared_exponents: torch.Tensor, signs: torch.Tensor,
     _require_device(magnitudes, "_pack_to_flat_buffer")
     rows, nblk, block_size = magnitudes.shape
     assert block_size % 4 == 0, f"block_size must be divisible by 4, got {block_size}"
-    e = shared_exponents.contiguous().to(torch.uint8)
-    c = magnitudes.contiguous().to(torch.uint8)
-    s = None if signs is None else signs.contiguous().to(torch.uint8)
+    e, c, s = components(shared_exponents, magnitudes, signs, rows, nblk, block_size, "_pack_to_flat_buffer")
     buf = torch.empty((rows * nblk * (1 + block_size * 3 // 4),), dtype=torch.uint8, device=c.device)
     if buf.numel():
         with _on_device(c):

@@ -37,6 +37,12 @@ def _require_device(t: torch.Tensor, fn: str) -> None:
         raise RuntimeError(f"{fn} requires a CUDA (ROCm/HIP) device tensor, got device {t.device}")
 
 
+def _same_device(fn: str, first: torch.Tensor, *others: torch.Tensor | None) -> None:
+    for t in others:
+        if t is not None and t.device != first.device:
+            raise RuntimeError(f"{fn}: tensors on {first.device} and {t.device}; all must be on one device")
+
+
 def _check_rounding(rounding: str) -> bool:
     if rounding not in ("nearest", "stochastic"):
         raise ValueError(f"rounding must be 'nearest' or 'stochastic', got {rounding!r}")
@@ -200,13 +206,33 @@ def hip_quantize(
     return exps, codes, signs.view(torch.bool), fq
 
 
+def components(exps: torch.Tensor, codes: torch.Tensor, signs: torch.Tensor | None, rows: int, nblk: int,
+               block_size: int, fn: str):
+    """The AXSTensor fields as contiguous uint8 tensors on the codes' device,
+    checked to hold at least the rows * nblk exponents and rows * nblk *
+    block_size codes (and signs) the kernels read: a short or host-side field
+    raises here instead of being read out of bounds on the device."""
+    _require_device(codes, fn)
+    for name, t in (("shared_exponents", exps), ("signs", signs)):
+        if t is not None and t.device != codes.device:
+            raise RuntimeError(f"{fn}: {name} is on {t.device}, the codes on {codes.device}")
+    need_e, need_c = rows * nblk, rows * nblk * block_size
+    if exps.numel() < need_e or codes.numel() < need_c or (signs is not None and signs.numel() < need_c):
+        raise ValueError(f"{fn}: fields too small for {rows} x {nblk} blocks of {block_size} "
+                         f"(exponents {exps.numel()}, codes {codes.numel()}"
+                         f"{'' if signs is None else f', signs {signs.numel()}'})")
+    def u8(t):
+        t = t.contiguous()
+        return t.view(torch.uint8) if t.dtype in (torch.bool, torch.int8) else t.to(torch.uint8)
+
+    return u8(exps), u8(codes), None if signs is None else u8(signs)
+
+
 def hip_dequantize(exps: torch.Tensor, codes: torch.Tensor, signs: torch.Tensor | None,
                    rows: int, cols: int, block_size: int) -> torch.Tensor:
-    _require_device(codes, "hip_dequantize")
     assert block_size in VALID_BLOCK_SIZES, f"block_size must be one of {VALID_BLOCK_SIZES}"
-    e = exps.contiguous()
-    c = codes.contiguous()
-    s = None if signs is None else signs.contiguous().view(torch.uint8)
+    e, c, s = components(exps, codes, signs, rows, (cols + block_size - 1) // block_size, block_size,
+                         "hip_dequantize")
     y = torch.empty((rows, cols), dtype=torch.float32, device=codes.device)
     if rows and cols:
         with _on_device(c):

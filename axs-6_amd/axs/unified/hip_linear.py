@@ -25,7 +25,7 @@ import torch.nn.functional as F
 
 from axs import _lib
 from axs.core import VALID_BLOCK_SIZES
-from axs.unified.hip_kernels import _on_device, _require_device
+from axs.unified.hip_kernels import _on_device, _require_device, _same_device
 
 _SUPPORTED = (torch.float32, torch.bfloat16, torch.float16)
 
@@ -107,6 +107,7 @@ def fused_forward(input, weight, bias=None, quantize_input=True):
     fn = "axs_fused_linear"
     _require_device(input, fn)
     _require_device(weight, fn)
+    _same_device(fn, input, weight, bias)
     K = input.shape[-1]
     N, Kw = weight.shape
     if Kw != K:
@@ -169,6 +170,7 @@ def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     fn = "axs_matmul"
     _require_device(a, fn)
     _require_device(b, fn)
+    _same_device(fn, a, b)
     if b.dim() != 2:
         raise RuntimeError(f"{fn}: b must be 2-D, got shape {tuple(b.shape)}")
     K = a.shape[-1]

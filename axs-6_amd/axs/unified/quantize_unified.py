@@ -83,7 +83,7 @@ def dequantize_unified(axs_tensor: AXSTensor) -> torch.Tensor:
     """Reconstruct float32 values ``+-codebook[code] * 2**(e - 127)``."""
     shape = axs_tensor.original_shape
     cols = shape[-1]
-    rows = axs_tensor.shared_exponents.shape[0]
+    rows = math.prod(shape[:-1])
     y = _hk.hip_dequantize(axs_tensor.shared_exponents, axs_tensor.magnitudes, axs_tensor.signs,
                            rows, cols, axs_tensor.block_size)
     return y.reshape(shape)

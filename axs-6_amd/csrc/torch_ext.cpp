@@ -155,6 +155,10 @@ Fwd linear_fwd_impl(const at::Tensor& input, const at::Tensor& weight, const std
     const char* fn = "axs_linear";
     require_device(input, fn);
     require_device(weight, fn);
+    TORCH_CHECK(weight.device() == input.device(), fn, ": weight is on ", weight.device(), ", input on ",
+                input.device());
+    TORCH_CHECK(!bias || !bias->defined() || bias->device() == input.device(), fn, ": bias is on ",
+                bias && bias->defined() ? bias->device() : input.device(), ", input on ", input.device());
     TORCH_CHECK(bs == 8 || bs == 16 || bs == 32, fn, ": block_size must be one of (8, 16, 32), got ", bs);
     TORCH_CHECK(input.dim() >= 1 && weight.dim() == 2, fn, ": expected input (*, K) and weight (N, K)");
     const int64_t K = input.size(-1), N = weight.size(0), Kw = weight.size(1);
@@ -203,6 +207,10 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> linear_bwd_impl(
     at::IntArrayRef x_shape, at::ScalarType w_dtype, int64_t bs, bool quantize_grad, bool need_x, bool need_w,
     bool need_b, std::optional<int64_t> seed) {
     const auto opts = xq.options();
+    TORCH_CHECK(grad_output.device() == xq.device(), "axs_linear backward: grad_output is on ", grad_output.device(),
+                ", the saved operands on ", xq.device());
+    TORCH_CHECK(grad_output.numel() == M * n_true, "axs_linear backward: grad_output has ", grad_output.numel(),
+                " elements, expected ", M * n_true);
     at::Tensor dy = rows2d(grad_output, n_true).to(dtype);
     if (N != n_true) dy = pad_last(dy, bs);
     dy = dense(dy);

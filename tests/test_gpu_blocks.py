@@ -189,3 +189,22 @@ def test_full_size_round_trip():
     assert torch.equal(y.view(torch.int32), wire.view(torch.int32))
     rows = torch.randperm(8192, generator=torch.Generator().manual_seed(2))[:64].to(DEV)
     assert np.array_equal(encode_blocks(x[rows], 32).cpu().numpy(), _oracle_records(x[rows].cpu().numpy(), 32))
+
+
+def test_short_or_host_fields_raise():
+    """AXSTensor fields smaller than their shape claims, or on another device,
+    raise before any kernel reads them."""
+    from axs.blocks import axs_tensor_to_bytes
+    from axs.core import AXSTensor
+    from axs.unified import distributed as d
+    from axs.unified.quantize_unified import dequantize_unified, quantize_unified
+
+    q = quantize_unified(_data((8, 64), 4).to(DEV), 32)
+    short = AXSTensor(q.shared_exponents[:4], q.signs, q.magnitudes, 32, q.original_shape, q.num_blocks)
+    with pytest.raises(ValueError, match="too small"):
+        dequantize_unified(short)
+    host = AXSTensor(q.shared_exponents.cpu(), q.signs, q.magnitudes, 32, q.original_shape, q.num_blocks)
+    with pytest.raises(RuntimeError, match="shared_exponents"):
+        axs_tensor_to_bytes(host)
+    with pytest.raises(ValueError, match="too small"):
+        d._pack_to_flat_buffer(q.shared_exponents, q.signs.reshape(-1)[:10], q.magnitudes)
