@@ -249,24 +249,51 @@ __global__ __launch_bounds__(kThreads) void quantize_vec_kernel(
             m = m > a ? m : a;
         }
         m = group_umax<G>(m);
-        int ex = (m == 0u || m >= kInfBits) ? 0 : floor_log2_torch(m, band_s) + 1 + kExpBias;
-        ex = ex < 0 ? 0 : (ex > 255 ? 255 : ex);
-        const int se = ex - kExpBias;              // scale = 2^se, se in [-127, 128]
         float d[V];
         const DitherVec dv = dither_vec(key, offset + (uint64_t)(vi * V));
 #pragma unroll
         for (int e = 0; e < V; ++e) d[e] = STOCH ? dither_step(dv, e) : 0.0f;
         uint32_t cw[2] = {0u, 0u}, sw[2] = {0u, 0u};   // V bytes of codes and signs
 #pragma unroll
-        for (int e = 0; e < V; ++e) {
-            const uint32_t ab = __float_as_uint(f[e]) & 0x7fffffffu;
-            float n;
-            if (se >= 128) n = ab >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;   // x / inf
-            else n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -se);
-            n = (n > 1.0f) ? 1.0f : n;             // clamp(0, 1); NaN passes through
-            const int idx = lut_index(n, STOCH, d[e]);
-            cw[e / 4] |= (uint32_t)rev_s[idx] << (8 * (e % 4));
-            sw[e / 4] |= (f[e] < 0.0f ? 1u : 0u) << (8 * (e % 4));
+        for (int e = 0; e < V; ++e) sw[e / 4] |= (f[e] < 0.0f ? 1u : 0u) << (8 * (e % 4));
+        const FqScale sc = fq_scale(m, band_s);
+        int ex;
+        if (__builtin_amdgcn_ballot_w64(sc.nan_block || sc.inf_scale || sc.e1 < kFastMinE1) == 0) {
+            // every block of the wave is finite with e1 in [-100, 127]: the
+            // shared exponent is e1 + 127 (0 for a zero block) without a clamp,
+            // and one index serves the code and the FQ value (fq_vector's
+            // short sequence; its range argument bounds the index)
+            ex = sc.zero ? 0 : sc.e1 + kExpBias;
+            const float c = __builtin_amdgcn_ldexpf(1023.0f, -sc.e1);
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const uint32_t xb = __float_as_uint(f[e]);
+                const uint32_t ab = xb & 0x7fffffffu;
+                const float t = STOCH ? (__builtin_amdgcn_ldexpf(__uint_as_float(ab), -sc.e1) + d[e]) * 1023.0f
+                                      : lut_pos(ab, c);
+                const int idx = (int)t;
+                cw[e / 4] |= (uint32_t)rev_s[idx] << (8 * (e % 4));
+                if (fq) {
+                    const float mag = __builtin_amdgcn_ldexpf(lut_s[idx], sc.e1);
+                    const uint32_t nz = (uint32_t)((int32_t)(ab + 0x7fffffffu) >> 31);
+                    f[e] = __uint_as_float((__float_as_uint(mag) ^ (xb & 0x80000000u)) & nz);
+                }
+            }
+        } else {
+            ex = (m == 0u || m >= kInfBits) ? 0 : floor_log2_torch(m, band_s) + 1 + kExpBias;
+            ex = ex < 0 ? 0 : (ex > 255 ? 255 : ex);
+            const int se = ex - kExpBias;          // scale = 2^se, se in [-127, 128]
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const uint32_t ab = __float_as_uint(f[e]) & 0x7fffffffu;
+                float n;
+                if (se >= 128) n = ab >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;   // x / inf
+                else n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -se);
+                n = (n > 1.0f) ? 1.0f : n;         // clamp(0, 1); NaN passes through
+                const int idx = lut_index(n, STOCH, d[e]);
+                cw[e / 4] |= (uint32_t)rev_s[idx] << (8 * (e % 4));
+            }
+            if (fq) fq_vector<V>(f, sc, lut_s, STOCH, d);
         }
         if (live) {
             if constexpr (V == 4) {
@@ -278,11 +305,7 @@ __global__ __launch_bounds__(kThreads) void quantize_vec_kernel(
             }
             if (vi % G == 0) exps[vi / G] = (uint8_t)ex;
         }
-        if (fq) {
-            const FqScale sc = fq_scale(m, band_s);
-            fq_vector<V>(f, sc, lut_s, STOCH, d);
-            if (live) reinterpret_cast<u32x4*>(fq)[vi] = E::pack(f);
-        }
+        if (fq && live) reinterpret_cast<u32x4*>(fq)[vi] = E::pack(f);
     }
 }
 
