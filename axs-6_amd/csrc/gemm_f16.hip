@@ -244,6 +244,18 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Waits until at most `ahead` slabs of IPW loads each are outstanding
+// (ahead <= MAXA, wave-uniform): s_waitcnt takes an immediate count.
+template <int MAXA, int IPW>
+__device__ __forceinline__ void wait_slabs(int ahead) {
+    if constexpr (MAXA == 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (ahead >= MAXA) wait_vmcnt<MAXA * IPW>();
+        else wait_slabs<MAXA - 1, IPW>(ahead);
+    }
+}
+
 // Multi-stage variant: operand tiles go from HBM straight into LDS
 // (buffer_load_dwordx4 ... lds, 16 bytes per lane, a wave instruction fills
 // 1 KiB = 8 rows of a 64-half K-slab) with STAGES slabs in flight, so a
@@ -349,16 +361,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     for (int kt = 0; kt < KT; ++kt) {
         // slab kt has landed once at most (slabs issued after it) * IPW loads are outstanding
         const int ahead = (KT - 1 - kt) < (STAGES - 2) ? (KT - 1 - kt) : (STAGES - 2);
-        if constexpr (STAGES >= 4) {
-            if (ahead >= 2) wait_vmcnt<2 * IPW>();
-            else if (ahead == 1) wait_vmcnt<IPW>();
-            else wait_vmcnt<0>();
-        } else if constexpr (STAGES == 3) {
-            if (ahead >= 1) wait_vmcnt<IPW>();
-            else wait_vmcnt<0>();
-        } else {
-            wait_vmcnt<0>();
-        }
+        wait_slabs<STAGES - 2, IPW>(ahead);
         // a bare s_barrier: __syncthreads() would also drain every outstanding
         // load (vmcnt(0)) and serialise the pipeline; the explicit vmcnt wait
         // above already orders this wave's LDS fills before the barrier.
