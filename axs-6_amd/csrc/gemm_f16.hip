@@ -256,6 +256,80 @@ __device__ __forceinline__ void wait_slabs(int ahead) {
     }
 }
 
+// Origin (m0, n0) of this workgroup's BM x BN output tile: workgroup ids are
+// dispatched round-robin over the 8 XCDs, so the id is remapped to give each
+// XCD a contiguous range of the grouped order (kGroupM rows of tiles per
+// group), whose A rows and B columns then stay inside that XCD's L2.
+template <int BM, int BN>
+__device__ __forceinline__ void tile_origin(const GemmK& g, int& m0, int& n0) {
+    const int tiles_m = (g.M + BM - 1) / BM;
+    const int tiles_n = (g.N + BN - 1) / BN;
+    const int total = tiles_m * tiles_n;
+    int bid = blockIdx.x;
+    if (total % 8 == 0) bid = (bid % 8) * (total / 8) + bid / 8;
+    const int per_group = kGroupM * tiles_n;
+    const int group = bid / per_group;
+    const int first_m = group * kGroupM;
+    const int gsize = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+    const int in_group = bid - group * per_group;
+    m0 = (first_m + in_group % gsize) * BM;
+    n0 = (in_group / gsize) * BN;
+}
+
+// The epilogue through LDS, after the K loop.  Each wave stages its 32-row
+// block row i (32 x WN floats, row stride WN+4 to spread banks;
+// stage_block_row) in its own LDS region, then reads it back as 4
+// consecutive columns per lane.  The slabs are dead once every wave has left
+// the K loop (barrier); after that a wave touches only its own region, and
+// LDS operations of one wave complete in order, so no further barrier is
+// needed.
+template <int WM, int WN>
+__device__ __forceinline__ void gemm_epilogue(const GemmK& g, const WaveAcc<WM, WN>& acc, char* smem, int m0,
+                                              int n0, int wm, int wn, int wave, int lane) {
+    constexpr int LDW = WN + 4;
+    constexpr int LANES_PER_ROW = WN / 4;
+    static_assert(64 % LANES_PER_ROW == 0 && 32 % (64 / LANES_PER_ROW) == 0, "wave tile width");
+    wait_vmcnt<0>();
+    __syncthreads();
+    float* ws = reinterpret_cast<float*>(smem) + wave * (32 * LDW);
+    const int gexp = g.glob_exp ? (*g.glob_exp == INT_MIN ? 0 : *g.glob_exp + g.glob_add) : 0;
+    const int gcol = n0 + wn * WN + (lane % LANES_PER_ROW) * 4;
+    int cexp[4];
+    float cbias[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const bool in = gcol + t < g.N;
+        cexp[t] = gexp + ((g.col_exp && in) ? g.col_exp[gcol + t] : 0);
+        cbias[t] = (g.bias && in) ? g.bias[gcol + t] : 0.0f;
+    }
+    // Row exponents of the wave's WM rows, WM/64 per lane, loaded once: a load
+    // per store pass would sit behind the previous pass's stores (the output
+    // may alias row_exp as far as the compiler knows) and pay a full memory
+    // latency each time -- ~15 us per launch, all of a small GEMM's runtime.
+    constexpr int RPL = WM / 64;                      // row exponents held per lane
+    static_assert(WM % 64 == 0, "wave tile height");
+    int rexp_l[RPL];
+#pragma unroll
+    for (int q = 0; q < RPL; ++q) {
+        const int grow = m0 + wm * WM + q * 64 + lane;
+        rexp_l[q] = (g.row_exp && grow < g.M) ? g.row_exp[grow] : 0;
+    }
+    const int esize = g.out_dtype == AXS6_F32 ? 4 : 2;
+    void* const out = reinterpret_cast<char*>(g.out) + (int64_t)blockIdx.y * g.split_stride * esize;
+    const bool vec = (g.ldo % 4 == 0) && ((uintptr_t)out % (4 * esize) == 0);
+    const bool nt = g.split_stride == 0;     // final output: streaming stores
+    const int row0 = m0 + wm * WM;
+    if (g.out_dtype == AXS6_F32)
+        epilogue_store<AXS6_F32, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+                                                      vec, nt, lane);
+    else if (g.out_dtype == AXS6_BF16)
+        epilogue_store<AXS6_BF16, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+                                                       vec, nt, lane);
+    else
+        epilogue_store<AXS6_F16, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
+                                                      vec, nt, lane);
+}
+
 // Multi-stage variant: operand tiles go from HBM straight into LDS
 // (buffer_load_dwordx4 ... lds, 16 bytes per lane, a wave instruction fills
 // 1 KiB = 8 rows of a 64-half K-slab) with STAGES slabs in flight, so a
@@ -279,18 +353,8 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     static_assert(A_INST >= 1 && B_INST >= 1 && STAGES >= 2, "tile shape");
     extern __shared__ __align__(16) char smem[];
 
-    const int tiles_m = (g.M + BM - 1) / BM;
-    const int tiles_n = (g.N + BN - 1) / BN;
-    const int total = tiles_m * tiles_n;
-    int bid = blockIdx.x;
-    if (total % 8 == 0) bid = (bid % 8) * (total / 8) + bid / 8;
-    const int per_group = kGroupM * tiles_n;
-    const int group = bid / per_group;
-    const int first_m = group * kGroupM;
-    const int gsize = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
-    const int in_group = bid - group * per_group;
-    const int m0 = (first_m + in_group % gsize) * BM;
-    const int n0 = (in_group / gsize) * BN;
+    int m0, n0;
+    tile_origin<BM, BN>(g, m0, n0);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -380,56 +444,8 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
         mma_step16<BK, WM, WN>(acc, slab, slab + BM * RB, a_row0, b_row0, fg);
     }
 
-    // ---- epilogue through LDS ------------------------------------------------
-    // Each wave stages its 32-row block row i (32 x WN floats, row stride
-    // WN+4 to spread banks; stage_block_row) in its own LDS region,
-    // then reads it back as 4 consecutive columns per lane.  The slabs are
-    // dead once every wave has left the K loop (barrier); after that a wave
-    // touches only its own region, and LDS operations of one wave complete in
-    // order, so no further barrier is needed.
-    constexpr int LDW = WN + 4;
-    constexpr int LANES_PER_ROW = WN / 4;
-    static_assert(NW * 32 * LDW * 4 <= STAGES * SLAB, "epilogue staging must fit in the slab LDS");
-    static_assert(64 % LANES_PER_ROW == 0 && 32 % (64 / LANES_PER_ROW) == 0, "wave tile width");
-    wait_vmcnt<0>();
-    __syncthreads();
-    float* ws = reinterpret_cast<float*>(smem) + wave * (32 * LDW);
-    const int gexp = g.glob_exp ? (*g.glob_exp == INT_MIN ? 0 : *g.glob_exp + g.glob_add) : 0;
-    const int gcol = n0 + wn * WN + (lane % LANES_PER_ROW) * 4;
-    int cexp[4];
-    float cbias[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const bool in = gcol + t < g.N;
-        cexp[t] = gexp + ((g.col_exp && in) ? g.col_exp[gcol + t] : 0);
-        cbias[t] = (g.bias && in) ? g.bias[gcol + t] : 0.0f;
-    }
-    // Row exponents of the wave's WM rows, WM/64 per lane, loaded once: a load
-    // per store pass would sit behind the previous pass's stores (the output
-    // may alias row_exp as far as the compiler knows) and pay a full memory
-    // latency each time -- ~15 us per launch, all of a small GEMM's runtime.
-    constexpr int RPL = WM / 64;                      // row exponents held per lane
-    static_assert(WM % 64 == 0, "wave tile height");
-    int rexp_l[RPL];
-#pragma unroll
-    for (int q = 0; q < RPL; ++q) {
-        const int grow = m0 + wm * WM + q * 64 + lane;
-        rexp_l[q] = (g.row_exp && grow < g.M) ? g.row_exp[grow] : 0;
-    }
-    const int esize = g.out_dtype == AXS6_F32 ? 4 : 2;
-    void* const out = reinterpret_cast<char*>(g.out) + (int64_t)blockIdx.y * g.split_stride * esize;
-    const bool vec = (g.ldo % 4 == 0) && ((uintptr_t)out % (4 * esize) == 0);
-    const bool nt = g.split_stride == 0;     // final output: streaming stores
-    const int row0 = m0 + wm * WM;
-    if (g.out_dtype == AXS6_F32)
-        epilogue_store<AXS6_F32, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
-                                                      vec, nt, lane);
-    else if (g.out_dtype == AXS6_BF16)
-        epilogue_store<AXS6_BF16, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
-                                                       vec, nt, lane);
-    else
-        epilogue_store<AXS6_F16, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
-                                                      vec, nt, lane);
+    static_assert(NW * 32 * (WN + 4) * 4 <= STAGES * SLAB, "epilogue staging must fit in the slab LDS");
+    gemm_epilogue<WM, WN>(g, acc, smem, m0, n0, wm, wn, wave, lane);
 #endif
 }
 
