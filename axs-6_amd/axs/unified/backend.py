@@ -87,10 +87,16 @@ def accelerated_fake_quantize(
     rounding: Literal["nearest", "stochastic"] = "nearest",
 ) -> torch.Tensor:
     """NF5 fake-quantize on the HIP path."""
+    note_device(tensor)
+    return _hk.hip_fused_fake_quantize(tensor, block_size, rounding)
+
+
+def note_device(tensor: torch.Tensor) -> None:
+    """Resolves the active backend (once) and records the tensor's device
+    as holding the tables (reported by backend_info)."""
     get_backend()
     if tensor.is_cuda:
         _LUT_CACHE.setdefault(tensor.device, True)
-    return _hk.hip_fused_fake_quantize(tensor, block_size, rounding)
 
 
 def accelerated_linear(

@@ -14,13 +14,19 @@ from typing import Literal
 
 import torch
 
+from axs import _lib
 from axs.core import DEFAULT_BLOCK_SIZE
+from axs.unified import backend as _backend
+from axs.unified import hip_kernels as _hk
 from axs.unified import hip_linear
 from axs.unified.backend import accelerated_fake_quantize as _accel_fq
 
 
 class _FusedQuantizeSTE(torch.autograd.Function):
-    """Forward: NF5 fake-quantize.  Backward: the incoming gradient, unchanged."""
+    """Forward: NF5 fake-quantize.  Backward: the incoming gradient, unchanged.
+
+    ``fake_quantize_unified`` runs the same operation as a C++ autograd node
+    (``axs._C.fq_ste``), without this class's Python forward and backward."""
 
     @staticmethod
     def forward(ctx, tensor: torch.Tensor, block_size: int, rounding: str) -> torch.Tensor:  # type: ignore[override]
@@ -36,8 +42,11 @@ def fake_quantize_unified(
     block_size: int = DEFAULT_BLOCK_SIZE,
     rounding: Literal["nearest", "stochastic"] = "nearest",
 ) -> torch.Tensor:
-    """NF5 fake-quantize with a straight-through gradient."""
-    return _FusedQuantizeSTE.apply(tensor, block_size, rounding)
+    """NF5 fake-quantize with a straight-through gradient: the backward
+    hands the incoming gradient back unchanged."""
+    stochastic = _hk.fq_checks(tensor, block_size, rounding, "fake_quantize_unified")
+    _backend.note_device(tensor)
+    return _lib.ext().fq_ste(tensor, block_size, stochastic)
 
 
 class _AXSLinearUnifiedFunction(torch.autograd.Function):

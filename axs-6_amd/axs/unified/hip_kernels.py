@@ -152,22 +152,25 @@ def hip_fused_fake_quantize(
     signature compatibility with the reference's Triton wrapper; the launch
     shape is chosen by the library.
     """
-    fn = "hip_fused_fake_quantize"
+    stochastic = fq_checks(tensor, block_size, rounding, "hip_fused_fake_quantize")
+    return _lib.ext().fq(tensor, block_size, stochastic, None if seed is None else _as_int64(seed))
+
+
+def fq_checks(tensor: torch.Tensor, block_size: int, rounding: str, fn: str) -> bool:
+    """The fake-quantize entry points' argument checks, in the reference's
+    order and exception types (triton_kernels.py:326-330): a host tensor
+    raises RuntimeError naming CUDA, a block size outside (8, 16, 32)
+    AssertionError, an unknown rounding mode ValueError.  Returns whether the
+    rounding is stochastic."""
     _require_device(tensor, fn)
     assert block_size in VALID_BLOCK_SIZES, f"block_size must be one of {VALID_BLOCK_SIZES}"
-    stochastic = _check_rounding(rounding)
-    orig_dtype = tensor.dtype
-    x, rows, cols = as_rows(tensor)
-    y = torch.empty_like(x)
-    if rows and cols:
-        s, sdev, ctr = stochastic_seed(x.device, seed) if stochastic else (0, None, None)
-        with _on_device(x):
-            _lib.call("axs6_nf5_fake_quantize", x.data_ptr(), y.data_ptr(), _lib.DTYPE_CODE[x.dtype],
-                      rows, cols, block_size, int(stochastic), s, 0, sdev, _lib.stream_of(x))
-            if ctr is not None:
-                ctr.add_(1)
-    y = y.reshape(tensor.shape)
-    return y if y.dtype == orig_dtype else y.to(orig_dtype)
+    return _check_rounding(rounding)
+
+
+def _as_int64(seed: int) -> int:
+    """``seed`` modulo 2^64 as a signed 64-bit value (the same 64 bits)."""
+    s = int(seed) & 0xFFFFFFFFFFFFFFFF
+    return s - (1 << 64) if s >= (1 << 63) else s
 
 
 def hip_quantize(

@@ -1,5 +1,10 @@
-// Torch extension `axs._C`: the host side of the AXS-6 quantized linear in
-// C++ over the C ABI of libaxs6.so (include/axs6.h).
+// Torch extension `axs._C`: the host side of the NF5 fake-quantize and the
+// AXS-6 quantized linear in C++ over the C ABI of libaxs6.so
+// (include/axs6.h).
+//
+// The fake-quantize with its straight-through gradient (the reference's
+// _FusedQuantizeSTE, functional_unified.py:38-60) is a C++ autograd node too,
+// so a call costs one node and one library call, with no Python in between.
 //
 // The reference's _AXSLinearUnifiedFunction (axs/unified/functional_unified.py:
 // 107-170) is a Python autograd Function.  Here the same operation is a C++
@@ -140,6 +145,47 @@ Seed stochastic_seed(const at::Device& device, std::optional<int64_t> seed) {
         }
     }
     return s;
+}
+
+// ---- fake-quantize ---------------------------------------------------------------
+
+// fused_fake_quantize (axs/unified/quantize_unified.py:121-204) on the GPU:
+// blocks along the last dim, computed in the tensor's own type when it is
+// float32, bfloat16 or float16 and in float32 otherwise (cast back after),
+// output contiguous with the input's shape.  The caller has checked the
+// device, block size and rounding mode.
+at::Tensor fq(const at::Tensor& tensor, int64_t bs, bool stochastic, std::optional<int64_t> seed) {
+    TORCH_CHECK_INDEX(tensor.dim() >= 1, "fake-quantize needs a tensor with a last dimension");
+    const at::ScalarType orig = tensor.scalar_type();
+    const at::Tensor x = (dtype_code(orig) >= 0 ? tensor : tensor.to(at::kFloat)).contiguous();
+    const int64_t cols = x.size(-1);
+    const int64_t rows = cols ? x.numel() / cols : 0;
+    at::Tensor y = at::empty_like(x, at::MemoryFormat::Contiguous);
+    if (rows && cols) {
+        c10::DeviceGuard guard(x.device());
+        Seed s;
+        if (stochastic) s = stochastic_seed(x.device(), seed);
+        check_rc(axs6_nf5_fake_quantize(x.data_ptr(), y.data_ptr(), dtype_code(x.scalar_type()), rows, cols,
+                                        (int32_t)bs, stochastic ? 1 : 0, s.seed, 0, s.dev, stream_of(x)),
+                 "axs6_nf5_fake_quantize");
+        if (s.counter.defined()) s.counter.add_(1);
+    }
+    return y.scalar_type() == orig ? y : y.to(orig);
+}
+
+// _FusedQuantizeSTE (functional_unified.py:38-60): forward fake-quantizes,
+// backward hands the incoming gradient back unchanged (the same tensor).
+struct FakeQuantizeSTE : public torch::autograd::Function<FakeQuantizeSTE> {
+    static at::Tensor forward(AutogradContext*, const at::Tensor& tensor, int64_t bs, bool stochastic) {
+        return fq(tensor, bs, stochastic, std::nullopt);
+    }
+    static variable_list backward(AutogradContext*, variable_list grads) {
+        return {grads[0], at::Tensor(), at::Tensor()};
+    }
+};
+
+at::Tensor fq_ste(const at::Tensor& tensor, int64_t bs, bool stochastic) {
+    return FakeQuantizeSTE::apply(tensor, bs, stochastic);
 }
 
 // ---- forward ------------------------------------------------------------------
@@ -304,7 +350,11 @@ py::tuple linear_fwd(const at::Tensor& input, const at::Tensor& weight, const st
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
-    m.doc() = "AXS-6 quantized linear: host logic and autograd node over libaxs6.so";
+    m.doc() = "AXS-6 fake-quantize and quantized linear: host logic and autograd nodes over libaxs6.so";
+    m.def("fq", &fq, "NF5 fake-quantize of the last dim (no autograd)", py::arg("tensor"), py::arg("block_size"),
+          py::arg("stochastic"), py::arg("seed") = py::none());
+    m.def("fq_ste", &fq_ste, "NF5 fake-quantize with the straight-through gradient (autograd node)",
+          py::arg("tensor"), py::arg("block_size"), py::arg("stochastic"));
     m.def("linear", &linear, "FQ(input) FQ(weight)^T + bias with the quantized backward (autograd node)",
           py::arg("input"), py::arg("weight"), py::arg("bias"), py::arg("block_size"), py::arg("quantize_input"),
           py::arg("quantize_grad"));

@@ -1,5 +1,5 @@
 """The torch extension axs._C (csrc/torch_ext.cpp) loads beside libaxs6.so,
-exports the linear's entry points, draws dither seeds exactly as the Python
+exports the fake-quantize's and the linear's entry points, draws dither seeds exactly as the Python
 wrappers do (torch.randint(0, 2**62, (1,)) on the default CPU generator),
 and rejects host tensors with the reference's CUDA error."""
 from __future__ import annotations
@@ -12,7 +12,7 @@ def test_extension_loads_and_exports():
     from axs import _lib
 
     C = _lib.ext()
-    for name in ("linear", "linear_fwd", "linear_bwd", "graph_counter", "next_seed"):
+    for name in ("fq", "fq_ste", "linear", "linear_fwd", "linear_bwd", "graph_counter", "next_seed"):
         assert callable(getattr(C, name)), name
 
 
@@ -38,3 +38,13 @@ def test_host_tensors_raise_cuda_error():
         C.linear(x, w, None, 32, True, True)
     with pytest.raises(RuntimeError, match="CUDA"):
         C.linear_fwd(x, w, None, 32, True)
+
+
+def test_fq_host_tensor_raises_before_the_extension():
+    """fake_quantize_unified checks its arguments in Python first, with the
+    reference's exception types."""
+    from axs.unified import functional_unified as fu
+
+    x = torch.randn(4, 64)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        fu.fake_quantize_unified(x)

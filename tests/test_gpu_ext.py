@@ -66,3 +66,49 @@ def test_partial_gradients_and_no_grad():
     with torch.no_grad():
         y = fu.axs_linear_unified(x, w, b)
     assert not y.requires_grad and torch.equal(y, y1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
+@pytest.mark.parametrize("shape", [(3, 40, 96), (7, 33), (1, 8)], ids=str)
+def test_fq_node(dtype, shape):
+    """fake_quantize_unified (the C++ node axs._C.fq_ste) gives the bits of
+    hip_fused_fake_quantize (pinned against the oracle by the FQ tests) and of
+    the Python _FusedQuantizeSTE, in the input's dtype and shape, and its
+    backward hands back the incoming gradient itself."""
+    from axs.unified import functional_unified as fu
+    from axs.unified.hip_kernels import hip_fused_fake_quantize
+
+    gen = torch.Generator().manual_seed(sum(shape))
+    x = (torch.randn(*shape, generator=gen) * 3).to(DEV, dtype)
+    g = torch.randn(*shape, generator=gen).to(DEV, dtype)
+    for bs in (8, 32):
+        xs = x.clone().requires_grad_(True)
+        y = fu.fake_quantize_unified(xs, bs, "nearest")
+        assert y.dtype == dtype and y.shape == x.shape and y.requires_grad
+        want = hip_fused_fake_quantize(x, bs, "nearest")
+        assert torch.equal(y.detach(), want)
+        assert torch.equal(fu._FusedQuantizeSTE.apply(x.clone().requires_grad_(True), bs, "nearest").detach(), want)
+        (gx,) = torch.autograd.grad(y, xs, g)
+        assert gx.data_ptr() == g.data_ptr()
+    # stochastic: the seed comes from torch's default CPU generator, as in the function
+    torch.manual_seed(21)
+    y1 = fu.fake_quantize_unified(x, 32, "stochastic")
+    torch.manual_seed(21)
+    y2 = hip_fused_fake_quantize(x, 32, "stochastic")
+    assert torch.equal(y1, y2)
+    # a non-contiguous view is quantized as its contiguous copy
+    if len(shape) == 3:
+        xt = x.transpose(0, 1)
+        assert torch.equal(fu.fake_quantize_unified(xt, 32, "nearest"),
+                           hip_fused_fake_quantize(xt.contiguous(), 32, "nearest"))
+
+
+def test_fq_node_empty_and_errors():
+    from axs.unified import functional_unified as fu
+
+    assert fu.fake_quantize_unified(torch.zeros(0, 64, device=DEV)).shape == (0, 64)
+    assert fu.fake_quantize_unified(torch.zeros(4, 0, device=DEV)).shape == (4, 0)
+    with pytest.raises(AssertionError):
+        fu.fake_quantize_unified(torch.zeros(4, 64, device=DEV), 12)
+    with pytest.raises(ValueError):
+        fu.fake_quantize_unified(torch.zeros(4, 64, device=DEV), 32, "up")

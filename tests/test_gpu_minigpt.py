@@ -152,7 +152,7 @@ def test_minigpt_graph_replay_matches_eager_training():
     assert gap < CURVE_TOL * eager[0]
 
 
-def test_graph_replays_draw_fresh_dither(monkeypatch):
+def test_graph_replays_draw_fresh_dither():
     """A stochastic fake-quantize recorded in a graph: each replay adds the
     device counter to the seed fixed at capture, so replays differ, and each
     replay is bit-exact against the oracle given that seed."""
@@ -165,13 +165,16 @@ def test_graph_replays_draw_fresh_dither(monkeypatch):
     xh = torch.randn(64, 256, generator=g)
     x = xh.cuda()
     hip_kernels.prepare_graph_capture(x.device)
-    monkeypatch.setattr(hip_kernels, "next_seed", lambda: 123456789)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         hip_kernels.hip_fused_fake_quantize(x, 32, "stochastic")
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
+    # the seed drawn at capture: the next draw of torch's CPU generator
+    torch.manual_seed(29)
+    seed = hip_kernels.next_seed()
+    torch.manual_seed(29)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         out = hip_kernels.hip_fused_fake_quantize(x, 32, "stochastic")
@@ -182,7 +185,7 @@ def test_graph_replays_draw_fresh_dither(monkeypatch):
         graph.replay()
         torch.cuda.synchronize()
         got = out.cpu().numpy()
-        want = oracle.fake_quantize(xh.numpy(), 32, oracle.uniform(123456789 + c, 0, xh.numel()))
+        want = oracle.fake_quantize(xh.numpy(), 32, oracle.uniform(seed + c, 0, xh.numel()))
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
         assert int(ctr.item()) == c + 1
         seen.append(got)
