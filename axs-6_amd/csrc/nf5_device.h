@@ -133,6 +133,23 @@ __device__ __forceinline__ uint32_t group_umax(uint32_t v) {
     return v;
 }
 
+// Unsigned max across each group of N neighbouring lanes (N in {8, 16, 32}),
+// returned in every lane of the group: the quad and half-row steps of
+// group_umax, row_mirror for 16 lanes, and for 32 the v_permlane16_swap of v
+// with itself, whose two results hold rows (0, 0, 2, 2) and (1, 1, 3, 3) --
+// each lane's row and its partner row.
+template <int N>
+__device__ __forceinline__ uint32_t lanes_umax(uint32_t v) {
+    static_assert(N == 8 || N == 16 || N == 32, "lane group");
+    v = group_umax<8>(v);
+    if constexpr (N >= 16) v = dpp_umax<0x140>(v);
+    if constexpr (N >= 32) {
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        v = p[0] > p[1] ? p[0] : p[1];
+    }
+    return v;
+}
+
 // Unsigned max over the whole wave, returned in every lane (a scalar): an
 // inclusive max-scan over each row of 16 lanes (row_shr 1, 2, 4, 8; lanes
 // without a source read 0), rows folded with row_bcast:15 and row_bcast:31,

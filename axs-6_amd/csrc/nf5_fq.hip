@@ -20,8 +20,11 @@
 // contiguous HBM; each thread keeps kUnroll vectors in flight.  The 4 KiB
 // LUT and the band table are staged in LDS once per workgroup and the grid
 // is capped (grid-stride loop) so that staging is amortised.
-// General path (ragged last dim or unaligned views): one element per lane,
-// one block per `block` lanes, shuffle reductions.
+// Row path (rows of >= 64 values with a ragged last block, or unaligned
+// views): one element per lane in row order, a block is `block` neighbouring
+// lanes (DPP / permlane maximum), rows cut into segments of 64 or 256
+// values, the next segment's loads in flight (fq_rows_kernel).  Shorter
+// rows: one block per lane group with shuffle reductions (fq_scalar_kernel).
 #include <math.h>
 
 #pragma clang fp contract(off)
@@ -138,6 +141,79 @@ __global__ __launch_bounds__(kThreads) void fq_scalar_kernel(const typename Elem
         const float d = STOCH ? dither_step(key, offset + (uint64_t)gi) : 0.0f;
         float o = fq_value(f, s, lut_s, STOCH, d);
         if (valid) y[gi] = E::from_f(o);
+    }
+}
+
+// Rows that do not tile into 16-byte vectors of whole blocks (a ragged last
+// block, or row starts off 16-byte alignment): one element per lane, lanes
+// in row order, so a block is BS neighbouring lanes and its maximum a DPP /
+// permlane reduction, and every load or store instruction covers 64
+// consecutive elements of one row.  A row is cut into segments of 64 * U
+// elements (a multiple of BS, so blocks never straddle segments); each wave
+// walks a contiguous range of segments, stepping its row index instead of
+// dividing per element.  Lanes past the row's end read 0 -- the reference's
+// zero padding of the last block -- and store nothing.
+template <int DT, int BS, bool STOCH, int U>
+__global__ __launch_bounds__(kThreads) void fq_rows_kernel(const typename Elem<DT>::S* __restrict__ x,
+                                                           typename Elem<DT>::S* __restrict__ y, int64_t rows,
+                                                           int64_t cols, int64_t segs_per_row, int64_t segs_per_wave,
+                                                           const float* __restrict__ lut_g,
+                                                           const uint8_t* __restrict__ band_g, uint64_t seed,
+                                                           const uint64_t* __restrict__ seed_dev, uint64_t offset) {
+    using E = Elem<DT>;
+    constexpr int SEG = 64 * U;
+    static_assert(SEG % BS == 0, "segments hold whole blocks");
+    const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
+    __shared__ float lut_s[kLutSize];
+    __shared__ uint32_t band_w[kBandSize / 4];
+    stage_tables(lut_s, band_w, lut_g, band_g);
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t total = rows * segs_per_row;
+    int64_t seg = wave * segs_per_wave;
+    const int64_t end = seg + segs_per_wave < total ? seg + segs_per_wave : total;
+    if (seg >= end) return;
+    int64_t r = seg / segs_per_row;
+    int64_t sx = seg - r * segs_per_row;
+    // the next segment's loads go out before the current one is processed
+    typename E::S raw[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const int64_t c = sx * SEG + lane + 64 * k;
+        raw[k] = c < cols ? x[r * cols + c] : (typename E::S)0;
+    }
+    for (; seg < end; ++seg) {
+        const int64_t base = r * cols;
+        const int64_t c0 = sx * SEG + lane;
+        float f[U];
+#pragma unroll
+        for (int k = 0; k < U; ++k) f[k] = E::to_f(raw[k]);
+        int64_t rn = r, sn = sx + 1;
+        if (sn == segs_per_row) {
+            sn = 0;
+            ++rn;
+        }
+        if (seg + 1 < end) {
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                const int64_t c = sn * SEG + lane + 64 * k;
+                raw[k] = c < cols ? x[rn * cols + c] : (typename E::S)0;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            const int64_t c = c0 + 64 * k;
+            const uint32_t m = lanes_umax<BS>(__float_as_uint(f[k]) & 0x7fffffffu);
+            const FqScale s = fq_scale(m, band_s);
+            float v[1] = {f[k]};
+            const float d[1] = {STOCH ? dither_step(key, offset + (uint64_t)(base + c)) : 0.0f};
+            fq_vector<1>(v, s, lut_s, STOCH, d);
+            if (c < cols) y[base + c] = E::from_f(v[0]);
+        }
+        r = rn;
+        sx = sn;
     }
 }
 
@@ -385,6 +461,34 @@ int64_t capped_grid(int64_t work_items, int64_t per_wg) {
     return need < cap ? need : cap;
 }
 
+// Row-segment launches (fq_rows_kernel and its quantize counterpart) for rows
+// of at least kRowsMinCols elements; shorter rows keep the block-per-lane-group
+// kernels.  Segments of 64 * u elements, a contiguous range of per_wave of
+// them per wave, sized for about kRowsWavesPerCu waves per CU and at least
+// kRowsMinSegs segments per wave (the tables are staged once per workgroup).
+constexpr int64_t kRowsMinCols = 64;
+constexpr int64_t kRowsWavesPerCu = 32;
+constexpr int64_t kRowsMinSegs = 2;
+
+struct RowSegs {
+    int u;
+    int64_t per_row, per_wave;
+    dim3 grid;
+};
+
+RowSegs row_segs(int64_t rows, int64_t cols, int u) {
+    RowSegs g;
+    g.u = u;
+    g.per_row = (cols + 64 * u - 1) / (64 * u);
+    const int64_t total = rows * g.per_row;
+    const int64_t waves = (int64_t)num_cus() * kRowsWavesPerCu;
+    int64_t per = (total + waves - 1) / waves;
+    g.per_wave = per < kRowsMinSegs ? kRowsMinSegs : per;
+    const int64_t need = (total + g.per_wave - 1) / g.per_wave;            // waves
+    g.grid = dim3((unsigned)((need + kThreads / 64 - 1) / (kThreads / 64)));
+    return g;
+}
+
 template <int DT, int BS>
 void launch_fq_typed(const void* x, void* y, int64_t rows, int64_t cols, bool stochastic, uint64_t seed, const uint64_t* seed_dev,
                      uint64_t offset, const DeviceTables& t, hipStream_t st) {
@@ -398,6 +502,19 @@ void launch_fq_typed(const void* x, void* y, int64_t rows, int64_t cols, bool st
             fq_vec_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, seed, seed_dev, offset);
         else
             fq_vec_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, seed, seed_dev, offset);
+    } else if (cols >= kRowsMinCols) {
+        const RowSegs g = row_segs(rows, cols, cols >= 4 * kRowsMinCols ? 4 : 1);
+        if (g.u == 4) {
+            if (stochastic)
+                fq_rows_kernel<DT, BS, true, 4><<<g.grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, g.per_row, g.per_wave, t.lut, t.band, seed, seed_dev, offset);
+            else
+                fq_rows_kernel<DT, BS, false, 4><<<g.grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, g.per_row, g.per_wave, t.lut, t.band, seed, seed_dev, offset);
+        } else {
+            if (stochastic)
+                fq_rows_kernel<DT, BS, true, 1><<<g.grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, g.per_row, g.per_wave, t.lut, t.band, seed, seed_dev, offset);
+            else
+                fq_rows_kernel<DT, BS, false, 1><<<g.grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, g.per_row, g.per_wave, t.lut, t.band, seed, seed_dev, offset);
+        }
     } else {
         const int64_t nblk = (cols + BS - 1) / BS;
         const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));

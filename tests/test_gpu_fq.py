@@ -282,3 +282,68 @@ def test_dequantize_vs_oracle(bs, cols):
     g = load_golden("edge_cases.npz")
     q = quantize_unified(torch.from_numpy(g["x"]).to(DEV), bs)
     assert bits_equal(dequantize_unified(q).cpu().numpy(), g[f"deq_bs{bs}"])
+
+
+# Row-segment kernel (fq_rows_kernel): rows of >= 64 values that do not tile
+# into 16-byte vectors of whole blocks -- a ragged last block, or a view whose
+# start is off 16-byte alignment.  One segment per wave (64 columns), four
+# (256 columns and more), rows ending mid-segment.
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+@pytest.mark.parametrize("shape", [(300, 4100), (64, 1000), (129, 777), (5, 64), (33, 255)], ids=str)
+def test_rows_kernel_bitexact(dt, bs, shape):
+    print(f"[fq rows {dt} bs={bs} {shape}]", flush=True)
+    x = config2_input(shape, 7 * bs + shape[1]).to(dt)
+    got = _fq(x.to(DEV), bs).cpu()
+    want = torch.from_numpy(oracle.fake_quantize(x.float().numpy(), bs)).to(dt)
+    if dt == torch.float32:
+        assert bits_equal(got.numpy(), want.numpy()), first_mismatch(got.numpy(), want.numpy())
+    else:
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("bs", [8, 32])
+def test_rows_kernel_unaligned_view(dt, bs):
+    """Whole-block rows in a view one element into its buffer (the vector
+    kernel needs 16-byte alignment): the row-segment kernel, same bits."""
+    x = config2_input((256, 4096), 91 + bs).to(dt)
+    buf = torch.zeros(x.numel() + 1, dtype=dt, device=DEV)
+    buf[1:] = x.reshape(-1).to(DEV)
+    xd = buf[1:].view(x.shape)
+    assert xd.data_ptr() % 16 != 0
+    bits = torch.int32 if dt == torch.float32 else torch.int16
+    got = _fq(xd, bs).cpu().view(bits)
+    assert torch.equal(got, _fq(x.to(DEV), bs).cpu().view(bits))
+
+
+def test_rows_kernel_exponent_range():
+    """Blocks across the whole float32 range (subnormal, tiny, huge, inf
+    scale, NaN) through the row-segment kernel: rows of four such blocks plus
+    a ragged block of seven values."""
+    rng = np.random.default_rng(8)
+    blocks = []
+    for e in range(-160, 130, 2):
+        blocks.append((rng.standard_normal(32) * 2.0 ** e).astype(np.float32))
+    nan = rng.standard_normal(32).astype(np.float32)
+    nan[5] = np.nan
+    inf = rng.standard_normal(32).astype(np.float32)
+    inf[9] = np.inf
+    blocks += [nan, inf, np.zeros(32, np.float32), np.full(32, -0.0, np.float32)]
+    while len(blocks) % 4:
+        blocks.append(rng.standard_normal(32).astype(np.float32))
+    wide = np.stack(blocks).reshape(-1, 128)
+    x = np.concatenate([wide, rng.standard_normal((wide.shape[0], 7)).astype(np.float32)], axis=1)
+    for bs in (8, 16, 32):
+        got = _fq(torch.from_numpy(x).to(DEV), bs).cpu().numpy()
+        want = oracle.fake_quantize(x, bs)
+        assert bits_equal(got, want), (bs, first_mismatch(got, want))
+
+
+@pytest.mark.parametrize("bs", [8, 32])
+def test_rows_kernel_stochastic_given_stream(bs):
+    x = config2_input((200, 1030), 55)
+    seed = 0x5EED0F00D
+    got = _fq(x.to(DEV), bs, "stochastic", seed=seed).cpu().numpy()
+    want = oracle.fake_quantize(x.numpy(), bs, oracle.uniform(seed, 0, x.numel()))
+    assert bits_equal(got, want), first_mismatch(got, want)
