@@ -280,6 +280,59 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(
     }
 }
 
+// quantize_unified of V values of one block whose maximum |x| bits are m:
+// the shared exponent (returned), the V codes and V signs as bytes packed
+// little-endian into cw / sw, and, with want_fq, f replaced by its FQ values.
+// When no lane of the wave holds a block with a NaN or an infinite scale or
+// an exponent below kFastMinE1 (one ballot, so the branch is uniform), the
+// shared exponent is e1 + 127 (0 for a zero block) without a clamp and one
+// LUT index serves the code and the FQ value (fq_vector's short sequence;
+// its range argument bounds the index); otherwise the general sequence.
+template <int V, bool STOCH>
+__device__ __forceinline__ int quant_values(float (&f)[V], uint32_t m, const float (&d)[V], const float* lut_s,
+                                            const uint8_t* band_s, const uint8_t* rev_s, bool want_fq,
+                                            uint32_t (&cw)[2], uint32_t (&sw)[2]) {
+    cw[0] = cw[1] = sw[0] = sw[1] = 0u;
+#pragma unroll
+    for (int e = 0; e < V; ++e) sw[e / 4] |= (f[e] < 0.0f ? 1u : 0u) << (8 * (e % 4));
+    const FqScale sc = fq_scale(m, band_s);
+    int ex;
+    if (__builtin_amdgcn_ballot_w64(sc.nan_block || sc.inf_scale || sc.e1 < kFastMinE1) == 0) {
+        ex = sc.zero ? 0 : sc.e1 + kExpBias;
+        const float c = __builtin_amdgcn_ldexpf(1023.0f, -sc.e1);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const uint32_t xb = __float_as_uint(f[e]);
+            const uint32_t ab = xb & 0x7fffffffu;
+            const float t = STOCH ? (__builtin_amdgcn_ldexpf(__uint_as_float(ab), -sc.e1) + d[e]) * 1023.0f
+                                  : lut_pos(ab, c);
+            const int idx = (int)t;
+            cw[e / 4] |= (uint32_t)rev_s[idx] << (8 * (e % 4));
+            if (want_fq) {
+                const float mag = __builtin_amdgcn_ldexpf(lut_s[idx], sc.e1);
+                const uint32_t nz = (uint32_t)((int32_t)(ab + 0x7fffffffu) >> 31);
+                f[e] = __uint_as_float((__float_as_uint(mag) ^ (xb & 0x80000000u)) & nz);
+            }
+        }
+    } else {
+        ex = (m == 0u || m >= kInfBits) ? 0 : floor_log2_torch(m, band_s) + 1 + kExpBias;
+        ex = ex < 0 ? 0 : (ex > 255 ? 255 : ex);
+        const int se = ex - kExpBias;          // scale = 2^se, se in [-127, 128]
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const uint32_t ab = __float_as_uint(f[e]) & 0x7fffffffu;
+            float n;
+            if (se >= 128) n = ab >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;   // x / inf
+            else n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -se);
+            n = (n > 1.0f) ? 1.0f : n;         // clamp(0, 1); NaN passes through
+            const int idx = lut_index(n, STOCH, d[e]);
+            cw[e / 4] |= (uint32_t)rev_s[idx] << (8 * (e % 4));
+        }
+        if (want_fq) fq_vector<V>(f, sc, lut_s, STOCH, d);
+    }
+    return ex;
+}
+
 // Vector form of quantize_kernel for rows that tile into whole blocks
 // (cols % BS == 0: codes and signs are then the flat [rows * cols] layout,
 // exponents one per BS flat values) and aligned pointers: each lane takes one
@@ -329,48 +382,8 @@ __global__ __launch_bounds__(kThreads) void quantize_vec_kernel(
         const DitherVec dv = dither_vec(key, offset + (uint64_t)(vi * V));
 #pragma unroll
         for (int e = 0; e < V; ++e) d[e] = STOCH ? dither_step(dv, e) : 0.0f;
-        uint32_t cw[2] = {0u, 0u}, sw[2] = {0u, 0u};   // V bytes of codes and signs
-#pragma unroll
-        for (int e = 0; e < V; ++e) sw[e / 4] |= (f[e] < 0.0f ? 1u : 0u) << (8 * (e % 4));
-        const FqScale sc = fq_scale(m, band_s);
-        int ex;
-        if (__builtin_amdgcn_ballot_w64(sc.nan_block || sc.inf_scale || sc.e1 < kFastMinE1) == 0) {
-            // every block of the wave is finite with e1 in [-100, 127]: the
-            // shared exponent is e1 + 127 (0 for a zero block) without a clamp,
-            // and one index serves the code and the FQ value (fq_vector's
-            // short sequence; its range argument bounds the index)
-            ex = sc.zero ? 0 : sc.e1 + kExpBias;
-            const float c = __builtin_amdgcn_ldexpf(1023.0f, -sc.e1);
-#pragma unroll
-            for (int e = 0; e < V; ++e) {
-                const uint32_t xb = __float_as_uint(f[e]);
-                const uint32_t ab = xb & 0x7fffffffu;
-                const float t = STOCH ? (__builtin_amdgcn_ldexpf(__uint_as_float(ab), -sc.e1) + d[e]) * 1023.0f
-                                      : lut_pos(ab, c);
-                const int idx = (int)t;
-                cw[e / 4] |= (uint32_t)rev_s[idx] << (8 * (e % 4));
-                if (fq) {
-                    const float mag = __builtin_amdgcn_ldexpf(lut_s[idx], sc.e1);
-                    const uint32_t nz = (uint32_t)((int32_t)(ab + 0x7fffffffu) >> 31);
-                    f[e] = __uint_as_float((__float_as_uint(mag) ^ (xb & 0x80000000u)) & nz);
-                }
-            }
-        } else {
-            ex = (m == 0u || m >= kInfBits) ? 0 : floor_log2_torch(m, band_s) + 1 + kExpBias;
-            ex = ex < 0 ? 0 : (ex > 255 ? 255 : ex);
-            const int se = ex - kExpBias;          // scale = 2^se, se in [-127, 128]
-#pragma unroll
-            for (int e = 0; e < V; ++e) {
-                const uint32_t ab = __float_as_uint(f[e]) & 0x7fffffffu;
-                float n;
-                if (se >= 128) n = ab >= kInfBits ? __uint_as_float(kNanBits) : 0.0f;   // x / inf
-                else n = __builtin_amdgcn_ldexpf(__uint_as_float(ab), -se);
-                n = (n > 1.0f) ? 1.0f : n;         // clamp(0, 1); NaN passes through
-                const int idx = lut_index(n, STOCH, d[e]);
-                cw[e / 4] |= (uint32_t)rev_s[idx] << (8 * (e % 4));
-            }
-            if (fq) fq_vector<V>(f, sc, lut_s, STOCH, d);
-        }
+        uint32_t cw[2], sw[2];                         // V bytes of codes and signs
+        const int ex = quant_values<V, STOCH>(f, m, d, lut_s, band_s, rev_s, fq != nullptr, cw, sw);
         if (live) {
             if constexpr (V == 4) {
                 reinterpret_cast<uint32_t*>(codes)[vi] = cw[0];
@@ -432,6 +445,128 @@ __global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t* __r
         const int64_t o = r * nblk * bs + c;
         const float v = cb[codes[o] & 31] * scale;
         y[i] = (signs && signs[o]) ? -v : v;
+    }
+}
+
+// Row-segment forms of quantize_kernel and dequantize_kernel, for rows of at
+// least 64 values that do not tile into vectors of whole blocks: the lane
+// and segment layout of fq_rows_kernel over the padded row (cpad = nblk * BS
+// values: the codes and signs of the padding positions are written too, as
+// quantize_kernel writes them), one value per lane.
+template <int DT, int BS, bool STOCH, int U>
+__global__ __launch_bounds__(kThreads) void quantize_rows_kernel(
+    const typename Elem<DT>::S* __restrict__ x, int64_t rows, int64_t cols, int64_t nblk, int64_t segs_per_row,
+    int64_t segs_per_wave, const float* __restrict__ lut_g, const uint8_t* __restrict__ band_g,
+    const uint8_t* __restrict__ rev_g, uint64_t seed, const uint64_t* __restrict__ seed_dev, uint64_t offset,
+    uint8_t* __restrict__ exps, uint8_t* __restrict__ codes, uint8_t* __restrict__ signs,
+    typename Elem<DT>::S* __restrict__ fq) {
+    using E = Elem<DT>;
+    constexpr int SEG = 64 * U;
+    static_assert(SEG % BS == 0, "segments hold whole blocks");
+    const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
+    __shared__ float lut_s[kLutSize];
+    __shared__ uint32_t band_w[kBandSize / 4];
+    __shared__ uint8_t rev_s[kLutSize];
+    reinterpret_cast<uint32_t*>(rev_s)[threadIdx.x] = reinterpret_cast<const uint32_t*>(rev_g)[threadIdx.x];
+    stage_tables(lut_s, band_w, lut_g, band_g);
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+
+    const int lane = threadIdx.x & 63;
+    const int64_t cpad = nblk * BS;
+    const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t total = rows * segs_per_row;
+    int64_t seg = wave * segs_per_wave;
+    const int64_t end = seg + segs_per_wave < total ? seg + segs_per_wave : total;
+    if (seg >= end) return;
+    int64_t r = seg / segs_per_row;
+    int64_t sx = seg - r * segs_per_row;
+    typename E::S raw[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const int64_t c = sx * SEG + lane + 64 * k;
+        raw[k] = c < cols ? x[r * cols + c] : (typename E::S)0;
+    }
+    for (; seg < end; ++seg) {
+        const int64_t base = r * cols;
+        const int64_t c0 = sx * SEG + lane;
+        float f[U];
+#pragma unroll
+        for (int k = 0; k < U; ++k) f[k] = E::to_f(raw[k]);
+        int64_t rn = r, sn = sx + 1;
+        if (sn == segs_per_row) {
+            sn = 0;
+            ++rn;
+        }
+        if (seg + 1 < end) {
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                const int64_t c = sn * SEG + lane + 64 * k;
+                raw[k] = c < cols ? x[rn * cols + c] : (typename E::S)0;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            const int64_t c = c0 + 64 * k;
+            const uint32_t m = lanes_umax<BS>(__float_as_uint(f[k]) & 0x7fffffffu);
+            float v[1] = {f[k]};
+            const float d[1] = {STOCH ? dither_step(key, offset + (uint64_t)(base + c)) : 0.0f};
+            uint32_t cw[2], sw[2];
+            const int ex = quant_values<1, STOCH>(v, m, d, lut_s, band_s, rev_s, fq != nullptr, cw, sw);
+            if (c < cpad) {
+                const int64_t o = r * cpad + c;
+                codes[o] = (uint8_t)cw[0];
+                if (signs) signs[o] = (uint8_t)sw[0];
+                if (c % BS == 0) exps[r * nblk + c / BS] = (uint8_t)ex;
+            }
+            if (fq && c < cols) fq[base + c] = E::from_f(v[0]);
+        }
+        r = rn;
+        sx = sn;
+    }
+}
+
+template <int U>
+__global__ __launch_bounds__(kThreads) void dequantize_rows_kernel(const uint8_t* __restrict__ exps,
+                                                                   const uint8_t* __restrict__ codes,
+                                                                   const uint8_t* __restrict__ signs,
+                                                                   float* __restrict__ y, int64_t rows, int64_t cols,
+                                                                   int64_t nblk, int bs, int64_t segs_per_row,
+                                                                   int64_t segs_per_wave,
+                                                                   const float* __restrict__ cb_g) {
+    constexpr int SEG = 64 * U;
+    __shared__ float cb[kLevels];
+    if (threadIdx.x < kLevels) cb[threadIdx.x] = cb_g[threadIdx.x];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int sh = bs == 8 ? 3 : (bs == 16 ? 4 : 5);
+    const int64_t cpad = nblk * bs;
+    const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t total = rows * segs_per_row;
+    int64_t seg = wave * segs_per_wave;
+    const int64_t end = seg + segs_per_wave < total ? seg + segs_per_wave : total;
+    if (seg >= end) return;
+    int64_t r = seg / segs_per_row;
+    int64_t sx = seg - r * segs_per_row;
+    for (; seg < end; ++seg) {
+        uint8_t cd[U], sg[U], ex[U];
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            const int64_t c = sx * SEG + lane + 64 * k;
+            const bool in = c < cols;
+            cd[k] = in ? codes[r * cpad + c] : 0;
+            sg[k] = (in && signs) ? signs[r * cpad + c] : 0;
+            ex[k] = in ? exps[r * nblk + (c >> sh)] : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            const int64_t c = sx * SEG + lane + 64 * k;
+            const float a = cb[cd[k] & 31] * pow2_float((int)ex[k] - kExpBias);
+            if (c < cols) y[r * cols + c] = sg[k] ? -a : a;
+        }
+        if (++sx == segs_per_row) {
+            sx = 0;
+            ++r;
+        }
     }
 }
 
@@ -550,6 +685,23 @@ void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochast
         return;
     }
     const int64_t nblk = (cols + BS - 1) / BS;
+    const int64_t cpad = nblk * BS;
+    if (cpad >= kRowsMinCols) {
+        const RowSegs g = row_segs(rows, cpad, cpad >= 4 * kRowsMinCols ? 4 : 1);
+#define AXS6_QROWS(ST_, U_)                                                                                  \
+        quantize_rows_kernel<DT, BS, ST_, U_><<<g.grid, kThreads, 0, st>>>(                                  \
+            (const S*)x, rows, cols, nblk, g.per_row, g.per_wave, t.lut, t.band, t.rev, seed, seed_dev, offset, \
+            exps, codes, signs, (S*)fq)
+        if (g.u == 4) {
+            if (stochastic) AXS6_QROWS(true, 4);
+            else AXS6_QROWS(false, 4);
+        } else {
+            if (stochastic) AXS6_QROWS(true, 1);
+            else AXS6_QROWS(false, 1);
+        }
+#undef AXS6_QROWS
+        return;
+    }
     const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));
     if (stochastic)
         quantize_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, seed, seed_dev, offset, exps, codes, signs, (S*)fq);
@@ -629,6 +781,16 @@ extern "C" int axs6_nf5_dequantize(const uint8_t* exponents, const uint8_t* code
         const int64_t n4 = rows * cols / 4;
         dequantize_vec_kernel<<<dim3((unsigned)capped_grid(n4, kThreads)), kThreads, 0, (hipStream_t)stream>>>(
             exponents, codes, signs, y, n4, block_size, t.codebook);
+        return check_launch(fn);
+    }
+    if (cols >= kRowsMinCols) {
+        const RowSegs g = row_segs(rows, cols, cols >= 4 * kRowsMinCols ? 4 : 1);
+        if (g.u == 4)
+            dequantize_rows_kernel<4><<<g.grid, kThreads, 0, (hipStream_t)stream>>>(
+                exponents, codes, signs, y, rows, cols, nblk, block_size, g.per_row, g.per_wave, t.codebook);
+        else
+            dequantize_rows_kernel<1><<<g.grid, kThreads, 0, (hipStream_t)stream>>>(
+                exponents, codes, signs, y, rows, cols, nblk, block_size, g.per_row, g.per_wave, t.codebook);
         return check_launch(fn);
     }
     const dim3 grid((unsigned)capped_grid(rows * cols, kThreads));

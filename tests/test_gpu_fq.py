@@ -347,3 +347,54 @@ def test_rows_kernel_stochastic_given_stream(bs):
     got = _fq(x.to(DEV), bs, "stochastic", seed=seed).cpu().numpy()
     want = oracle.fake_quantize(x.numpy(), bs, oracle.uniform(seed, 0, x.numel()))
     assert bits_equal(got, want), first_mismatch(got, want)
+
+
+# Row-segment quantize / dequantize (quantize_rows_kernel,
+# dequantize_rows_kernel): ragged rows of >= 64 values, padded-layout codes.
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+@pytest.mark.parametrize("shape", [(300, 4100), (129, 777), (16, 2049)], ids=str)
+def test_quantize_rows_kernel(dt, bs, shape):
+    from axs.unified.hip_kernels import hip_dequantize, hip_quantize
+
+    print(f"[quantize rows {dt} bs={bs} {shape}]", flush=True)
+    x = config2_input(shape, 3 * bs + shape[1]).to(dt)
+    x[0, :5] = torch.tensor([float("nan"), 0.0, -0.0, 1e-40, -3e38]).to(dt)
+    xf = x.float().numpy()
+    for rounding, seed in (("nearest", None), ("stochastic", 1234)):
+        e, c, s, fq = hip_quantize(x.to(DEV), bs, rounding, with_fake_quantized=True, seed=seed)
+        u = oracle.uniform(seed, 0, x.numel()) if seed else None
+        oe, oc, os_ = oracle.quantize(xf, bs, u)
+        assert np.array_equal(e.cpu().numpy(), oe), (rounding, first_mismatch(e.cpu().numpy(), oe))
+        assert np.array_equal(c.cpu().numpy(), oc) and np.array_equal(s.cpu().numpy(), os_)
+        want = torch.from_numpy(oracle.fake_quantize(xf, bs, u)).to(dt)
+        got = fq.cpu()
+        nan = torch.isnan(want)
+        assert torch.equal(torch.isnan(got), nan)
+        bits = torch.int32 if dt == torch.float32 else torch.int16
+        assert torch.equal(got.view(bits)[~nan], want.view(bits)[~nan])
+    e, c, s, _ = hip_quantize(x.to(DEV), bs, "nearest")
+    d = hip_dequantize(e, c, s, shape[0], shape[1], bs).cpu().numpy()
+    want = oracle.dequantize(*oracle.quantize(xf, bs), shape[1], bs)
+    assert bits_equal(d, want), first_mismatch(d, want)
+
+
+def test_quantize_rows_kernel_without_optional_outputs():
+    """No signs and no FQ output on the row-segment kernel, and the dequantize
+    without signs (all values positive)."""
+    from axs import _lib
+
+    rows, cols, bs = 50, 1001, 32
+    nblk = (cols + bs - 1) // bs
+    x = config2_input((rows, cols), 17).abs().to(DEV)
+    e = torch.empty((rows, nblk), dtype=torch.uint8, device=DEV)
+    c = torch.empty((rows, nblk * bs), dtype=torch.uint8, device=DEV)
+    st = _lib.stream_of(x)
+    _lib.call("axs6_nf5_quantize", x.data_ptr(), _lib.F32, rows, cols, bs, 0, 0, 0, e.data_ptr(), c.data_ptr(),
+              None, None, None, st)
+    y = torch.empty((rows, cols), device=DEV)
+    _lib.call("axs6_nf5_dequantize", e.data_ptr(), c.data_ptr(), None, y.data_ptr(), rows, cols, bs, st)
+    torch.cuda.synchronize()
+    oe, oc, os_ = oracle.quantize(x.cpu().numpy(), bs)
+    assert np.array_equal(e.cpu().numpy(), oe) and np.array_equal(c.cpu().numpy().reshape(oc.shape), oc)
+    assert bits_equal(y.cpu().numpy(), oracle.dequantize(oe, oc, os_, cols, bs))
