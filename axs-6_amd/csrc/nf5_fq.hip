@@ -525,7 +525,10 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(
     }
 }
 
-template <int U>
+// Dequantize rows: the codes and signs of a row start at r * cpad, a
+// multiple of 8 bytes, so a lane reads its four consecutive codes and signs
+// as one 4-byte load each (four values per lane, 256 per wave segment) and
+// writes the values it has inside the row.
 __global__ __launch_bounds__(kThreads) void dequantize_rows_kernel(const uint8_t* __restrict__ exps,
                                                                    const uint8_t* __restrict__ codes,
                                                                    const uint8_t* __restrict__ signs,
@@ -533,7 +536,7 @@ __global__ __launch_bounds__(kThreads) void dequantize_rows_kernel(const uint8_t
                                                                    int64_t nblk, int bs, int64_t segs_per_row,
                                                                    int64_t segs_per_wave,
                                                                    const float* __restrict__ cb_g) {
-    constexpr int SEG = 64 * U;
+    constexpr int SEG = 256;
     __shared__ float cb[kLevels];
     if (threadIdx.x < kLevels) cb[threadIdx.x] = cb_g[threadIdx.x];
     __syncthreads();
@@ -548,20 +551,17 @@ __global__ __launch_bounds__(kThreads) void dequantize_rows_kernel(const uint8_t
     int64_t r = seg / segs_per_row;
     int64_t sx = seg - r * segs_per_row;
     for (; seg < end; ++seg) {
-        uint8_t cd[U], sg[U], ex[U];
+        const int64_t c = sx * SEG + 4 * lane;
+        if (c < cols) {
+            const uint32_t cw = *reinterpret_cast<const uint32_t*>(codes + r * cpad + c);
+            const uint32_t sw = signs ? *reinterpret_cast<const uint32_t*>(signs + r * cpad + c) : 0u;
+            const float scale = pow2_float((int)exps[r * nblk + (c >> sh)] - kExpBias);
+            float* yr = y + r * cols + c;
 #pragma unroll
-        for (int k = 0; k < U; ++k) {
-            const int64_t c = sx * SEG + lane + 64 * k;
-            const bool in = c < cols;
-            cd[k] = in ? codes[r * cpad + c] : 0;
-            sg[k] = (in && signs) ? signs[r * cpad + c] : 0;
-            ex[k] = in ? exps[r * nblk + (c >> sh)] : 0;
-        }
-#pragma unroll
-        for (int k = 0; k < U; ++k) {
-            const int64_t c = sx * SEG + lane + 64 * k;
-            const float a = cb[cd[k] & 31] * pow2_float((int)ex[k] - kExpBias);
-            if (c < cols) y[r * cols + c] = sg[k] ? -a : a;
+            for (int e = 0; e < 4; ++e) {
+                const float a = cb[(cw >> (8 * e)) & 31] * scale;
+                if (c + e < cols) yr[e] = ((sw >> (8 * e)) & 0xffu) ? -a : a;
+            }
         }
         if (++sx == segs_per_row) {
             sx = 0;
@@ -783,14 +783,10 @@ extern "C" int axs6_nf5_dequantize(const uint8_t* exponents, const uint8_t* code
             exponents, codes, signs, y, n4, block_size, t.codebook);
         return check_launch(fn);
     }
-    if (cols >= kRowsMinCols) {
-        const RowSegs g = row_segs(rows, cols, cols >= 4 * kRowsMinCols ? 4 : 1);
-        if (g.u == 4)
-            dequantize_rows_kernel<4><<<g.grid, kThreads, 0, (hipStream_t)stream>>>(
-                exponents, codes, signs, y, rows, cols, nblk, block_size, g.per_row, g.per_wave, t.codebook);
-        else
-            dequantize_rows_kernel<1><<<g.grid, kThreads, 0, (hipStream_t)stream>>>(
-                exponents, codes, signs, y, rows, cols, nblk, block_size, g.per_row, g.per_wave, t.codebook);
+    if (cols >= kRowsMinCols && (uintptr_t)codes % 4 == 0 && (uintptr_t)signs % 4 == 0) {
+        const RowSegs g = row_segs(rows, cols, 4);
+        dequantize_rows_kernel<<<g.grid, kThreads, 0, (hipStream_t)stream>>>(
+            exponents, codes, signs, y, rows, cols, nblk, block_size, g.per_row, g.per_wave, t.codebook);
         return check_launch(fn);
     }
     const dim3 grid((unsigned)capped_grid(rows * cols, kThreads));
