@@ -21,11 +21,14 @@
 // LUT and the band table are staged in LDS once per workgroup and the grid
 // is capped (grid-stride loop) so that staging is amortised.
 // Row path (rows of >= 64 values with a ragged last block, or unaligned
-// views): one element per lane in row order, a block is `block` neighbouring
-// lanes (DPP / permlane maximum), rows cut into segments of 64 or 256
-// values, the next segment's loads in flight (fq_rows_kernel).  Shorter
-// rows: one block per lane group with shuffle reductions (fq_scalar_kernel).
+// views): four values (or one) per lane in row order, a block is
+// `block` / 4 (or `block`) neighbouring lanes (DPP / permlane maximum), rows
+// cut into segments of 256 (or 64) values, the next segment's loads in
+// flight (fq_rows_kernel).  Shorter rows: one block per lane group with
+// shuffle reductions (fq_scalar_kernel).
 #include <math.h>
+
+#include <type_traits>
 
 #pragma clang fp contract(off)
 
@@ -144,16 +147,32 @@ __global__ __launch_bounds__(kThreads) void fq_scalar_kernel(const typename Elem
     }
 }
 
+// Four consecutive values at p (aligned to four values) from floats.
+template <int DT>
+__device__ __forceinline__ void store4(typename Elem<DT>::S* p, const float (&f)[4]) {
+    using E = Elem<DT>;
+    if constexpr (DT == AXS6_F32) {
+        *reinterpret_cast<u32x4*>(p) = E::pack(f);
+    } else {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const float g[8] = {f[0], f[1], f[2], f[3], 0.0f, 0.0f, 0.0f, 0.0f};
+        const u32x4 w = E::pack(g);
+        *reinterpret_cast<u32x2*>(p) = u32x2{w.x, w.y};
+    }
+}
+
 // Rows that do not tile into 16-byte vectors of whole blocks (a ragged last
-// block, or row starts off 16-byte alignment): one element per lane, lanes
-// in row order, so a block is BS neighbouring lanes and its maximum a DPP /
-// permlane reduction, and every load or store instruction covers 64
-// consecutive elements of one row.  A row is cut into segments of 64 * U
-// elements (a multiple of BS, so blocks never straddle segments); each wave
-// walks a contiguous range of segments, stepping its row index instead of
-// dividing per element.  Lanes past the row's end read 0 -- the reference's
-// zero padding of the last block -- and store nothing.
-template <int DT, int BS, bool STOCH, int U>
+// block, or row starts off 16-byte alignment): VL values per lane (4 when
+// the row length is a multiple of 4 and the pointers allow 4-value loads,
+// else 1), lanes in row order, so a block is BS / VL neighbouring lanes and
+// its maximum a DPP (and, for 32 lanes, permlane) reduction; a load or store
+// instruction covers 64 * VL consecutive values of one row.  A row is cut
+// into segments of 64 * VL * U values (a multiple of BS, so blocks never
+// straddle segments); each wave walks a contiguous range of segments,
+// stepping its row index instead of dividing, with the next segment's loads
+// in flight.  Lanes past the row's end read 0 -- the reference's zero
+// padding of the last block -- and store nothing.
+template <int DT, int BS, bool STOCH, int U, int VL>
 __global__ __launch_bounds__(kThreads) void fq_rows_kernel(const typename Elem<DT>::S* __restrict__ x,
                                                            typename Elem<DT>::S* __restrict__ y, int64_t rows,
                                                            int64_t cols, int64_t segs_per_row, int64_t segs_per_wave,
@@ -161,8 +180,9 @@ __global__ __launch_bounds__(kThreads) void fq_rows_kernel(const typename Elem<D
                                                            const uint8_t* __restrict__ band_g, uint64_t seed,
                                                            const uint64_t* __restrict__ seed_dev, uint64_t offset) {
     using E = Elem<DT>;
-    constexpr int SEG = 64 * U;
-    static_assert(SEG % BS == 0, "segments hold whole blocks");
+    constexpr int SEG = 64 * VL * U;
+    static_assert(VL == 1 || VL == 4, "values per lane");
+    static_assert(SEG % BS == 0 && BS % VL == 0, "segments hold whole blocks");
     const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
@@ -177,40 +197,68 @@ __global__ __launch_bounds__(kThreads) void fq_rows_kernel(const typename Elem<D
     if (seg >= end) return;
     int64_t r = seg / segs_per_row;
     int64_t sx = seg - r * segs_per_row;
-    // the next segment's loads go out before the current one is processed
-    typename E::S raw[U];
+    // raw words of segment (row rr, index ss) for this lane, zero past the
+    // row's end; converted to floats only when the segment is processed, so
+    // the loads of the next segment stay in flight meanwhile
+    using Raw = typename std::conditional<VL == 1, typename E::S, u32x4>::type;
+    auto load_seg = [&](int64_t rr, int64_t ss, Raw (&w)[U]) {
 #pragma unroll
-    for (int k = 0; k < U; ++k) {
-        const int64_t c = sx * SEG + lane + 64 * k;
-        raw[k] = c < cols ? x[r * cols + c] : (typename E::S)0;
-    }
+        for (int k = 0; k < U; ++k) {
+            const int64_t c = ss * SEG + VL * lane + 64 * VL * k;
+            if constexpr (VL == 1) {
+                w[k] = c < cols ? x[rr * cols + c] : (typename E::S)0;
+            } else if constexpr (DT == AXS6_F32) {
+                w[k] = c < cols ? *reinterpret_cast<const u32x4*>(x + rr * cols + c) : u32x4{0u, 0u, 0u, 0u};
+            } else {
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                const u32x2 h = c < cols ? *reinterpret_cast<const u32x2*>(x + rr * cols + c) : u32x2{0u, 0u};
+                w[k] = u32x4{h.x, h.y, 0u, 0u};
+            }
+        }
+    };
+    Raw nw[U];
+    load_seg(r, sx, nw);
     for (; seg < end; ++seg) {
         const int64_t base = r * cols;
-        const int64_t c0 = sx * SEG + lane;
-        float f[U];
+        float f[U][VL];
 #pragma unroll
-        for (int k = 0; k < U; ++k) f[k] = E::to_f(raw[k]);
+        for (int k = 0; k < U; ++k) {
+            if constexpr (VL == 1) {
+                f[k][0] = E::to_f(nw[k]);
+            } else {
+                float g[E::V];
+                E::unpack(nw[k], g);
+#pragma unroll
+                for (int e = 0; e < VL; ++e) f[k][e] = g[e];
+            }
+        }
         int64_t rn = r, sn = sx + 1;
         if (sn == segs_per_row) {
             sn = 0;
             ++rn;
         }
-        if (seg + 1 < end) {
-#pragma unroll
-            for (int k = 0; k < U; ++k) {
-                const int64_t c = sn * SEG + lane + 64 * k;
-                raw[k] = c < cols ? x[rn * cols + c] : (typename E::S)0;
-            }
-        }
+        if (seg + 1 < end) load_seg(rn, sn, nw);
 #pragma unroll
         for (int k = 0; k < U; ++k) {
-            const int64_t c = c0 + 64 * k;
-            const uint32_t m = lanes_umax<BS>(__float_as_uint(f[k]) & 0x7fffffffu);
+            const int64_t c = sx * SEG + VL * lane + 64 * VL * k;
+            uint32_t a = 0;
+#pragma unroll
+            for (int e = 0; e < VL; ++e) {
+                const uint32_t b = __float_as_uint(f[k][e]) & 0x7fffffffu;
+                a = a > b ? a : b;
+            }
+            uint32_t m;
+            if constexpr (VL == 1) m = lanes_umax<BS>(a);
+            else m = group_umax<BS / VL>(a);
             const FqScale s = fq_scale(m, band_s);
-            float v[1] = {f[k]};
-            const float d[1] = {STOCH ? dither_step(key, offset + (uint64_t)(base + c)) : 0.0f};
-            fq_vector<1>(v, s, lut_s, STOCH, d);
-            if (c < cols) y[base + c] = E::from_f(v[0]);
+            float d[VL];
+#pragma unroll
+            for (int e = 0; e < VL; ++e) d[e] = STOCH ? dither_step(key, offset + (uint64_t)(base + c + e)) : 0.0f;
+            fq_vector<VL>(f[k], s, lut_s, STOCH, d);
+            if (c < cols) {
+                if constexpr (VL == 1) y[base + c] = E::from_f(f[k][0]);
+                else store4<DT>(y + base + c, f[k]);
+            }
         }
         r = rn;
         sx = sn;
@@ -602,7 +650,7 @@ int64_t capped_grid(int64_t work_items, int64_t per_wg) {
 // them per wave, sized for about kRowsWavesPerCu waves per CU and at least
 // kRowsMinSegs segments per wave (the tables are staged once per workgroup).
 constexpr int64_t kRowsMinCols = 64;
-constexpr int64_t kRowsWavesPerCu = 32;
+constexpr int64_t kRowsWavesPerCu = 64;
 constexpr int64_t kRowsMinSegs = 2;
 
 struct RowSegs {
@@ -638,18 +686,22 @@ void launch_fq_typed(const void* x, void* y, int64_t rows, int64_t cols, bool st
         else
             fq_vec_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, seed, seed_dev, offset);
     } else if (cols >= kRowsMinCols) {
-        const RowSegs g = row_segs(rows, cols, cols >= 4 * kRowsMinCols ? 4 : 1);
-        if (g.u == 4) {
-            if (stochastic)
-                fq_rows_kernel<DT, BS, true, 4><<<g.grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, g.per_row, g.per_wave, t.lut, t.band, seed, seed_dev, offset);
-            else
-                fq_rows_kernel<DT, BS, false, 4><<<g.grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, g.per_row, g.per_wave, t.lut, t.band, seed, seed_dev, offset);
-        } else {
-            if (stochastic)
-                fq_rows_kernel<DT, BS, true, 1><<<g.grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, g.per_row, g.per_wave, t.lut, t.band, seed, seed_dev, offset);
-            else
-                fq_rows_kernel<DT, BS, false, 1><<<g.grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, g.per_row, g.per_wave, t.lut, t.band, seed, seed_dev, offset);
-        }
+        const int esize = (int)sizeof(S);
+        const bool four = cols % 4 == 0 && (uintptr_t)x % (4 * esize) == 0 && (uintptr_t)y % (4 * esize) == 0;
+#define AXS6_FQROWS(U_, VL_)                                                                                   \
+        do {                                                                                                   \
+            const RowSegs g = row_segs(rows, cols, (U_) * (VL_));                                              \
+            if (stochastic)                                                                                    \
+                fq_rows_kernel<DT, BS, true, U_, VL_><<<g.grid, kThreads, 0, st>>>(                            \
+                    (const S*)x, (S*)y, rows, cols, g.per_row, g.per_wave, t.lut, t.band, seed, seed_dev, offset); \
+            else                                                                                               \
+                fq_rows_kernel<DT, BS, false, U_, VL_><<<g.grid, kThreads, 0, st>>>(                           \
+                    (const S*)x, (S*)y, rows, cols, g.per_row, g.per_wave, t.lut, t.band, seed, seed_dev, offset); \
+        } while (0)
+        if (four) AXS6_FQROWS(1, 4);
+        else if (cols >= 4 * kRowsMinCols) AXS6_FQROWS(4, 1);
+        else AXS6_FQROWS(1, 1);
+#undef AXS6_FQROWS
     } else {
         const int64_t nblk = (cols + BS - 1) / BS;
         const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));
