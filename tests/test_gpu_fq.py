@@ -333,16 +333,19 @@ def test_rows_kernel_exponent_range():
     while len(blocks) % 4:
         blocks.append(rng.standard_normal(32).astype(np.float32))
     wide = np.stack(blocks).reshape(-1, 128)
-    x = np.concatenate([wide, rng.standard_normal((wide.shape[0], 7)).astype(np.float32)], axis=1)
-    for bs in (8, 16, 32):
-        got = _fq(torch.from_numpy(x).to(DEV), bs).cpu().numpy()
-        want = oracle.fake_quantize(x, bs)
-        assert bits_equal(got, want), (bs, first_mismatch(got, want))
+    # 7 extra values: one value per lane; 8: four per lane (rows of 136)
+    for extra in (7, 8):
+        x = np.concatenate([wide, rng.standard_normal((wide.shape[0], extra)).astype(np.float32)], axis=1)
+        for bs in (8, 16, 32):
+            got = _fq(torch.from_numpy(x).to(DEV), bs).cpu().numpy()
+            want = oracle.fake_quantize(x, bs)
+            assert bits_equal(got, want), (extra, bs, first_mismatch(got, want))
 
 
 @pytest.mark.parametrize("bs", [8, 32])
-def test_rows_kernel_stochastic_given_stream(bs):
-    x = config2_input((200, 1030), 55)
+@pytest.mark.parametrize("cols", [1030, 1032], ids=["one-per-lane", "four-per-lane"])
+def test_rows_kernel_stochastic_given_stream(bs, cols):
+    x = config2_input((200, cols), 55)
     seed = 0x5EED0F00D
     got = _fq(x.to(DEV), bs, "stochastic", seed=seed).cpu().numpy()
     want = oracle.fake_quantize(x.numpy(), bs, oracle.uniform(seed, 0, x.numel()))
