@@ -501,7 +501,7 @@ __global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t* __r
 // and segment layout of fq_rows_kernel over the padded row (cpad = nblk * BS
 // values: the codes and signs of the padding positions are written too, as
 // quantize_kernel writes them), one value per lane.
-template <int DT, int BS, bool STOCH, int U>
+template <int DT, int BS, bool STOCH, int U, int VL>
 __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(
     const typename Elem<DT>::S* __restrict__ x, int64_t rows, int64_t cols, int64_t nblk, int64_t segs_per_row,
     int64_t segs_per_wave, const float* __restrict__ lut_g, const uint8_t* __restrict__ band_g,
@@ -509,8 +509,9 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(
     uint8_t* __restrict__ exps, uint8_t* __restrict__ codes, uint8_t* __restrict__ signs,
     typename Elem<DT>::S* __restrict__ fq) {
     using E = Elem<DT>;
-    constexpr int SEG = 64 * U;
-    static_assert(SEG % BS == 0, "segments hold whole blocks");
+    constexpr int SEG = 64 * VL * U;
+    static_assert(VL == 1 || VL == 4, "values per lane");
+    static_assert(SEG % BS == 0 && BS % VL == 0, "segments hold whole blocks");
     const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
@@ -528,45 +529,77 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(
     if (seg >= end) return;
     int64_t r = seg / segs_per_row;
     int64_t sx = seg - r * segs_per_row;
-    typename E::S raw[U];
+    // raw words of the next segment in flight while the current one is processed
+    using Raw = typename std::conditional<VL == 1, typename E::S, u32x4>::type;
+    auto load_seg = [&](int64_t rr, int64_t ss, Raw (&w)[U]) {
 #pragma unroll
-    for (int k = 0; k < U; ++k) {
-        const int64_t c = sx * SEG + lane + 64 * k;
-        raw[k] = c < cols ? x[r * cols + c] : (typename E::S)0;
-    }
+        for (int k = 0; k < U; ++k) {
+            const int64_t c = ss * SEG + VL * lane + 64 * VL * k;
+            if constexpr (VL == 1) {
+                w[k] = c < cols ? x[rr * cols + c] : (typename E::S)0;
+            } else if constexpr (DT == AXS6_F32) {
+                w[k] = c < cols ? *reinterpret_cast<const u32x4*>(x + rr * cols + c) : u32x4{0u, 0u, 0u, 0u};
+            } else {
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                const u32x2 h = c < cols ? *reinterpret_cast<const u32x2*>(x + rr * cols + c) : u32x2{0u, 0u};
+                w[k] = u32x4{h.x, h.y, 0u, 0u};
+            }
+        }
+    };
+    Raw nw[U];
+    load_seg(r, sx, nw);
     for (; seg < end; ++seg) {
         const int64_t base = r * cols;
-        const int64_t c0 = sx * SEG + lane;
-        float f[U];
+        float f[U][VL];
 #pragma unroll
-        for (int k = 0; k < U; ++k) f[k] = E::to_f(raw[k]);
+        for (int k = 0; k < U; ++k) {
+            if constexpr (VL == 1) {
+                f[k][0] = E::to_f(nw[k]);
+            } else {
+                float g[E::V];
+                E::unpack(nw[k], g);
+#pragma unroll
+                for (int e = 0; e < VL; ++e) f[k][e] = g[e];
+            }
+        }
         int64_t rn = r, sn = sx + 1;
         if (sn == segs_per_row) {
             sn = 0;
             ++rn;
         }
-        if (seg + 1 < end) {
-#pragma unroll
-            for (int k = 0; k < U; ++k) {
-                const int64_t c = sn * SEG + lane + 64 * k;
-                raw[k] = c < cols ? x[rn * cols + c] : (typename E::S)0;
-            }
-        }
+        if (seg + 1 < end) load_seg(rn, sn, nw);
 #pragma unroll
         for (int k = 0; k < U; ++k) {
-            const int64_t c = c0 + 64 * k;
-            const uint32_t m = lanes_umax<BS>(__float_as_uint(f[k]) & 0x7fffffffu);
-            float v[1] = {f[k]};
-            const float d[1] = {STOCH ? dither_step(key, offset + (uint64_t)(base + c)) : 0.0f};
+            const int64_t c = sx * SEG + VL * lane + 64 * VL * k;
+            uint32_t a = 0;
+#pragma unroll
+            for (int e = 0; e < VL; ++e) {
+                const uint32_t b = __float_as_uint(f[k][e]) & 0x7fffffffu;
+                a = a > b ? a : b;
+            }
+            uint32_t m;
+            if constexpr (VL == 1) m = lanes_umax<BS>(a);
+            else m = group_umax<BS / VL>(a);
+            float d[VL];
+#pragma unroll
+            for (int e = 0; e < VL; ++e) d[e] = STOCH ? dither_step(key, offset + (uint64_t)(base + c + e)) : 0.0f;
             uint32_t cw[2], sw[2];
-            const int ex = quant_values<1, STOCH>(v, m, d, lut_s, band_s, rev_s, fq != nullptr, cw, sw);
+            const int ex = quant_values<VL, STOCH>(f[k], m, d, lut_s, band_s, rev_s, fq != nullptr, cw, sw);
             if (c < cpad) {
                 const int64_t o = r * cpad + c;
-                codes[o] = (uint8_t)cw[0];
-                if (signs) signs[o] = (uint8_t)sw[0];
+                if constexpr (VL == 1) {
+                    codes[o] = (uint8_t)cw[0];
+                    if (signs) signs[o] = (uint8_t)sw[0];
+                } else {
+                    *reinterpret_cast<uint32_t*>(codes + o) = cw[0];
+                    if (signs) *reinterpret_cast<uint32_t*>(signs + o) = sw[0];
+                }
                 if (c % BS == 0) exps[r * nblk + c / BS] = (uint8_t)ex;
             }
-            if (fq && c < cols) fq[base + c] = E::from_f(v[0]);
+            if (fq && c < cols) {
+                if constexpr (VL == 1) fq[base + c] = E::from_f(f[k][0]);
+                else store4<DT>(fq + base + c, f[k]);
+            }
         }
         r = rn;
         sx = sn;
@@ -739,18 +772,24 @@ void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochast
     const int64_t nblk = (cols + BS - 1) / BS;
     const int64_t cpad = nblk * BS;
     if (cpad >= kRowsMinCols) {
-        const RowSegs g = row_segs(rows, cpad, cpad >= 4 * kRowsMinCols ? 4 : 1);
-#define AXS6_QROWS(ST_, U_)                                                                                  \
-        quantize_rows_kernel<DT, BS, ST_, U_><<<g.grid, kThreads, 0, st>>>(                                  \
-            (const S*)x, rows, cols, nblk, g.per_row, g.per_wave, t.lut, t.band, t.rev, seed, seed_dev, offset, \
-            exps, codes, signs, (S*)fq)
-        if (g.u == 4) {
-            if (stochastic) AXS6_QROWS(true, 4);
-            else AXS6_QROWS(false, 4);
-        } else {
-            if (stochastic) AXS6_QROWS(true, 1);
-            else AXS6_QROWS(false, 1);
-        }
+        const int esize = (int)sizeof(S);
+        const bool four = cols % 4 == 0 && (uintptr_t)x % (4 * esize) == 0 && (uintptr_t)fq % (4 * esize) == 0 &&
+                          (uintptr_t)codes % 4 == 0 && (uintptr_t)signs % 4 == 0;
+#define AXS6_QROWS(U_, VL_)                                                                                  \
+        do {                                                                                                 \
+            const RowSegs g = row_segs(rows, cpad, (U_) * (VL_));                                            \
+            if (stochastic)                                                                                  \
+                quantize_rows_kernel<DT, BS, true, U_, VL_><<<g.grid, kThreads, 0, st>>>(                    \
+                    (const S*)x, rows, cols, nblk, g.per_row, g.per_wave, t.lut, t.band, t.rev, seed, seed_dev, \
+                    offset, exps, codes, signs, (S*)fq);                                                     \
+            else                                                                                             \
+                quantize_rows_kernel<DT, BS, false, U_, VL_><<<g.grid, kThreads, 0, st>>>(                   \
+                    (const S*)x, rows, cols, nblk, g.per_row, g.per_wave, t.lut, t.band, t.rev, seed, seed_dev, \
+                    offset, exps, codes, signs, (S*)fq);                                                     \
+        } while (0)
+        if (four) AXS6_QROWS(1, 4);
+        else if (cpad >= 4 * kRowsMinCols) AXS6_QROWS(4, 1);
+        else AXS6_QROWS(1, 1);
 #undef AXS6_QROWS
         return;
     }
