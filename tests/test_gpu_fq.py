@@ -382,12 +382,13 @@ def test_quantize_rows_kernel(dt, bs, shape):
     assert bits_equal(d, want), first_mismatch(d, want)
 
 
-def test_quantize_rows_kernel_without_optional_outputs():
+@pytest.mark.parametrize("cols", [1001, 1004], ids=["one-per-lane", "four-per-lane"])
+def test_quantize_rows_kernel_without_optional_outputs(cols):
     """No signs and no FQ output on the row-segment kernel, and the dequantize
     without signs (all values positive)."""
     from axs import _lib
 
-    rows, cols, bs = 50, 1001, 32
+    rows, bs = 50, 32
     nblk = (cols + bs - 1) // bs
     x = config2_input((rows, cols), 17).abs().to(DEV)
     e = torch.empty((rows, nblk), dtype=torch.uint8, device=DEV)
