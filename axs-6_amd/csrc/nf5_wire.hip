@@ -27,8 +27,11 @@
 // groups in LDS -- 800, 832 or 896 bytes per tile for bs 32, 16, 8, each a
 // multiple of 16 -- and writes them as whole 16-byte vectors.  Unpacking
 // reverses it: 16-byte record loads into LDS, one 16-byte f32 store per
-// group.  Ragged rows (the virtual zero padding) and unaligned pointers take
-// the general kernels, one group per thread with byte accesses.
+// group.  Ragged rows (the virtual zero padding) and values off 4-value
+// alignment keep these record tiles -- the record stream is the same run of
+// whole blocks -- and read or write the values by row geometry (RowGeom);
+// only a buffer off 16-byte alignment takes the general kernels, one group
+// per thread with byte accesses.
 #include "nf5_device.h"
 
 namespace axs6 {
@@ -168,11 +171,53 @@ __device__ __forceinline__ void load_group(const typename Elem<DT>::S* x, int64_
     }
 }
 
+// Rows that do not tile into whole blocks (a ragged last block) or whose
+// values are not aligned to 4-value groups: the record stream is the same
+// run of whole blocks over the zero-padded rows (gpr = groups per padded
+// row), so the fast kernels keep their record tiles and only the values'
+// side changes.  Group q holds values 4 * (q % gpr) .. + 3 of row q / gpr;
+// the row of a tile's first group comes from one wave-uniform division and
+// each lane steps forward over whole rows from it.
+struct RowGeom {
+    int64_t cols, gpr;
+    bool vec4;      // cols % 4 == 0 and the tensor aligned to 4 values: one load/store per group
+};
+
+__device__ __forceinline__ void group_pos(int64_t q, int64_t qt, const RowGeom& rg, int64_t& r, int64_t& c) {
+    const uint64_t u = (uint64_t)qt;
+    const int64_t qs = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(u >> 32)) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u));
+    r = qs / rg.gpr;
+    int64_t qq = q - r * rg.gpr;
+    while (qq >= rg.gpr) {
+        qq -= rg.gpr;
+        ++r;
+    }
+    c = 4 * qq;
+}
+
+template <int DT>
+__device__ __forceinline__ void load_group_rows(const typename Elem<DT>::S* x, int64_t q, int64_t qt,
+                                                const RowGeom& rg, float (&f)[4]) {
+    using E = Elem<DT>;
+    int64_t r, c;
+    group_pos(q, qt, rg, r, c);
+    const typename E::S* p = x + r * rg.cols + c;
+    if (rg.vec4 && c + 4 <= rg.cols) {
+        load_group<DT>(p, 0, f);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = c + e < rg.cols ? E::to_f(p[e]) : 0.0f;
+    }
+}
+
 // Fast-path pack: groups = rows * cols / 4 with cols % BS == 0; x aligned to
 // its 4-value group, buf to 16 bytes.  Same record bytes as wire_pack_kernel.
-template <int HB, int DT, int BS>
+// ROWS: any rows, values read through RowGeom (buf still 16-byte aligned).
+template <int HB, int DT, int BS, bool ROWS>
 __global__ __launch_bounds__(kThreads) void wire_pack_vec_kernel(const typename Elem<DT>::S* __restrict__ x,
-                                                                 int64_t groups, const uint8_t* __restrict__ band_g,
+                                                                 int64_t groups, RowGeom rg,
+                                                                 const uint8_t* __restrict__ band_g,
                                                                  const uint8_t* __restrict__ rev_g,
                                                                  uint8_t* __restrict__ buf) {
     constexpr int GPB = BS / 4;
@@ -197,9 +242,14 @@ __global__ __launch_bounds__(kThreads) void wire_pack_vec_kernel(const typename 
         float f[U][4];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t q = (t0 + u) * kThreads + tid;
-            if (q < groups) load_group<DT>(x, q, f[u]);
-            else f[u][0] = f[u][1] = f[u][2] = f[u][3] = 0.0f;
+            const int64_t qt = (t0 + u) * kThreads;
+            const int64_t q = qt + tid;
+            if (q < groups) {
+                if constexpr (ROWS) load_group_rows<DT>(x, q, qt, rg, f[u]);
+                else load_group<DT>(x, q, f[u]);
+            } else {
+                f[u][0] = f[u][1] = f[u][2] = f[u][3] = 0.0f;
+            }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -233,9 +283,9 @@ __global__ __launch_bounds__(kThreads) void wire_pack_vec_kernel(const typename 
 }
 
 // Fast-path unpack, the inverse geometry: y [groups * 4] f32 (16-byte aligned), buf 16-byte aligned.
-template <int HB, int BS>
+template <int HB, int BS, bool ROWS>
 __global__ __launch_bounds__(kThreads) void wire_unpack_vec_kernel(const uint8_t* __restrict__ buf, int64_t groups,
-                                                                   const float* __restrict__ cb_g,
+                                                                   RowGeom rg, const float* __restrict__ cb_g,
                                                                    float* __restrict__ y) {
     constexpr int GPB = BS / 4;
     constexpr int REC = HB + BS * 3 / 4;
@@ -265,7 +315,8 @@ __global__ __launch_bounds__(kThreads) void wire_unpack_vec_kernel(const uint8_t
         __syncthreads();   // records (and, the first time, the codebook) staged
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t q = (t0 + u) * kThreads + tid;
+            const int64_t qt = (t0 + u) * kThreads;
+            const int64_t q = qt + tid;
             if (q < groups) {
                 const uint8_t* r = rec + u * TB;
                 const float scale = pow2_float(get_exponent<HB>(r) - kExpBias);
@@ -280,7 +331,20 @@ __global__ __launch_bounds__(kThreads) void wire_unpack_vec_kernel(const uint8_t
                 u32x4 w;
                 w.x = __float_as_uint(v[0]); w.y = __float_as_uint(v[1]);
                 w.z = __float_as_uint(v[2]); w.w = __float_as_uint(v[3]);
-                *reinterpret_cast<u32x4*>(y + q * 4) = w;
+                if constexpr (ROWS) {
+                    int64_t row, c;
+                    group_pos(q, qt, rg, row, c);
+                    float* p = y + row * rg.cols + c;
+                    if (rg.vec4 && c + 4 <= rg.cols) {
+                        *reinterpret_cast<u32x4*>(p) = w;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (c + e < rg.cols) p[e] = v[e];
+                    }
+                } else {
+                    *reinterpret_cast<u32x4*>(y + q * 4) = w;
+                }
             }
         }
         __syncthreads();   // recs is rewritten by the next iteration
@@ -391,16 +455,24 @@ int64_t record_bytes(int hb, int64_t rows, int64_t cols, int bs) {
     return rows * nblk * (hb + bs * 3 / 4);
 }
 
+// vec: whole-block rows, x aligned to 4 values, buf to 16 bytes; rows: any
+// rows with buf aligned to 16 bytes (the fast kernels' row-geometry mode).
 template <int HB, int DT>
-void launch_pack(const void* x, const WireGeom& g, int bs, bool vec, const DeviceTables& t, uint8_t* buf,
-                 hipStream_t st) {
+void launch_pack(const void* x, const WireGeom& g, int bs, bool vec, bool rows, const RowGeom& rg,
+                 const DeviceTables& t, uint8_t* buf, hipStream_t st) {
     using S = typename Elem<DT>::S;
     const S* xs = (const S*)x;
-    if (vec) {
+    if (vec || rows) {
         const dim3 grid(wire_vec_grid(g.groups));
-        if (bs == 8) wire_pack_vec_kernel<HB, DT, 8><<<grid, kThreads, 0, st>>>(xs, g.groups, t.band, t.rev, buf);
-        else if (bs == 16) wire_pack_vec_kernel<HB, DT, 16><<<grid, kThreads, 0, st>>>(xs, g.groups, t.band, t.rev, buf);
-        else wire_pack_vec_kernel<HB, DT, 32><<<grid, kThreads, 0, st>>>(xs, g.groups, t.band, t.rev, buf);
+#define AXS6_WPACK(R_)                                                                                                 \
+        do {                                                                                                           \
+            if (bs == 8) wire_pack_vec_kernel<HB, DT, 8, R_><<<grid, kThreads, 0, st>>>(xs, g.groups, rg, t.band, t.rev, buf);   \
+            else if (bs == 16) wire_pack_vec_kernel<HB, DT, 16, R_><<<grid, kThreads, 0, st>>>(xs, g.groups, rg, t.band, t.rev, buf); \
+            else wire_pack_vec_kernel<HB, DT, 32, R_><<<grid, kThreads, 0, st>>>(xs, g.groups, rg, t.band, t.rev, buf); \
+        } while (0)
+        if (vec) AXS6_WPACK(false);
+        else AXS6_WPACK(true);
+#undef AXS6_WPACK
     } else {
         const dim3 grid(wire_grid(g.groups));
         if (bs == 8) wire_pack_kernel<HB, DT, 8><<<grid, kThreads, 0, st>>>(xs, g, t.band, t.rev, buf);
@@ -423,11 +495,14 @@ int pack_records(const char* fn, const void* x, int dtype, int64_t rows, int64_t
     const int64_t nblk = (cols + bs - 1) / bs;
     const WireGeom g{rows, cols, nblk, rows * nblk * (bs / 4)};
     const int esize = dtype == AXS6_F32 ? 4 : 2;
-    const bool vec = cols % bs == 0 && (uintptr_t)x % (4 * esize) == 0 && (uintptr_t)buffer % 16 == 0;
+    const bool xal = (uintptr_t)x % (4 * esize) == 0;
+    const bool vec = cols % bs == 0 && xal && (uintptr_t)buffer % 16 == 0;
+    const bool rows_mode = !vec && (uintptr_t)buffer % 16 == 0;
+    const RowGeom rg{cols, nblk * (bs / 4), cols % 4 == 0 && xal};
     hipStream_t st = (hipStream_t)stream;
-    if (dtype == AXS6_F32) launch_pack<HB, AXS6_F32>(x, g, bs, vec, t, buffer, st);
-    else if (dtype == AXS6_BF16) launch_pack<HB, AXS6_BF16>(x, g, bs, vec, t, buffer, st);
-    else launch_pack<HB, AXS6_F16>(x, g, bs, vec, t, buffer, st);
+    if (dtype == AXS6_F32) launch_pack<HB, AXS6_F32>(x, g, bs, vec, rows_mode, rg, t, buffer, st);
+    else if (dtype == AXS6_BF16) launch_pack<HB, AXS6_BF16>(x, g, bs, vec, rows_mode, rg, t, buffer, st);
+    else launch_pack<HB, AXS6_F16>(x, g, bs, vec, rows_mode, rg, t, buffer, st);
     return check_launch(fn);
 }
 
@@ -444,11 +519,20 @@ int unpack_records(const char* fn, const uint8_t* buffer, int64_t rows, int64_t 
     const int64_t nblk = (cols + bs - 1) / bs;
     const WireGeom g{rows, cols, nblk, rows * nblk * (bs / 4)};
     hipStream_t st = (hipStream_t)stream;
-    if (cols % bs == 0 && (uintptr_t)y % 16 == 0 && (uintptr_t)buffer % 16 == 0) {
+    if ((uintptr_t)buffer % 16 == 0) {
+        const bool yal = (uintptr_t)y % 16 == 0;
+        const bool vec = cols % bs == 0 && yal;
+        const RowGeom rg{cols, nblk * (bs / 4), cols % 4 == 0 && yal};
         const dim3 grid(wire_vec_grid(g.groups));
-        if (bs == 8) wire_unpack_vec_kernel<HB, 8><<<grid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
-        else if (bs == 16) wire_unpack_vec_kernel<HB, 16><<<grid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
-        else wire_unpack_vec_kernel<HB, 32><<<grid, kThreads, 0, st>>>(buffer, g.groups, t.codebook, y);
+#define AXS6_WUNPACK(R_)                                                                                       \
+        do {                                                                                                   \
+            if (bs == 8) wire_unpack_vec_kernel<HB, 8, R_><<<grid, kThreads, 0, st>>>(buffer, g.groups, rg, t.codebook, y);   \
+            else if (bs == 16) wire_unpack_vec_kernel<HB, 16, R_><<<grid, kThreads, 0, st>>>(buffer, g.groups, rg, t.codebook, y); \
+            else wire_unpack_vec_kernel<HB, 32, R_><<<grid, kThreads, 0, st>>>(buffer, g.groups, rg, t.codebook, y); \
+        } while (0)
+        if (vec) AXS6_WUNPACK(false);
+        else AXS6_WUNPACK(true);
+#undef AXS6_WUNPACK
         return check_launch(fn);
     }
     const dim3 grid(wire_grid(g.groups));

@@ -54,7 +54,8 @@ def _oracle_values(x2: np.ndarray, bs: int) -> np.ndarray:
 # whole-block rows (vector kernels, with partial tiles and partial workgroup
 # iterations) and ragged rows (general kernels), as for the wire format
 @pytest.mark.parametrize("bs", [8, 16, 32])
-@pytest.mark.parametrize("shape", [(64, 256), (300, 512), (7, 96), (37, 100), (5, 33), (1, 8)], ids=str)
+@pytest.mark.parametrize("shape", [(64, 256), (300, 512), (7, 96), (37, 100), (5, 33), (1, 8),
+                                   (300, 4100), (129, 777)], ids=str)
 def test_encode_decode_bitexact(bs, shape):
     from axs.blocks import decode_blocks, encode_blocks
 

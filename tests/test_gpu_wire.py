@@ -48,9 +48,12 @@ def _oracle_buffer(x2: np.ndarray, bs: int) -> np.ndarray:
 # (64, 256), (300, 512), (7, 96), (1, 8): rows tile into whole blocks (the
 # vector kernels; 300 x 512 ends in a partial workgroup iteration, 7 x 96 in a
 # partial tile whose record bytes end mid 16-byte chunk); the others are
-# ragged for some block sizes (the general kernels)
+# ragged for some block sizes (the vector kernels' row-geometry mode: tiles
+# spanning many short rows, rows of 4100 with four-value loads, rows of 777
+# and 4095 with one-value loads)
 @pytest.mark.parametrize("bs", [8, 16, 32])
-@pytest.mark.parametrize("shape", [(64, 256), (300, 512), (7, 96), (37, 100), (5, 33), (1, 8)], ids=str)
+@pytest.mark.parametrize("shape", [(64, 256), (300, 512), (7, 96), (37, 100), (5, 33), (1, 8),
+                                   (300, 4100), (129, 777), (40, 4095)], ids=str)
 def test_pack_wire_bitexact(bs, shape):
     from axs.unified.distributed import pack_gradient_to_buffer, unpack_buffer_to_gradient
 
@@ -99,7 +102,7 @@ def test_pack_wire_edge_cases(bs):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("bs,cols", [(32, 320), (8, 328), (16, 100)])
+@pytest.mark.parametrize("bs,cols", [(32, 320), (8, 328), (16, 100), (32, 4100), (8, 777)])
 def test_pack_wire_16bit_inputs(dtype, bs, cols):
     from axs.unified.distributed import pack_gradient_to_buffer
 
