@@ -8,8 +8,10 @@ and ``matmul`` is ``accelerated_matmul`` (``backend.py:621``).
 The GEMMs run on fp16 MFMA with operands packed as power-of-two-scaled fp16
 rows (see include/axs6.h); results are float32-accumulated and land within
 rel-L2 ~3e-4 of the fp32 product of the fake-quantized operands.
-Ragged K or N (not a multiple of the block size) are zero-padded on the
-device first -- NF5 pads the last block with zeros, so this changes nothing.
+K or N off a multiple of the block size go to the kernels as they are when
+they are multiples of 4 (float32) or 8 (bfloat16, float16) -- the kernels
+zero-pad the last NF5 block, as the reference pads it; other lengths are
+zero-padded on the device to such a multiple first, which changes nothing.
 
 The training forward and backward (shape handling, allocation, the dither
 seed and the library calls) live in the torch extension ``axs._C``

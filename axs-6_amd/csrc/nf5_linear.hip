@@ -66,9 +66,12 @@ int check_dims(const char* fn, int64_t M, int64_t N, int64_t K, int block, int d
     if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
     if (!valid_block(block)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: block_size must be 8, 16 or 32 (got %d)", fn, block);
     if (M < 0 || N < 0 || K < 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: negative dimension", fn);
-    if (K % block != 0 || N % block != 0)
-        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: K (%lld) and N (%lld) must be multiples of block_size %d "
-                    "(pad them with zeros first)", fn, (long long)K, (long long)N, block);
+    // whole 16-byte vectors per row of X, W and dY (a ragged last NF5 block is
+    // zero-padded by the kernels, as the reference pads it)
+    const int64_t vm = dtype == AXS6_F32 ? 4 : 8;
+    if (K % vm != 0 || N % vm != 0)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: K (%lld) and N (%lld) must be multiples of %lld "
+                    "(pad them with zeros first)", fn, (long long)K, (long long)N, (long long)vm);
     if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: dimension too large", fn);
     return AXS6_OK;
 }

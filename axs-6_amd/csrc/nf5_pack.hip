@@ -273,9 +273,16 @@ __global__ __launch_bounds__(NT * RPW) void pack_rows_kernel(PackRowsK k, PackRo
                     }
                 }
             }
-            const int64_t zvec = (q.cols_pad - q.cols) / 8;   // 8-half zero chunks
+            // zeros up to cols_pad: a 4-half chunk first when cols % 8 == 4
+            // (f32 rows of 4k + 4 values), then 8-half (16-byte) chunks
+            int64_t zc = q.cols;
+            if ((q.cols_pad - zc) % 8 != 0) {
+                if (tid == 0) *reinterpret_cast<uint2*>(orow + zc) = uint2{0u, 0u};
+                zc += 4;
+            }
+            const int64_t zvec = (q.cols_pad - zc) / 8;
             for (int64_t z = tid; z < zvec; z += NT)
-                *reinterpret_cast<u32x4*>(orow + q.cols + z * 8) = u32x4{0u, 0u, 0u, 0u};
+                *reinterpret_cast<u32x4*>(orow + zc + z * 8) = u32x4{0u, 0u, 0u, 0u};
         }
         if (tid == 0) {
             q.s_out[r] = S_row;
@@ -341,7 +348,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
         constexpr bool FULL = decltype(full_tag)::value;
         const int64_t c0 = tx * kTile, r0 = ty * kTile;
         const int64_t c = c0 + tc * V;
-        const bool cin = FULL || c < k.cols;        // cols % block == 0: vectors are whole
+        const bool cin = FULL || c < k.cols;        // cols % V == 0: vectors are whole
         const int64_t rt = r0 + tr;                 // this thread's row in pass 0
         const S* xp = xs + rt * k.cols + c;
         const int64_t x_pass = (int64_t)RPP * k.cols;
@@ -957,8 +964,10 @@ int check_pack_rows(const PackRowsArgs& a, RowsShape* sh_out) {
     const int V = a.dtype == AXS6_F32 ? 4 : 8;
     if (a.rows > INT_MAX)   // one workgroup (or a quarter of one) per row: the grid is 32-bit
         return fail(AXS6_ERR_UNSUPPORTED, "pack_rows: %lld rows exceed the launch grid", (long long)a.rows);
-    if (a.cols % a.block != 0)
-        return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: cols (%lld) must be a multiple of block_size", (long long)a.cols);
+    // a ragged last block is fine (lanes past the row read zeros, the
+    // reference's padding); rows must be whole 16-byte vectors
+    if (a.cols % V != 0)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: cols (%lld) must be a multiple of %d", (long long)a.cols, V);
     if ((uintptr_t)a.x % 16 != 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: input not 16-byte aligned");
     if (a.colx && (uintptr_t)a.colx % 16 != 0)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_rows: column exponents not 16-byte aligned");
@@ -1048,8 +1057,8 @@ int launch_pack_rows2(const PackRowsArgs& a, const PackRowsArgs& b, const Device
 }
 
 int launch_pack_t(const PackTArgs& a, const DeviceTables& t, hipStream_t st) {
-    if (a.cols % a.block != 0)
-        return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_t: cols must be a multiple of block_size");
+    if (a.cols % (a.dtype == AXS6_F32 ? 4 : 8) != 0)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_t: cols must be a multiple of 4 (f32) or 8 (bf16, f16)");
     if ((uintptr_t)a.x % 16 != 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_t: input not 16-byte aligned");
     if (a.out && (a.ld_out % 8 != 0 || (uintptr_t)a.out % 16 != 0 || a.ld_out < pad_to(a.rows, kTile)))
         return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_t: output rows must be 16-byte aligned and hold the padded rows");
@@ -1070,8 +1079,8 @@ int launch_pack_t(const PackTArgs& a, const DeviceTables& t, hipStream_t st) {
 int64_t row_stats_col_tiles(int64_t cols) { return (cols + kStatsCols - 1) / kStatsCols; }
 
 int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t st) {
-    if (a.cols % a.block != 0)
-        return fail(AXS6_ERR_INVALID_ARGUMENT, "row_stats: cols must be a multiple of block_size");
+    if (a.cols % (a.dtype == AXS6_F32 ? 4 : 8) != 0)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "row_stats: cols must be a multiple of 4 (f32) or 8 (bf16, f16)");
     if ((uintptr_t)a.x % 16 != 0 || (a.colx && (uintptr_t)a.colx % 16 != 0))
         return fail(AXS6_ERR_INVALID_ARGUMENT, "row_stats: input and column exponents must be 16-byte aligned");
     if (a.rows == 0) return AXS6_OK;

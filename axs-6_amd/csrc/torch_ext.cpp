@@ -17,8 +17,10 @@
 // Semantics (as the Python wrappers documented them before this extension):
 //   * input (*, K) and weight (N, K) on one GPU; float32, bfloat16 or float16
 //     are computed in their own type, any other dtype in float32;
-//   * a K or N that is not a multiple of the block size is zero-padded on the
-//     device (NF5 pads the last block with zeros, so nothing changes);
+//   * a K or N that is not a multiple of 4 (float32) or 8 (bfloat16, float16)
+//     is zero-padded on the device to one (NF5 pads the last block with
+//     zeros, so nothing changes); other ragged lengths go to the kernels as
+//     they are, which zero-pad the last block themselves;
 //   * views whose data pointer is not 16-byte aligned are copied (the packing
 //     kernels load 16-byte vectors);
 //   * K == 0 gives the bias (or zeros) like F.linear, M == 0 empty outputs and
@@ -75,6 +77,11 @@ at::Tensor rows2d(const at::Tensor& t, int64_t cols) {
     for (int64_t d = 0; d + 1 < t.dim(); ++d) rows *= t.size(d);
     return t.reshape({rows, cols});
 }
+
+// Row lengths the kernels take without a copy: whole 16-byte vectors (4
+// float32 or 8 bfloat16 / float16 values); a ragged last NF5 block is
+// zero-padded by the kernels themselves.
+int64_t vec_multiple(at::ScalarType dtype) { return dtype == at::kFloat ? 4 : 8; }
 
 at::Tensor pad_last(const at::Tensor& t, int64_t mult) {
     const int64_t p = pad_amount(t.size(-1), mult);
@@ -210,8 +217,9 @@ Fwd linear_fwd_impl(const at::Tensor& input, const at::Tensor& weight, const std
     const int64_t K = input.size(-1), N = weight.size(0), Kw = weight.size(1);
     TORCH_CHECK(Kw == K, fn, ": input has ", K, " features but weight expects ", Kw);
     const at::ScalarType dtype = compute_dtype(input.scalar_type());
-    at::Tensor x2 = dense(pad_last(rows2d(input, K).to(dtype), bs));
-    at::Tensor w2 = dense(pad_rows(pad_last(weight.to(dtype), bs), bs));
+    const int64_t vm = vec_multiple(dtype);
+    at::Tensor x2 = dense(pad_last(rows2d(input, K).to(dtype), vm));
+    at::Tensor w2 = dense(pad_rows(pad_last(weight.to(dtype), vm), vm));
     const int64_t M = x2.size(0), Kb = x2.size(1), Nb = w2.size(0);
     at::Tensor b;
     if (bias && bias->defined()) {
@@ -239,7 +247,7 @@ Fwd linear_fwd_impl(const at::Tensor& input, const at::Tensor& weight, const std
                                          r.wq.data_ptr(), r.sw.data_ptr<int32_t>(), stream_of(x2)),
                  "axs6_nf5_linear_forward");
     }
-    if (Nb != N) y = y.narrow(1, 0, N);
+    if (Nb != N) y = y.narrow(1, 0, N).contiguous();   // N off the vector multiple: F.linear's dense output
     r.out = y.reshape(lead_shape(input.sizes(), N));
     r.M = M; r.N = Nb; r.K = Kb; r.n_true = N; r.k_true = K; r.dtype = dtype;
     return r;
@@ -258,7 +266,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> linear_bwd_impl(
     TORCH_CHECK(grad_output.numel() == M * n_true, "axs_linear backward: grad_output has ", grad_output.numel(),
                 " elements, expected ", M * n_true);
     at::Tensor dy = rows2d(grad_output, n_true).to(dtype);
-    if (N != n_true) dy = pad_last(dy, bs);
+    if (N != n_true) dy = pad_last(dy, vec_multiple(dtype));
     dy = dense(dy);
     at::Tensor dx, dw, db;
     if (need_x) dx = at::empty({M, K}, opts.dtype(dtype));

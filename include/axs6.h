@@ -207,7 +207,9 @@ int axs6_gemm_f16_nt(const void* a, int64_t lda, const void* b, int64_t ldb, int
                      void* out, int64_t ldo, int32_t out_dtype, void* stream);
 
 /* Y[M, N] = FQ(X)[M, K] . FQ(W)[N, K]^T + bias, with X, W, Y of `dtype` and an
- * f32 bias (may be NULL).  K and N must be multiples of block_size.  The
+ * f32 bias (may be NULL).  K and N must be multiples of 4 (f32) or 8 (bf16,
+ * f16): whole 16-byte vectors per row (a ragged last NF5 block is zero-padded
+ * by the kernels, as the reference pads it).  The
  * caller provides xq_f16 [M, Kp], x_shift [M], wq_f16 [N, Kp], w_shift [N];
  * they hold the packed operands afterwards and feed the backward.
  * quantize_input = 0 packs X without fake-quantizing it.

@@ -145,9 +145,9 @@ def test_noalloc_backward_rejects_shapes_beyond_its_scratch_without_device():
                       None, None, None)
     assert rc == 2 and "scratch" in msg
     # argument checks are the workspace entry point's
-    rc, msg = _status("axs6_nf5_linear_backward_noalloc", p, 0, 64, 48, 64, 32, 0, 0, 0, p, p, p, p, p, p, p,
+    rc, msg = _status("axs6_nf5_linear_backward_noalloc", p, 0, 64, 50, 64, 32, 0, 0, 0, p, p, p, p, p, p, p,
                       None, None)
-    assert rc == 1 and "multiples of block_size" in msg
+    assert rc == 1 and "multiples of 4" in msg
     # nothing requested, or no rows: a no-op
     rc, _ = _status("axs6_nf5_linear_backward_noalloc", p, 0, 0, 64, 64, 32, 0, 0, 0, p, p, p, p, p, p, p,
                     None, None)

@@ -294,3 +294,49 @@ def test_matmul_vs_float64():
     want = a.numpy().astype(np.float64) @ b.numpy().astype(np.float64)
     assert got.shape == (5, 33, 45)
     assert oracle.rel_l2(got, want) < TOL
+
+
+# K and N that are multiples of 4 (f32) / 8 (bf16) but not of the block size
+# go to the kernels as they are (a ragged last NF5 block, zero-padded by the
+# kernels; K = 20004 takes the two-pass pack of long rows); other lengths are
+# padded to such a multiple first (K 50, N 70).
+@pytest.mark.parametrize("M,K,N", [(64, 100, 100), (96, 1004, 36), (33, 20004, 44), (70, 50, 70)], ids=str)
+@pytest.mark.parametrize("qgrad", [False, True], ids=["exact_dy", "stochastic_dy"])
+def test_linear_ragged_k_n(M, K, N, qgrad):
+    from axs.unified import hip_linear
+
+    print(f"[linear ragged {M}x{K}x{N} qgrad={qgrad}]", flush=True)
+    x = gauss((M, K), 41, outliers=True)
+    w = gauss((N, K), 42, scale=K ** -0.5)
+    b = gauss((N,), 43)
+    dy = gauss((M, N), 44)
+    xq, wq, ref = _oracle_linear(x, w, b)
+    y, saved = hip_linear.forward_train(x.to(DEV), w.to(DEV), b.to(DEV), 32, True)
+    assert y.shape == (M, N) and y.is_contiguous()
+    assert oracle.rel_l2(y.cpu().numpy(), ref) < TOL
+    seed = 24680
+    dx, dw, db = hip_linear.backward(dy.to(DEV), saved, 32, qgrad, True, True, True, seed=seed)
+    assert dx.shape == (M, K) and dw.shape == (N, K) and db.shape == (N,)
+    dyq = oracle.fake_quantize(dy.numpy(), 32, oracle.uniform(seed, 0, dy.numel())) if qgrad else dy.numpy()
+    d2 = dyq.astype(np.float64)
+    if N % 4 == 0:
+        # dY goes to the kernels unpadded: the stochastic draws follow its own layout
+        assert oracle.rel_l2(dx.cpu().numpy(), d2 @ wq.astype(np.float64)) < TOL
+        assert oracle.rel_l2(dw.cpu().numpy(), d2.T @ xq.astype(np.float64)) < TOL
+        assert oracle.rel_l2(db.cpu().numpy(), d2.sum(0)) < 1e-5
+    elif not qgrad:
+        assert oracle.rel_l2(dx.cpu().numpy(), d2 @ wq.astype(np.float64)) < TOL
+        assert oracle.rel_l2(dw.cpu().numpy(), d2.T @ xq.astype(np.float64)) < TOL
+
+
+@pytest.mark.parametrize("K,N", [(1000, 1000), (1004, 40)], ids=["k1000", "k1004_padded"])
+def test_linear_bf16_ragged_k(K, N):
+    from axs.unified import hip_linear
+
+    x = gauss((64, K), 75).bfloat16()
+    w = (gauss((N, K), 76) / 16).bfloat16()
+    y = hip_linear.linear_forward(x.to(DEV), w.to(DEV), None, 32, True)
+    assert y.dtype == torch.bfloat16 and y.shape == (64, N)
+    xq = oracle.fake_quantize(x.float().numpy(), 32)
+    wq = oracle.fake_quantize(w.float().numpy(), 32)
+    assert oracle.rel_l2(y.float().cpu().numpy(), oracle.linear_reference(xq, wq)) < 5e-3
