@@ -1,4 +1,4 @@
-"""Seeded random sweep over the FQ, quantize/dequantize and wire entry points:
+"""Seeded random sweep over the FQ, quantize/dequantize, wire and linear entry points:
 shapes of 1-3 dims with row lengths from 1 to ~5000 values, the three input
 dtypes, block sizes 8/16/32, nearest and stochastic rounding, and views that
 start 0-7 elements into their buffer.  Each case lands on whichever kernel
@@ -138,3 +138,49 @@ def test_wire_sweep(i):
     wd = oracle.dequantize(exps, codes, signs, cols, bs)
     yd = y[off:].cpu().numpy().reshape(rows, cols)
     assert bits_equal(yd, wd), first_mismatch(yd, wd)
+
+
+def _linear_case(i: int):
+    """M, K, N, block size, bias and dY rounding of linear case i: K and N
+    mostly multiples of 4 (the kernels take them as they are, ragged last
+    block included), sometimes not (padded first)."""
+    rng = np.random.default_rng(5000 + i)
+    M = int(np.exp(rng.uniform(0.0, np.log(600.0))))
+    K, N = (int(4 * rng.integers(1, 750)) if rng.random() < 0.8 else int(rng.integers(1, 3000)) for _ in range(2))
+    bs = (8, 16, 32)[int(rng.integers(0, 3))]
+    return M, K, N, bs, bool(rng.random() < 0.7), bool(rng.random() < 0.5), rng
+
+
+@pytest.mark.parametrize("i", range(32))
+def test_linear_sweep(i):
+    """Forward (training and no-grad paths) and backward of the quantized
+    linear against the fp64 product of the oracle's FQ operands, rel-L2 within
+    the north star's 1e-3 (db, a plain column sum, within 1e-5)."""
+    from axs.unified import hip_linear
+
+    M, K, N, bs, has_bias, qgrad, rng = _linear_case(i)
+    print(f"[sweep linear case {i}: M={M} K={K} N={N} bs={bs} bias={has_bias} qgrad={qgrad}]", flush=True)
+    x = torch.from_numpy(_values((M, K), rng))
+    w = torch.from_numpy(rng.standard_normal((N, K)).astype(np.float32) * K ** -0.5)
+    b = torch.from_numpy(rng.standard_normal(N).astype(np.float32)) if has_bias else None
+    dy = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32))
+    xq = oracle.fake_quantize(x.numpy(), bs).astype(np.float64)
+    wq = oracle.fake_quantize(w.numpy(), bs).astype(np.float64)
+    ref = xq @ wq.T + (0.0 if b is None else b.numpy().astype(np.float64))
+    bd = None if b is None else b.to(DEV)
+    y, saved = hip_linear.forward_train(x.to(DEV), w.to(DEV), bd, bs, True)
+    assert y.shape == (M, N) and y.dtype == torch.float32
+    assert oracle.rel_l2(y.cpu().numpy(), ref) < 1e-3
+    y2 = hip_linear.linear_forward(x.to(DEV), w.to(DEV), bd, bs, True)
+    assert oracle.rel_l2(y2.cpu().numpy(), ref) < 1e-3
+    seed = 777 + i
+    dx, dw, db = hip_linear.backward(dy.to(DEV), saved, bs, qgrad, True, True, has_bias, seed=seed)
+    assert dx.shape == (M, K) and dw.shape == (N, K)
+    if qgrad and N % 4:
+        return   # dY is padded before its stochastic draws: parity covered where N % 4 == 0
+    d2 = (oracle.fake_quantize(dy.numpy(), bs, oracle.uniform(seed, 0, dy.numel())) if qgrad
+          else dy.numpy()).astype(np.float64)
+    assert oracle.rel_l2(dx.cpu().numpy(), d2 @ wq) < 1e-3
+    assert oracle.rel_l2(dw.cpu().numpy(), d2.T @ xq) < 1e-3
+    if has_bias:
+        assert oracle.rel_l2(db.cpu().numpy(), d2.sum(0)) < 1e-5
