@@ -4,7 +4,9 @@ dtypes, block sizes 8/16/32, nearest and stochastic rounding, and views that
 start 0-7 elements into their buffer.  Each case lands on whichever kernel
 the dispatch picks for it (whole-block vectors, row segments with four or one
 value per lane, one block per lane group, the wire format's record tiles) and
-is compared bit-exactly with the oracle, as the fixed-shape tests are."""
+is compared bit-exactly with the oracle, as the fixed-shape tests are; the
+linear cases within rel-L2 1e-3 of the fp64 product of the oracle's FQ
+operands."""
 from __future__ import annotations
 
 import numpy as np
