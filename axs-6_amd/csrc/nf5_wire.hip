@@ -457,6 +457,15 @@ int64_t record_bytes(int hb, int64_t rows, int64_t cols, int bs) {
 
 // vec: whole-block rows, x aligned to 4 values, buf to 16 bytes; rows: any
 // rows with buf aligned to 16 bytes (the fast kernels' row-geometry mode).
+//
+// The row-geometry mode steps each lane from its tile's first row over whole
+// rows, one step per row passed, so its cost grows as rows get short: rows of
+// fewer than kWireRowsMinGroups 4-value groups (padded) take the general
+// kernels, which divide per group.  Measured (f32, pack / unpack us):
+// 2^20 x 3 (2 groups per row) 46.7 / 43.8 in row mode against 11.0 / 8.5;
+// 2^18 x 40 (16) 26.0 / 20.4 against 22.3 / 20.8; 2^17 x 100 (32)
+// 21.2 / 16.6 against 22.8 / 22.4; 2^15 x 1000 30.2 / 25.1 against 45.7 / 46.5.
+constexpr int64_t kWireRowsMinGroups = 32;
 template <int HB, int DT>
 void launch_pack(const void* x, const WireGeom& g, int bs, bool vec, bool rows, const RowGeom& rg,
                  const DeviceTables& t, uint8_t* buf, hipStream_t st) {
@@ -497,7 +506,7 @@ int pack_records(const char* fn, const void* x, int dtype, int64_t rows, int64_t
     const int esize = dtype == AXS6_F32 ? 4 : 2;
     const bool xal = (uintptr_t)x % (4 * esize) == 0;
     const bool vec = cols % bs == 0 && xal && (uintptr_t)buffer % 16 == 0;
-    const bool rows_mode = !vec && (uintptr_t)buffer % 16 == 0;
+    const bool rows_mode = !vec && (uintptr_t)buffer % 16 == 0 && nblk * (bs / 4) >= kWireRowsMinGroups;
     const RowGeom rg{cols, nblk * (bs / 4), cols % 4 == 0 && xal};
     hipStream_t st = (hipStream_t)stream;
     if (dtype == AXS6_F32) launch_pack<HB, AXS6_F32>(x, g, bs, vec, rows_mode, rg, t, buffer, st);
@@ -519,9 +528,9 @@ int unpack_records(const char* fn, const uint8_t* buffer, int64_t rows, int64_t 
     const int64_t nblk = (cols + bs - 1) / bs;
     const WireGeom g{rows, cols, nblk, rows * nblk * (bs / 4)};
     hipStream_t st = (hipStream_t)stream;
-    if ((uintptr_t)buffer % 16 == 0) {
-        const bool yal = (uintptr_t)y % 16 == 0;
-        const bool vec = cols % bs == 0 && yal;
+    const bool yal = (uintptr_t)y % 16 == 0;
+    const bool vec = cols % bs == 0 && yal;
+    if ((uintptr_t)buffer % 16 == 0 && (vec || nblk * (bs / 4) >= kWireRowsMinGroups)) {
         const RowGeom rg{cols, nblk * (bs / 4), cols % 4 == 0 && yal};
         const dim3 grid(wire_vec_grid(g.groups));
 #define AXS6_WUNPACK(R_)                                                                                       \
