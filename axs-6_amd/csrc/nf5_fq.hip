@@ -24,8 +24,8 @@
 // views): four values (or one) per lane in row order, a block is
 // `block` / 4 (or `block`) neighbouring lanes (DPP / permlane maximum), rows
 // cut into segments of 256 (or 64) values, the next segment's loads in
-// flight (fq_rows_kernel).  Shorter rows: one block per lane group with
-// shuffle reductions (fq_scalar_kernel).
+// flight (fq_rows_kernel).  Shorter rows: whole rows per wave, one value per
+// lane, block maxima by segmented shuffle reductions (fq_short_kernel).
 #include <math.h>
 
 #include <type_traits>
@@ -111,13 +111,21 @@ __global__ __launch_bounds__(kThreads) void fq_vec_kernel(const typename Elem<DT
     }
 }
 
+// Rows under 64 values that do not tile into vectors of whole blocks: each
+// wave takes R = 64 / cols whole rows per step, lane l holding value l of the
+// wave's contiguous run of R * cols values, so loads and stores are
+// consecutive and at most cols - 1 lanes idle.  A lane's block is the run of
+// lanes from the block's first value to its end (BS values, or the row's end
+// for a ragged last block); its maximum is a segmented suffix maximum
+// (log2(BS) shuffle steps that never cross the block's end) read back from
+// the block's first lane.  Lanes past the run, and rows past the tensor,
+// form blocks of their own holding 0 and store nothing.
 template <int DT, int BS, bool STOCH>
-__global__ __launch_bounds__(kThreads) void fq_scalar_kernel(const typename Elem<DT>::S* x,
-                                                             typename Elem<DT>::S* y, int64_t rows,
-                                                             int64_t cols, int64_t nblk,
-                                                             const float* __restrict__ lut_g,
-                                                             const uint8_t* __restrict__ band_g,
-                                                             uint64_t seed, const uint64_t* __restrict__ seed_dev, uint64_t offset) {
+__global__ __launch_bounds__(kThreads) void fq_short_kernel(const typename Elem<DT>::S* __restrict__ x,
+                                                            typename Elem<DT>::S* __restrict__ y, int64_t rows,
+                                                            int cols, const float* __restrict__ lut_g,
+                                                            const uint8_t* __restrict__ band_g, uint64_t seed,
+                                                            const uint64_t* __restrict__ seed_dev, uint64_t offset) {
     using E = Elem<DT>;
     const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
     __shared__ float lut_s[kLutSize];
@@ -125,25 +133,30 @@ __global__ __launch_bounds__(kThreads) void fq_scalar_kernel(const typename Elem
     stage_tables(lut_s, band_w, lut_g, band_g);
     const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
 
-    constexpr int BPW = 64 / BS;  // blocks per wave and iteration
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int64_t total = rows * nblk;
-    const int64_t wstep = (int64_t)gridDim.x * (kThreads / 64) * BPW;
-    for (int64_t wb = ((int64_t)blockIdx.x * (kThreads / 64) + wave) * BPW; wb < total; wb += wstep) {
-        const int64_t blk = wb + lane / BS;
-        const int j = lane % BS;
-        const bool vb = blk < total;
-        const int64_t r = vb ? blk / nblk : 0;
-        const int64_t c = (vb ? blk - r * nblk : 0) * BS + j;
-        const bool valid = vb && c < cols;
-        const int64_t gi = r * cols + c;
-        float f = valid ? E::to_f(x[gi]) : 0.0f;
-        uint32_t m = group_umax_shfl<BS>(__float_as_uint(f) & 0x7fffffffu);
-        FqScale s = fq_scale(m, band_s);
-        const float d = STOCH ? dither_step(key, offset + (uint64_t)gi) : 0.0f;
-        float o = fq_value(f, s, lut_s, STOCH, d);
-        if (valid) y[gi] = E::from_f(o);
+    const int R = 64 / cols;                       // whole rows per wave step
+    const bool in_run = lane < R * cols;
+    const int lr = lane / cols;                    // row of the lane within the step
+    const int row0 = lr * cols;
+    const int b0 = in_run ? row0 + ((lane - row0) & ~(BS - 1)) : lane;      // first lane of the block
+    const int bend = in_run ? (b0 + BS < row0 + cols ? b0 + BS : row0 + cols) : lane + 1;
+    const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int64_t rstep = (int64_t)gridDim.x * (kThreads / 64) * R;
+    for (int64_t r0 = wave * R; r0 < rows; r0 += rstep) {
+        const int64_t base = r0 * cols;
+        const bool valid = in_run && r0 + lr < rows;
+        float f[1] = {valid ? E::to_f(x[base + lane]) : 0.0f};
+        uint32_t v = __float_as_uint(f[0]) & 0x7fffffffu;
+#pragma unroll
+        for (int d = 1; d < BS; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_down((int)v, (unsigned)d, 64);
+            if (lane + d < bend) v = v > o ? v : o;
+        }
+        const uint32_t m = (uint32_t)__shfl((int)v, b0, 64);
+        const FqScale s = fq_scale(m, band_s);
+        const float d[1] = {STOCH ? dither_step(key, offset + (uint64_t)(base + lane)) : 0.0f};
+        fq_vector<1>(f, s, lut_s, STOCH, d);
+        if (valid) y[base + lane] = E::from_f(f[0]);
     }
 }
 
@@ -736,12 +749,17 @@ void launch_fq_typed(const void* x, void* y, int64_t rows, int64_t cols, bool st
         else AXS6_FQROWS(1, 1);
 #undef AXS6_FQROWS
     } else {
-        const int64_t nblk = (cols + BS - 1) / BS;
-        const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));
+        // rows of 1..63 values: R = 64 / cols rows per wave step, at least
+        // kRowsMinSegs steps per wave, about kRowsWavesPerCu waves per CU
+        const int64_t steps = (rows + 64 / cols - 1) / (64 / cols);
+        int64_t waves = (steps + kRowsMinSegs - 1) / kRowsMinSegs;
+        const int64_t cap = (int64_t)num_cus() * kRowsWavesPerCu;
+        waves = waves < cap ? waves : cap;
+        const dim3 grid((unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64)));
         if (stochastic)
-            fq_scalar_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, seed, seed_dev, offset);
+            fq_short_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, (int)cols, t.lut, t.band, seed, seed_dev, offset);
         else
-            fq_scalar_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, cols, nblk, t.lut, t.band, seed, seed_dev, offset);
+            fq_short_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, (int)cols, t.lut, t.band, seed, seed_dev, offset);
     }
 }
 

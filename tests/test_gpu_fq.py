@@ -352,6 +352,39 @@ def test_rows_kernel_stochastic_given_stream(bs, cols):
     assert bits_equal(got, want), first_mismatch(got, want)
 
 
+# Short rows (fq_short_kernel): rows of 1-63 values that are not whole blocks
+# or not 16-byte aligned -- whole rows per wave step, one value per lane,
+# block maxima by segmented shuffles; row counts that leave the last step
+# partly empty, and NaN / inf / subnormal / zero values in the blocks.
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_short_rows_kernel_bitexact(dt, bs):
+    specials = torch.tensor([float("nan"), float("inf"), -0.0, 0.0, 1e-40, -3e38, 2.0 ** -130])
+    for cols in (1, 3, 7, 9, 17, 31, 33, 40, 63):
+        for rows in (1, 5, 1000):
+            print(f"[fq short {dt} bs={bs} {rows}x{cols}]", flush=True)
+            x = config2_input((rows, cols), 13 * cols + rows + bs)
+            if rows * cols > 64:
+                x.view(-1)[7:7 + 7 * 9:9] = specials
+            x = x.to(dt)
+            got = _fq(x.to(DEV), bs).cpu()
+            want = torch.from_numpy(oracle.fake_quantize(x.float().numpy(), bs)).to(dt)
+            bits = torch.int32 if dt == torch.float32 else torch.int16
+            nan = torch.isnan(want)
+            assert torch.equal(torch.isnan(got), nan), (rows, cols)
+            assert torch.equal(got.view(bits)[~nan], want.view(bits)[~nan]), (rows, cols)
+
+
+@pytest.mark.parametrize("bs", [8, 32])
+@pytest.mark.parametrize("cols", [3, 20, 45])
+def test_short_rows_kernel_stochastic_given_stream(bs, cols):
+    x = config2_input((3001, cols), 71 + cols)
+    seed = 0xD1CE
+    got = _fq(x.to(DEV), bs, "stochastic", seed=seed).cpu().numpy()
+    want = oracle.fake_quantize(x.numpy(), bs, oracle.uniform(seed, 0, x.numel()))
+    assert bits_equal(got, want), first_mismatch(got, want)
+
+
 # Row-segment quantize / dequantize (quantize_rows_kernel,
 # dequantize_rows_kernel): ragged rows of >= 64 values, padded-layout codes.
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
