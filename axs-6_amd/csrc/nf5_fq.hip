@@ -459,6 +459,75 @@ __global__ __launch_bounds__(kThreads) void quantize_vec_kernel(
     }
 }
 
+// quantize_kernel for padded rows under 64 positions (cpad = nblk * BS):
+// the codes, signs and exponents of such a tensor are one run of whole
+// blocks, so each lane takes four consecutive positions of that run (a block
+// is BS / 4 neighbouring lanes, DPP amax; one 4-byte code and sign store) and
+// reads the values at positions inside the row one by one (zero past the
+// row's end, as the reference pads).  The row of a position comes from one
+// wave-uniform division per step and a 32-bit division inside it.  Same
+// arithmetic and dither counters (offset + r * cols + c, padding positions
+// included) as quantize_kernel.
+template <int DT, int BS, bool STOCH>
+__global__ __launch_bounds__(kThreads) void quantize_short_kernel(
+    const typename Elem<DT>::S* __restrict__ x, int64_t rows, int64_t cols, int64_t nblk,
+    const float* __restrict__ lut_g, const uint8_t* __restrict__ band_g, const uint8_t* __restrict__ rev_g,
+    uint64_t seed, const uint64_t* __restrict__ seed_dev, uint64_t offset, uint8_t* __restrict__ exps,
+    uint8_t* __restrict__ codes, uint8_t* __restrict__ signs, typename Elem<DT>::S* __restrict__ fq) {
+    using E = Elem<DT>;
+    constexpr int G = BS / 4;
+    const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
+    __shared__ float lut_s[kLutSize];
+    __shared__ uint32_t band_w[kBandSize / 4];
+    __shared__ uint8_t rev_s[kLutSize];
+    reinterpret_cast<uint32_t*>(rev_s)[threadIdx.x] = reinterpret_cast<const uint32_t*>(rev_g)[threadIdx.x];
+    stage_tables(lut_s, band_w, lut_g, band_g);
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+
+    const int lane = threadIdx.x & 63;
+    const int cpad = (int)(nblk * BS);
+    const int64_t n4 = rows * nblk * G;                // four-position groups
+    const int64_t step = (int64_t)gridDim.x * kThreads;
+    const int64_t span = (n4 + 63) / 64 * 64;          // whole waves: every DPP group runs
+    for (int64_t vi = (int64_t)blockIdx.x * kThreads + threadIdx.x; vi < span; vi += step) {
+        const uint64_t w0 = (uint64_t)(vi - lane);
+        const int64_t p0 = 4 * (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(w0 >> 32)) << 32) |
+                                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)w0));
+        const int64_t r0 = p0 / cpad;                  // wave-uniform
+        const uint32_t q = (uint32_t)(p0 - r0 * cpad) + 4u * (uint32_t)lane;
+        const uint32_t lr = q / (uint32_t)cpad;
+        const int64_t r = r0 + lr;
+        const int c = (int)(q - lr * (uint32_t)cpad);
+        const bool live = vi < n4;
+        const int64_t base = r * cols;
+        float f[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = live && c + e < cols ? E::to_f(x[base + c + e]) : 0.0f;
+        uint32_t m = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t a = __float_as_uint(f[e]) & 0x7fffffffu;
+            m = m > a ? m : a;
+        }
+        m = group_umax<G>(m);
+        float d[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d[e] = STOCH ? dither_step(key, offset + (uint64_t)(base + c + e)) : 0.0f;
+        uint32_t cw[2], sw[2];
+        const int ex = quant_values<4, STOCH>(f, m, d, lut_s, band_s, rev_s, fq != nullptr, cw, sw);
+        if (live) {
+            reinterpret_cast<uint32_t*>(codes)[vi] = cw[0];
+            if (signs) reinterpret_cast<uint32_t*>(signs)[vi] = sw[0];
+            if (c % BS == 0) exps[vi / G] = (uint8_t)ex;
+            if (fq) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (c + e < cols) fq[base + c + e] = E::from_f(f[e]);
+            }
+        }
+    }
+}
+
 // Vector form of dequantize_kernel (cols % bs == 0, 4-byte aligned codes and
 // signs, 16-byte aligned y): four values per lane, one 16-byte store.
 __global__ __launch_bounds__(kThreads) void dequantize_vec_kernel(const uint8_t* __restrict__ exps,
@@ -809,6 +878,15 @@ void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochast
         else if (cpad >= 4 * kRowsMinCols) AXS6_QROWS(4, 1);
         else AXS6_QROWS(1, 1);
 #undef AXS6_QROWS
+        return;
+    }
+    if ((uintptr_t)codes % 4 == 0 && (uintptr_t)signs % 4 == 0) {
+        // padded rows under 64 positions: four positions per lane over the run of blocks
+        const dim3 grid((unsigned)capped_grid(rows * cpad / 4, (int64_t)kThreads * 2));
+        if (stochastic)
+            quantize_short_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, seed, seed_dev, offset, exps, codes, signs, (S*)fq);
+        else
+            quantize_short_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, seed, seed_dev, offset, exps, codes, signs, (S*)fq);
         return;
     }
     const dim3 grid((unsigned)capped_grid(rows * nblk, (int64_t)kThreads / BS));

@@ -385,6 +385,40 @@ def test_short_rows_kernel_stochastic_given_stream(bs, cols):
     assert bits_equal(got, want), first_mismatch(got, want)
 
 
+# Quantize of padded rows under 64 positions (quantize_short_kernel): four
+# positions per lane over the run of whole blocks, values read one by one.
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_quantize_short_rows_kernel(dt, bs):
+    from axs.unified.hip_kernels import hip_dequantize, hip_quantize
+
+    specials = torch.tensor([float("nan"), float("inf"), -0.0, 0.0, 1e-40, -3e38, 2.0 ** -130])
+    for cols in (1, 3, 7, 9, 17, 31, 33, 40, 55):
+        if (cols + bs - 1) // bs * bs >= 64:
+            continue
+        for rows in (1, 7, 1001):
+            print(f"[quantize short {dt} bs={bs} {rows}x{cols}]", flush=True)
+            x = config2_input((rows, cols), 31 * cols + rows + bs)
+            if rows * cols > 64:
+                x.view(-1)[5:5 + 7 * 8:8] = specials
+            x = x.to(dt)
+            xf = x.float().numpy()
+            for rounding, seed in (("nearest", None), ("stochastic", 4321)):
+                e, c, s, fq = hip_quantize(x.to(DEV), bs, rounding, with_fake_quantized=True, seed=seed)
+                u = oracle.uniform(seed, 0, x.numel()) if seed else None
+                oe, oc, os_ = oracle.quantize(xf, bs, u)
+                assert np.array_equal(e.cpu().numpy(), oe), (rows, cols, rounding)
+                assert np.array_equal(c.cpu().numpy(), oc), (rows, cols, rounding)
+                assert np.array_equal(s.cpu().numpy(), os_), (rows, cols, rounding)
+                want = torch.from_numpy(oracle.fake_quantize(xf, bs, u)).to(dt)
+                nan = torch.isnan(want)
+                bits = torch.int32 if dt == torch.float32 else torch.int16
+                assert torch.equal(torch.isnan(fq.cpu()), nan)
+                assert torch.equal(fq.cpu().view(bits)[~nan], want.view(bits)[~nan]), (rows, cols, rounding)
+            d = hip_dequantize(e, c, s, rows, cols, bs).cpu().numpy()
+            assert bits_equal(d, oracle.dequantize(oe, oc, os_, cols, bs)), (rows, cols)
+
+
 # Row-segment quantize / dequantize (quantize_rows_kernel,
 # dequantize_rows_kernel): ragged rows of >= 64 values, padded-layout codes.
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
@@ -415,7 +449,7 @@ def test_quantize_rows_kernel(dt, bs, shape):
     assert bits_equal(d, want), first_mismatch(d, want)
 
 
-@pytest.mark.parametrize("cols", [1001, 1004], ids=["one-per-lane", "four-per-lane"])
+@pytest.mark.parametrize("cols", [1001, 1004, 13], ids=["one-per-lane", "four-per-lane", "short"])
 def test_quantize_rows_kernel_without_optional_outputs(cols):
     """No signs and no FQ output on the row-segment kernel, and the dequantize
     without signs (all values positive)."""
