@@ -691,7 +691,8 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(
 // Dequantize rows: the codes and signs of a row start at r * cpad, a
 // multiple of 8 bytes, so a lane reads its four consecutive codes and signs
 // as one 4-byte load each (four values per lane, 256 per wave segment) and
-// writes the values it has inside the row.
+// writes the values it has inside the row (one 16-byte store when the row
+// length is a multiple of four and y is 16-byte aligned).
 __global__ __launch_bounds__(kThreads) void dequantize_rows_kernel(const uint8_t* __restrict__ exps,
                                                                    const uint8_t* __restrict__ codes,
                                                                    const uint8_t* __restrict__ signs,
@@ -706,6 +707,8 @@ __global__ __launch_bounds__(kThreads) void dequantize_rows_kernel(const uint8_t
     const int lane = threadIdx.x & 63;
     const int sh = bs == 8 ? 3 : (bs == 16 ? 4 : 5);
     const int64_t cpad = nblk * bs;
+    // one 16-byte store per lane where the row's four values are whole and aligned
+    const bool vec4 = cols % 4 == 0 && (uintptr_t)y % 16 == 0;
     const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t total = rows * segs_per_row;
     int64_t seg = wave * segs_per_wave;
@@ -720,15 +723,63 @@ __global__ __launch_bounds__(kThreads) void dequantize_rows_kernel(const uint8_t
             const uint32_t sw = signs ? *reinterpret_cast<const uint32_t*>(signs + r * cpad + c) : 0u;
             const float scale = pow2_float((int)exps[r * nblk + (c >> sh)] - kExpBias);
             float* yr = y + r * cols + c;
+            float v[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float a = cb[(cw >> (8 * e)) & 31] * scale;
-                if (c + e < cols) yr[e] = ((sw >> (8 * e)) & 0xffu) ? -a : a;
+                v[e] = ((sw >> (8 * e)) & 0xffu) ? -a : a;
+            }
+            if (vec4 && c + 4 <= cols) {
+                *reinterpret_cast<float4*>(yr) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (c + e < cols) yr[e] = v[e];
             }
         }
         if (++sx == segs_per_row) {
             sx = 0;
             ++r;
+        }
+    }
+}
+
+// dequantize_kernel for rows under 64 values: four positions per lane over
+// the codes' run of whole blocks (the padded rows, rows * cpad positions,
+// are contiguous), one 4-byte code and sign load each, writing the values at
+// positions inside the row; the row of a position as in quantize_short_kernel.
+__global__ __launch_bounds__(kThreads) void dequantize_short_kernel(const uint8_t* __restrict__ exps,
+                                                                    const uint8_t* __restrict__ codes,
+                                                                    const uint8_t* __restrict__ signs,
+                                                                    float* __restrict__ y, int64_t rows, int64_t cols,
+                                                                    int64_t nblk, int bs,
+                                                                    const float* __restrict__ cb_g) {
+    __shared__ float cb[kLevels];
+    if (threadIdx.x < kLevels) cb[threadIdx.x] = cb_g[threadIdx.x];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int sh = bs == 8 ? 3 : (bs == 16 ? 4 : 5);
+    const int cpad = (int)(nblk * bs);
+    const int64_t n4 = rows * cpad / 4;
+    const int64_t step = (int64_t)gridDim.x * kThreads;
+    for (int64_t vi = (int64_t)blockIdx.x * kThreads + threadIdx.x; vi - lane < n4; vi += step) {
+        const uint64_t w0 = (uint64_t)(vi - lane);
+        const int64_t p0 = 4 * (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(w0 >> 32)) << 32) |
+                                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)w0));
+        const int64_t r0 = p0 / cpad;                  // wave-uniform
+        const uint32_t q = (uint32_t)(p0 - r0 * cpad) + 4u * (uint32_t)lane;
+        const uint32_t lr = q / (uint32_t)cpad;
+        const int c = (int)(q - lr * (uint32_t)cpad);
+        if (vi >= n4 || c >= cols) continue;
+        const int64_t r = r0 + lr;
+        const uint32_t cw = reinterpret_cast<const uint32_t*>(codes)[vi];
+        const uint32_t sw = signs ? reinterpret_cast<const uint32_t*>(signs)[vi] : 0u;
+        const float scale = pow2_float((int)exps[(4 * vi) >> sh] - kExpBias);
+        float* yr = y + r * cols + c;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float a = cb[(cw >> (8 * e)) & 31] * scale;
+            if (c + e < cols) yr[e] = ((sw >> (8 * e)) & 0xffu) ? -a : a;
         }
     }
 }
@@ -974,6 +1025,16 @@ extern "C" int axs6_nf5_dequantize(const uint8_t* exponents, const uint8_t* code
         const RowSegs g = row_segs(rows, cols, 4);
         dequantize_rows_kernel<<<g.grid, kThreads, 0, (hipStream_t)stream>>>(
             exponents, codes, signs, y, rows, cols, nblk, block_size, g.per_row, g.per_wave, t.codebook);
+        return check_launch(fn);
+    }
+    if ((uintptr_t)codes % 4 == 0 && (uintptr_t)signs % 4 == 0 && 4 * cols >= nblk * block_size) {
+        // rows under 64 values filling at least a quarter of their padded
+        // blocks: four positions per lane over the padded run (sparser rows,
+        // e.g. 3 values in a block of 32, keep one thread per value: 2^20 x 3
+        // 16.3 us against 27.7 in this form)
+        const dim3 grid((unsigned)capped_grid(rows * nblk * block_size / 4, kThreads));
+        dequantize_short_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(exponents, codes, signs, y, rows, cols,
+                                                                            nblk, block_size, t.codebook);
         return check_launch(fn);
     }
     const dim3 grid((unsigned)capped_grid(rows * cols, kThreads));
