@@ -120,46 +120,6 @@ __global__ __launch_bounds__(kThreads) void fq_vec_kernel(const typename Elem<DT
 // (log2(BS) shuffle steps that never cross the block's end) read back from
 // the block's first lane.  Lanes past the run, and rows past the tensor,
 // form blocks of their own holding 0 and store nothing.
-template <int DT, int BS, bool STOCH>
-__global__ __launch_bounds__(kThreads) void fq_short_kernel(const typename Elem<DT>::S* __restrict__ x,
-                                                            typename Elem<DT>::S* __restrict__ y, int64_t rows,
-                                                            int cols, const float* __restrict__ lut_g,
-                                                            const uint8_t* __restrict__ band_g, uint64_t seed,
-                                                            const uint64_t* __restrict__ seed_dev, uint64_t offset) {
-    using E = Elem<DT>;
-    const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
-    __shared__ float lut_s[kLutSize];
-    __shared__ uint32_t band_w[kBandSize / 4];
-    stage_tables(lut_s, band_w, lut_g, band_g);
-    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
-
-    const int lane = threadIdx.x & 63;
-    const int R = 64 / cols;                       // whole rows per wave step
-    const bool in_run = lane < R * cols;
-    const int lr = lane / cols;                    // row of the lane within the step
-    const int row0 = lr * cols;
-    const int b0 = in_run ? row0 + ((lane - row0) & ~(BS - 1)) : lane;      // first lane of the block
-    const int bend = in_run ? (b0 + BS < row0 + cols ? b0 + BS : row0 + cols) : lane + 1;
-    const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    const int64_t rstep = (int64_t)gridDim.x * (kThreads / 64) * R;
-    for (int64_t r0 = wave * R; r0 < rows; r0 += rstep) {
-        const int64_t base = r0 * cols;
-        const bool valid = in_run && r0 + lr < rows;
-        float f[1] = {valid ? E::to_f(x[base + lane]) : 0.0f};
-        uint32_t v = __float_as_uint(f[0]) & 0x7fffffffu;
-#pragma unroll
-        for (int d = 1; d < BS; d <<= 1) {
-            const uint32_t o = (uint32_t)__shfl_down((int)v, (unsigned)d, 64);
-            if (lane + d < bend) v = v > o ? v : o;
-        }
-        const uint32_t m = (uint32_t)__shfl((int)v, b0, 64);
-        const FqScale s = fq_scale(m, band_s);
-        const float d[1] = {STOCH ? dither_step(key, offset + (uint64_t)(base + lane)) : 0.0f};
-        fq_vector<1>(f, s, lut_s, STOCH, d);
-        if (valid) y[base + lane] = E::from_f(f[0]);
-    }
-}
-
 // Four consecutive values at p (aligned to four values) from floats.
 template <int DT>
 __device__ __forceinline__ void store4(typename Elem<DT>::S* p, const float (&f)[4]) {
@@ -171,6 +131,85 @@ __device__ __forceinline__ void store4(typename Elem<DT>::S* p, const float (&f)
         const float g[8] = {f[0], f[1], f[2], f[3], 0.0f, 0.0f, 0.0f, 0.0f};
         const u32x4 w = E::pack(g);
         *reinterpret_cast<u32x2*>(p) = u32x2{w.x, w.y};
+    }
+}
+
+// Rows too short for the row-segment layout (under 64 values, or under 256
+// with four values per lane): each wave takes R = 64 * VL / cols whole rows
+// per step, lane l holding values VL*l .. VL*l + VL-1 of the wave's
+// contiguous run of R * cols values, so loads and stores are consecutive
+// (VL = 4: the rows are whole 4-value groups, x and y aligned to them, one
+// 16-byte f32 or 8-byte 16-bit access per lane) and at most cols - 1 values'
+// lanes idle.  A lane's block is the run of lanes from the block's first
+// value to its end (BS values, or the row's end for a ragged last block);
+// its maximum is a segmented suffix maximum (log2(BS / VL) shuffle steps
+// that never cross the block's end) read back from the block's first lane.
+// Lanes past the run, and rows past the tensor, form blocks of their own
+// holding 0 and store nothing.
+template <int DT, int BS, bool STOCH, int VL>
+__global__ __launch_bounds__(kThreads) void fq_short_kernel(const typename Elem<DT>::S* __restrict__ x,
+                                                            typename Elem<DT>::S* __restrict__ y, int64_t rows,
+                                                            int cols, const float* __restrict__ lut_g,
+                                                            const uint8_t* __restrict__ band_g, uint64_t seed,
+                                                            const uint64_t* __restrict__ seed_dev, uint64_t offset) {
+    using E = Elem<DT>;
+    static_assert(VL == 1 || VL == 4, "values per lane");
+    const uint64_t key = STOCH ? dither_key(seed + (seed_dev ? *seed_dev : 0ull)) : 0ull;
+    __shared__ float lut_s[kLutSize];
+    __shared__ uint32_t band_w[kBandSize / 4];
+    stage_tables(lut_s, band_w, lut_g, band_g);
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+
+    const int lane = threadIdx.x & 63;
+    const int R = 64 * VL / cols;                  // whole rows per wave step
+    const int pos = VL * lane;                     // first value of the lane in the run
+    const bool in_run = pos < R * cols;
+    const int lr = pos / cols;                     // row of the lane within the step
+    const int row0 = lr * cols;
+    const int bstart = row0 + ((pos - row0) & ~(BS - 1));
+    const int bstop = bstart + BS < row0 + cols ? bstart + BS : row0 + cols;
+    const int b0 = in_run ? bstart / VL : lane;                       // first lane of the block
+    const int bend = in_run ? (bstop + VL - 1) / VL : lane + 1;       // one past its last lane
+    const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int64_t rstep = (int64_t)gridDim.x * (kThreads / 64) * R;
+    for (int64_t r0 = wave * R; r0 < rows; r0 += rstep) {
+        const int64_t base = r0 * cols;
+        const bool valid = in_run && r0 + lr < rows;
+        float f[VL];
+        if constexpr (VL == 1) {
+            f[0] = valid ? E::to_f(x[base + pos]) : 0.0f;
+        } else if constexpr (DT == AXS6_F32) {
+            const u32x4 w = valid ? *reinterpret_cast<const u32x4*>(x + base + pos) : u32x4{0u, 0u, 0u, 0u};
+            E::unpack(w, f);
+        } else {
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 h = valid ? *reinterpret_cast<const u32x2*>(x + base + pos) : u32x2{0u, 0u};
+            float g[8];
+            E::unpack(u32x4{h.x, h.y, 0u, 0u}, g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) f[e] = g[e];
+        }
+        uint32_t v = 0;
+#pragma unroll
+        for (int e = 0; e < VL; ++e) {
+            const uint32_t a = __float_as_uint(f[e]) & 0x7fffffffu;
+            v = v > a ? v : a;
+        }
+#pragma unroll
+        for (int d = 1; d < BS / VL; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_down((int)v, (unsigned)d, 64);
+            if (lane + d < bend) v = v > o ? v : o;
+        }
+        const uint32_t m = (uint32_t)__shfl((int)v, b0, 64);
+        const FqScale s = fq_scale(m, band_s);
+        float d[VL];
+#pragma unroll
+        for (int e = 0; e < VL; ++e) d[e] = STOCH ? dither_step(key, offset + (uint64_t)(base + pos + e)) : 0.0f;
+        fq_vector<VL>(f, s, lut_s, STOCH, d);
+        if (valid) {
+            if constexpr (VL == 1) y[base + pos] = E::from_f(f[0]);
+            else store4<DT>(y + base + pos, f);
+        }
     }
 }
 
@@ -459,7 +498,7 @@ __global__ __launch_bounds__(kThreads) void quantize_vec_kernel(
     }
 }
 
-// quantize_kernel for padded rows under 64 positions (cpad = nblk * BS):
+// quantize_kernel for short padded rows (cpad = nblk * BS positions):
 // the codes, signs and exponents of such a tensor are one run of whole
 // blocks, so each lane takes four consecutive positions of that run (a block
 // is BS / 4 neighbouring lanes, DPP amax; one 4-byte code and sign store) and
@@ -818,6 +857,10 @@ int64_t capped_grid(int64_t work_items, int64_t per_wg) {
 constexpr int64_t kRowsMinCols = 64;
 constexpr int64_t kRowsWavesPerCu = 64;
 constexpr int64_t kRowsMinSegs = 2;
+// Quantize rows padded to fewer positions than this take quantize_short_kernel
+// (measured: 131072 x 100 at block 32, 128 positions, 27.0 -> 20.7 us; at 224
+// positions the row-segment kernel's 17.3 us beat 19.2 us).
+constexpr int64_t kQuantShortMax = 192;
 
 struct RowSegs {
     int u;
@@ -851,9 +894,11 @@ void launch_fq_typed(const void* x, void* y, int64_t rows, int64_t cols, bool st
             fq_vec_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, seed, seed_dev, offset);
         else
             fq_vec_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, n_vec, t.lut, t.band, seed, seed_dev, offset);
-    } else if (cols >= kRowsMinCols) {
-        const int esize = (int)sizeof(S);
-        const bool four = cols % 4 == 0 && (uintptr_t)x % (4 * esize) == 0 && (uintptr_t)y % (4 * esize) == 0;
+        return;
+    }
+    const int esize = (int)sizeof(S);
+    const bool four = cols % 4 == 0 && (uintptr_t)x % (4 * esize) == 0 && (uintptr_t)y % (4 * esize) == 0;
+    if (cols >= 4 * kRowsMinCols || (cols >= kRowsMinCols && !four)) {
 #define AXS6_FQROWS(U_, VL_)                                                                                   \
         do {                                                                                                   \
             const RowSegs g = row_segs(rows, cols, (U_) * (VL_));                                              \
@@ -869,17 +914,29 @@ void launch_fq_typed(const void* x, void* y, int64_t rows, int64_t cols, bool st
         else AXS6_FQROWS(1, 1);
 #undef AXS6_FQROWS
     } else {
-        // rows of 1..63 values: R = 64 / cols rows per wave step, at least
-        // kRowsMinSegs steps per wave, about kRowsWavesPerCu waves per CU
-        const int64_t steps = (rows + 64 / cols - 1) / (64 / cols);
+        // short rows: 1..63 values one per lane, or whole 4-value groups under
+        // 256 values (aligned) four per lane; R = 64 * VL / cols rows per wave
+        // step, at least kRowsMinSegs steps per wave, about kRowsWavesPerCu
+        // waves per CU
+        const int vl = four ? 4 : 1;
+        const int64_t per = 64 * vl / cols;
+        const int64_t steps = (rows + per - 1) / per;
         int64_t waves = (steps + kRowsMinSegs - 1) / kRowsMinSegs;
         const int64_t cap = (int64_t)num_cus() * kRowsWavesPerCu;
         waves = waves < cap ? waves : cap;
         const dim3 grid((unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64)));
-        if (stochastic)
-            fq_short_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, (int)cols, t.lut, t.band, seed, seed_dev, offset);
-        else
-            fq_short_kernel<DT, BS, false><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, (int)cols, t.lut, t.band, seed, seed_dev, offset);
+#define AXS6_FQSHORT(VL_)                                                                                      \
+        do {                                                                                                   \
+            if (stochastic)                                                                                    \
+                fq_short_kernel<DT, BS, true, VL_><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, (int)cols, \
+                                                                              t.lut, t.band, seed, seed_dev, offset); \
+            else                                                                                               \
+                fq_short_kernel<DT, BS, false, VL_><<<grid, kThreads, 0, st>>>((const S*)x, (S*)y, rows, (int)cols, \
+                                                                               t.lut, t.band, seed, seed_dev, offset); \
+        } while (0)
+        if (vl == 4) AXS6_FQSHORT(4);
+        else AXS6_FQSHORT(1);
+#undef AXS6_FQSHORT
     }
 }
 
@@ -909,7 +966,11 @@ void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochast
     }
     const int64_t nblk = (cols + BS - 1) / BS;
     const int64_t cpad = nblk * BS;
-    if (cpad >= kRowsMinCols) {
+    const bool c4 = (uintptr_t)codes % 4 == 0 && (uintptr_t)signs % 4 == 0;
+    // padded rows under kQuantShortMax positions run four per lane over the
+    // run of blocks (quantize_short_kernel); longer ones fill most of the
+    // row-segment kernel's 256-position segments, whose vector loads then win
+    if (cpad >= kQuantShortMax || (cpad >= kRowsMinCols && !c4)) {
         const int esize = (int)sizeof(S);
         const bool four = cols % 4 == 0 && (uintptr_t)x % (4 * esize) == 0 && (uintptr_t)fq % (4 * esize) == 0 &&
                           (uintptr_t)codes % 4 == 0 && (uintptr_t)signs % 4 == 0;
@@ -931,8 +992,8 @@ void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochast
 #undef AXS6_QROWS
         return;
     }
-    if ((uintptr_t)codes % 4 == 0 && (uintptr_t)signs % 4 == 0) {
-        // padded rows under 64 positions: four positions per lane over the run of blocks
+    if (c4) {
+        // padded rows under kQuantShortMax positions: four per lane over the run of blocks
         const dim3 grid((unsigned)capped_grid(rows * cpad / 4, (int64_t)kThreads * 2));
         if (stochastic)
             quantize_short_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, seed, seed_dev, offset, exps, codes, signs, (S*)fq);

@@ -352,15 +352,17 @@ def test_rows_kernel_stochastic_given_stream(bs, cols):
     assert bits_equal(got, want), first_mismatch(got, want)
 
 
-# Short rows (fq_short_kernel): rows of 1-63 values that are not whole blocks
-# or not 16-byte aligned -- whole rows per wave step, one value per lane,
-# block maxima by segmented shuffles; row counts that leave the last step
-# partly empty, and NaN / inf / subnormal / zero values in the blocks.
+# Short rows (fq_short_kernel): rows of 1-63 values, or of whole 4-value
+# groups under 256, that are not whole blocks or not 16-byte aligned --
+# whole rows per wave step, one or four values per lane, block maxima by
+# segmented shuffles; row counts that leave the last step partly empty, and
+# NaN / inf / subnormal / zero values in the blocks.
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("bs", [8, 16, 32])
 def test_short_rows_kernel_bitexact(dt, bs):
     specials = torch.tensor([float("nan"), float("inf"), -0.0, 0.0, 1e-40, -3e38, 2.0 ** -130])
-    for cols in (1, 3, 7, 9, 17, 31, 33, 40, 63):
+    # 4, 40, 68 ... 252: whole 4-value groups, four values per lane
+    for cols in (1, 3, 4, 7, 9, 17, 31, 33, 40, 63, 68, 100, 132, 200, 252, 99):
         for rows in (1, 5, 1000):
             print(f"[fq short {dt} bs={bs} {rows}x{cols}]", flush=True)
             x = config2_input((rows, cols), 13 * cols + rows + bs)
@@ -375,8 +377,23 @@ def test_short_rows_kernel_bitexact(dt, bs):
             assert torch.equal(got.view(bits)[~nan], want.view(bits)[~nan]), (rows, cols)
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("cols", [20, 100, 200])
+def test_short_rows_kernel_unaligned_view(dt, cols):
+    """Short rows of whole 4-value groups in a view one element into its
+    buffer: one value per lane (or the row-segment kernel), same bits as the
+    aligned tensor's four-per-lane form."""
+    x = config2_input((999, cols), 5 + cols).to(dt)
+    buf = torch.zeros(x.numel() + 1, dtype=dt, device=DEV)
+    buf[1:] = x.reshape(-1).to(DEV)
+    bits = torch.int32 if dt == torch.float32 else torch.int16
+    for bs in (8, 16, 32):
+        got = _fq(buf[1:].view(x.shape), bs).cpu().view(bits)
+        assert torch.equal(got, _fq(x.to(DEV), bs).cpu().view(bits)), bs
+
+
 @pytest.mark.parametrize("bs", [8, 32])
-@pytest.mark.parametrize("cols", [3, 20, 45])
+@pytest.mark.parametrize("cols", [3, 20, 45, 100])
 def test_short_rows_kernel_stochastic_given_stream(bs, cols):
     x = config2_input((3001, cols), 71 + cols)
     seed = 0xD1CE
@@ -385,7 +402,7 @@ def test_short_rows_kernel_stochastic_given_stream(bs, cols):
     assert bits_equal(got, want), first_mismatch(got, want)
 
 
-# Quantize of padded rows under 64 positions (quantize_short_kernel): four
+# Quantize of padded rows under 192 positions (quantize_short_kernel): four
 # positions per lane over the run of whole blocks, values read one by one.
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("bs", [8, 16, 32])
@@ -393,8 +410,8 @@ def test_quantize_short_rows_kernel(dt, bs):
     from axs.unified.hip_kernels import hip_dequantize, hip_quantize
 
     specials = torch.tensor([float("nan"), float("inf"), -0.0, 0.0, 1e-40, -3e38, 2.0 ** -130])
-    for cols in (1, 3, 7, 9, 17, 31, 33, 40, 55):
-        if (cols + bs - 1) // bs * bs >= 64:
+    for cols in (1, 3, 7, 9, 17, 31, 33, 40, 55, 68, 100, 131, 200, 225):
+        if (cols + bs - 1) // bs * bs >= 192:      # longer padded rows: the row-segment kernel
             continue
         for rows in (1, 7, 1001):
             print(f"[quantize short {dt} bs={bs} {rows}x{cols}]", flush=True)
