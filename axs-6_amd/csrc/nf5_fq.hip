@@ -850,8 +850,8 @@ int64_t capped_grid(int64_t work_items, int64_t per_wg) {
 }
 
 // Row-segment launches (fq_rows_kernel and its quantize counterpart) for rows
-// of at least kRowsMinCols elements; shorter rows keep the block-per-lane-group
-// kernels.  Segments of 64 * u elements, a contiguous range of per_wave of
+// of at least kRowsMinCols elements; shorter rows take the short-row kernels
+// (whole rows per wave step).  Segments of 64 * u elements, a contiguous range of per_wave of
 // them per wave, sized for about kRowsWavesPerCu waves per CU and at least
 // kRowsMinSegs segments per wave (the tables are staged once per workgroup).
 constexpr int64_t kRowsMinCols = 64;
