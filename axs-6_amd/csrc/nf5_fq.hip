@@ -967,10 +967,17 @@ void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochast
     const int64_t nblk = (cols + BS - 1) / BS;
     const int64_t cpad = nblk * BS;
     const bool c4 = (uintptr_t)codes % 4 == 0 && (uintptr_t)signs % 4 == 0;
-    // padded rows under kQuantShortMax positions run four per lane over the
-    // run of blocks (quantize_short_kernel); longer ones fill most of the
-    // row-segment kernel's 256-position segments, whose vector loads then win
-    if (cpad >= kQuantShortMax || (cpad >= kRowsMinCols && !c4)) {
+    const bool x4 = cols % 4 == 0 && (uintptr_t)x % (4 * sizeof(S)) == 0;
+    // Four positions per lane over the run of blocks (quantize_short_kernel)
+    // for padded rows under kQuantShortMax positions, and for longer rows
+    // that the row-segment kernel would read one value per lane when there
+    // is no FQ output (4-byte code and sign stores against byte stores:
+    // 8192 x 4095 f32 53-56 -> 41-44 us, 32768 x 999 53-56 -> 40-41 us; with
+    // an FQ output its per-lane value stores lose: 82-85 -> 117-120 us).
+    // Otherwise long rows fill most of the row-segment kernel's 256-position
+    // segments, whose vector loads then win.
+    const bool short_form = c4 && (cpad < kQuantShortMax || (fq == nullptr && !x4));
+    if (!short_form && cpad >= kRowsMinCols) {
         const int esize = (int)sizeof(S);
         const bool four = cols % 4 == 0 && (uintptr_t)x % (4 * esize) == 0 && (uintptr_t)fq % (4 * esize) == 0 &&
                           (uintptr_t)codes % 4 == 0 && (uintptr_t)signs % 4 == 0;
@@ -992,8 +999,7 @@ void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochast
 #undef AXS6_QROWS
         return;
     }
-    if (c4) {
-        // padded rows under kQuantShortMax positions: four per lane over the run of blocks
+    if (short_form) {
         const dim3 grid((unsigned)capped_grid(rows * cpad / 4, (int64_t)kThreads * 2));
         if (stochastic)
             quantize_short_kernel<DT, BS, true><<<grid, kThreads, 0, st>>>((const S*)x, rows, cols, nblk, t.lut, t.band, t.rev, seed, seed_dev, offset, exps, codes, signs, (S*)fq);

@@ -454,6 +454,11 @@ def test_quantize_rows_kernel(dt, bs, shape):
         oe, oc, os_ = oracle.quantize(xf, bs, u)
         assert np.array_equal(e.cpu().numpy(), oe), (rounding, first_mismatch(e.cpu().numpy(), oe))
         assert np.array_equal(c.cpu().numpy(), oc) and np.array_equal(s.cpu().numpy(), os_)
+        # without the FQ output (rows that are not whole aligned 4-value groups
+        # then take the four-positions-per-lane run kernel)
+        e2, c2, s2, _ = hip_quantize(x.to(DEV), bs, rounding, seed=seed)
+        assert np.array_equal(e2.cpu().numpy(), oe) and np.array_equal(c2.cpu().numpy(), oc)
+        assert np.array_equal(s2.cpu().numpy(), os_)
         want = torch.from_numpy(oracle.fake_quantize(xf, bs, u)).to(dt)
         got = fq.cpu()
         nan = torch.isnan(want)
