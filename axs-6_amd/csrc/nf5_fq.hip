@@ -976,7 +976,8 @@ void launch_quant_typed(const void* x, int64_t rows, int64_t cols, bool stochast
     // an FQ output its per-lane value stores lose: 82-85 -> 117-120 us).
     // Otherwise long rows fill most of the row-segment kernel's 256-position
     // segments, whose vector loads then win.
-    const bool short_form = c4 && (cpad < kQuantShortMax || (fq == nullptr && !x4));
+    // (its in-wave row arithmetic is 32-bit: rows of fewer than 2^30 positions)
+    const bool short_form = c4 && (cpad < kQuantShortMax || (fq == nullptr && !x4 && cpad < ((int64_t)1 << 30)));
     if (!short_form && cpad >= kRowsMinCols) {
         const int esize = (int)sizeof(S);
         const bool four = cols % 4 == 0 && (uintptr_t)x % (4 * esize) == 0 && (uintptr_t)fq % (4 * esize) == 0 &&
