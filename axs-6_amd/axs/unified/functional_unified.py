@@ -101,8 +101,12 @@ def axs_matmul_unified(
     quantize_inputs: bool = True,
 ) -> torch.Tensor:
     """``FQ(a) @ FQ(b)`` (blocks along each operand's last dim, as the
-    reference) on the HIP GEMM; no autograd."""
+    reference) on the HIP GEMM; no autograd.  ``a (*, M, K)``, ``b (*, K, N)``
+    with torch.matmul's broadcasting; the result has the operands' dtype, as
+    the reference's torch.matmul of the FQ values."""
+    dtype = torch.promote_types(a.dtype, b.dtype)
     if quantize_inputs:
         a = _accel_fq(a, block_size, "nearest")
         b = _accel_fq(b, block_size, "nearest")
-    return hip_linear.matmul(a, b)
+    out = hip_linear.matmul(a, b)
+    return out.to(dtype) if dtype.is_floating_point and out.dtype != dtype else out

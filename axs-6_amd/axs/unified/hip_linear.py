@@ -61,17 +61,19 @@ def _dense(t: torch.Tensor) -> torch.Tensor:
 class Saved:
     """Packed operands of a forward, kept for its backward."""
 
-    def __init__(self, xq, sx, wq, sw, M, N, K, n_true, k_true, dtype, x_shape, w_dtype):
+    def __init__(self, xq, sx, wq, sw, M, N, K, n_true, k_true, dtype, x_shape, w_dtype, x_dtype=None):
         self.xq, self.sx, self.wq, self.sw = xq, sx, wq, sw
         self.M, self.N, self.K = M, N, K
         self.n_true, self.k_true = n_true, k_true
         self.dtype, self.x_shape, self.w_dtype = dtype, x_shape, w_dtype
+        self.x_dtype = dtype if x_dtype is None else x_dtype   # dX comes back in this dtype
 
     def tensors(self):
         return (self.xq, self.sx, self.wq, self.sw)
 
     def meta(self):
-        return (self.M, self.N, self.K, self.n_true, self.k_true, self.dtype, self.x_shape, self.w_dtype)
+        return (self.M, self.N, self.K, self.n_true, self.k_true, self.dtype, self.x_shape, self.w_dtype,
+                self.x_dtype)
 
     @staticmethod
     def restore(tensors, meta) -> "Saved":
@@ -87,7 +89,8 @@ def _forward(input, weight, bias, block_size, quantize_input):
     assert block_size in VALID_BLOCK_SIZES, f"block_size must be one of {VALID_BLOCK_SIZES}"
     out, xq, sx, wq, sw, M, N, K, n_true, k_true, dtype = _lib.ext().linear_fwd(
         input, weight, bias, block_size, bool(quantize_input))
-    return out, Saved(xq, sx, wq, sw, M, N, K, n_true, k_true, dtype, tuple(input.shape), weight.dtype)
+    return out, Saved(xq, sx, wq, sw, M, N, K, n_true, k_true, dtype, tuple(input.shape), weight.dtype,
+                      input.dtype)
 
 
 def forward_train(input, weight, bias, block_size=32, quantize_input=True):
@@ -101,11 +104,31 @@ def forward_train(input, weight, bias, block_size=32, quantize_input=True):
 FUSED_SIZE_THRESHOLD = 128 * 1024
 
 
+def _bias_vector(bias, N: int, fn: str):
+    """The bias as F.linear broadcasts it over N output features (N values
+    as (N,) or (1, N), or one value), float32 and contiguous; other shapes
+    raise, as F.linear does -- the kernels read N values."""
+    if bias is None:
+        return None
+    n = bias.numel()
+    if n == 1 and N != 1:
+        return bias.reshape(1).expand(N).to(torch.float32).contiguous()
+    if n != N or not (bias.dim() == 1 or (bias.dim() == 2 and bias.shape[0] == 1)):
+        raise RuntimeError(f"{fn}: bias of shape {tuple(bias.shape)} does not broadcast to the {N} output features")
+    return bias.reshape(N).to(torch.float32).contiguous()
+
+
+def _as_input_dtype(out: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Y in the input's floating dtype (float64 is computed in float32 and
+    returned as float64, as the reference's F.linear on its FQ values)."""
+    return out.to(dtype) if out.dtype != dtype and dtype.is_floating_point else out
+
+
 def fused_forward(input, weight, bias=None, quantize_input=True):
     """``FQ(input) FQ(weight)^T + bias`` with block size 32 in one launch of
     the fused kernel (FQ in the tile loads, fp32 contraction): the
     reference's ``triton_fused_linear`` (``triton_kernels.py:385-482``).
-    Returns the input's dtype (float32 for other dtypes)."""
+    Returns the input's dtype (other floating dtypes are computed in float32)."""
     fn = "axs_fused_linear"
     _require_device(input, fn)
     _require_device(weight, fn)
@@ -114,33 +137,33 @@ def fused_forward(input, weight, bias=None, quantize_input=True):
     N, Kw = weight.shape
     if Kw != K:
         raise RuntimeError(f"{fn}: input has {K} features but weight expects {Kw}")
+    b = _bias_vector(bias, N, fn)
     dtype = input.dtype if input.dtype in _SUPPORTED else torch.float32
     x2 = _dense(_pad_last(_rows(input, K).to(dtype), 32))
     w2 = _dense(_pad_last(weight.to(dtype), 32))
     M, Kb = x2.shape
     dev = x2.device
     y = torch.empty((M, N), dtype=dtype, device=dev)
-    b = None if bias is None else bias.to(torch.float32).contiguous()
     if M and N and not Kb:
         y.copy_(b.to(dtype).expand(M, N) if b is not None else torch.zeros((), dtype=dtype, device=dev).expand(M, N))
     elif M and N:
         with _on_device(x2):
             _lib.call("axs6_nf5_fused_linear", x2.data_ptr(), w2.data_ptr(), _lib.ptr(b), y.data_ptr(),
                       _lib.DTYPE_CODE[dtype], M, N, Kb, 32, int(bool(quantize_input)), _lib.stream_of(x2))
-    return y.reshape(*input.shape[:-1], N)
+    return _as_input_dtype(y.reshape(*input.shape[:-1], N), input.dtype)
 
 
 def linear_forward(input, weight, bias=None, block_size=32, quantize_input=True):
     """Y = FQ(input) FQ(weight)^T + bias (no autograd bookkeeping): the fused
     single-launch kernel for block size 32 and at most FUSED_SIZE_THRESHOLD
-    outputs, else the packing kernels and the fp16-MFMA GEMM."""
+    outputs, else the packing kernels and the fp16-MFMA GEMM.  Y has the
+    input's dtype."""
     if block_size == 32 and input.shape[-1] == weight.shape[-1]:
         rows = input.numel() // input.shape[-1] if input.shape[-1] else 0
         if rows * weight.shape[0] <= FUSED_SIZE_THRESHOLD:
-            out = fused_forward(input, weight, bias, quantize_input)
-            return out if input.dtype == out.dtype or input.dtype not in _SUPPORTED else out.to(input.dtype)
+            return fused_forward(input, weight, bias, quantize_input)
     out, _ = _forward(input, weight, bias, block_size, quantize_input)
-    return out if input.dtype == out.dtype or input.dtype not in _SUPPORTED else out.to(input.dtype)
+    return out
 
 
 def backward(grad_output, saved: Saved, block_size: int, quantize_grad: bool,
@@ -152,7 +175,7 @@ def backward(grad_output, saved: Saved, block_size: int, quantize_grad: bool,
     return _lib.ext().linear_bwd(
         grad_output, saved.xq, saved.sx, saved.wq, saved.sw, saved.M, saved.N, saved.K, saved.n_true,
         saved.k_true, saved.dtype, list(saved.x_shape), saved.w_dtype, block_size, bool(quantize_grad),
-        bool(need_x), bool(need_w), bool(need_b), seed)
+        bool(need_x), bool(need_w), bool(need_b), seed, saved.x_dtype)
 
 
 def linear_autograd(input, weight, bias, block_size=32, quantize_input=True, quantize_grad=True):
@@ -166,39 +189,73 @@ def linear_autograd(input, weight, bias, block_size=32, quantize_input=True, qua
     return _lib.ext().linear(input, weight, bias, block_size, bool(quantize_input), bool(quantize_grad))
 
 
+def _matmul_2d(a2: torch.Tensor, bt: torch.Tensor, count: int, rows_b: int) -> torch.Tensor:
+    """``count`` products a2[i] (M, K) @ bt[i]^T, bt[i] (N, K), with a2 and bt
+    given as row stacks [count*M, K] and [count*N, K] (float32): one packing
+    launch per operand for the whole stack, then one GEMM per product on the
+    row ranges of the packed stacks.  Returns [count, M, N] float32."""
+    K = a2.shape[1]
+    M = a2.shape[0] // count if count else 0
+    N = rows_b
+    a2 = _dense(_pad_last(a2, 32))
+    bt = _dense(_pad_last(bt, 32))
+    Kb = a2.shape[1]
+    Kp = padded_k(Kb)
+    dev = a2.device
+    out = torch.empty((count, M, N), dtype=torch.float32, device=dev)
+    if not (count and M and N):
+        return out
+    if not Kb:
+        return out.zero_()
+    aq = torch.empty((count * M, Kp), dtype=torch.float16, device=dev)
+    bq = torch.empty((count * N, Kp), dtype=torch.float16, device=dev)
+    sa = torch.empty((count * M,), dtype=torch.int32, device=dev)
+    sb = torch.empty((count * N,), dtype=torch.int32, device=dev)
+    st = _lib.stream_of(a2)
+    with _on_device(a2):
+        _lib.call("axs6_nf5_pack_rows", a2.data_ptr(), _lib.F32, count * M, Kb, 32, 0, 0, 0, None,
+                  aq.data_ptr(), Kp, Kp, sa.data_ptr(), None, st)
+        _lib.call("axs6_nf5_pack_rows", bt.data_ptr(), _lib.F32, count * N, Kb, 32, 0, 0, 0, None,
+                  bq.data_ptr(), Kp, Kp, sb.data_ptr(), None, st)
+        for i in range(count):
+            _lib.call("axs6_gemm_f16_nt", aq[i * M:].data_ptr(), Kp, bq[i * N:].data_ptr(), Kp, M, N, Kp,
+                      sa[i * M:].data_ptr(), sb[i * N:].data_ptr(), None, out[i].data_ptr(), N, _lib.F32, st)
+    return out
+
+
 def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """``a (*, K) @ b (K, N)`` -> float32, fp16 MFMA with per-row power-of-two
-    scaled operands (no NF5 step)."""
+    """``torch.matmul(a, b)`` -> float32 on fp16 MFMA with per-row power-of-two
+    scaled operands (no NF5 step): ``a (*, M, K) @ b (*, K, N)`` with the
+    batch dims broadcast, and 1-D operands promoted and squeezed as
+    torch.matmul does.  A 2-D ``b`` contracts all of a's rows in one GEMM."""
     fn = "axs_matmul"
     _require_device(a, fn)
     _require_device(b, fn)
     _same_device(fn, a, b)
-    if b.dim() != 2:
-        raise RuntimeError(f"{fn}: b must be 2-D, got shape {tuple(b.shape)}")
-    K = a.shape[-1]
-    if b.shape[0] != K:
+    if a.dim() == 0 or b.dim() == 0:
+        raise RuntimeError(f"{fn}: both arguments need at least 1 dimension, got {a.dim()}D and {b.dim()}D")
+    a_vec, b_vec = a.dim() == 1, b.dim() == 1
+    A = a.unsqueeze(0) if a_vec else a
+    B = b.unsqueeze(-1) if b_vec else b
+    K = A.shape[-1]
+    if B.shape[-2] != K:
         raise RuntimeError(f"{fn}: shapes {tuple(a.shape)} and {tuple(b.shape)} do not contract")
-    N = b.shape[1]
-    a2 = _dense(_pad_last(_rows(a, K).float(), 32))
-    bt = _dense(_pad_last(b.float().t(), 32))               # [N, K'] rows along the contraction
-    M, Kb = a2.shape
-    Kp = padded_k(Kb)
-    dev = a2.device
-    aq = torch.empty((M, Kp), dtype=torch.float16, device=dev)
-    bq = torch.empty((N, Kp), dtype=torch.float16, device=dev)
-    sa = torch.empty((M,), dtype=torch.int32, device=dev)
-    sb = torch.empty((N,), dtype=torch.int32, device=dev)
-    out = torch.empty((M, N), dtype=torch.float32, device=dev)
-    if M and N:
-        st = _lib.stream_of(a2)
-        with _on_device(a2):
-            _lib.call("axs6_nf5_pack_rows", a2.data_ptr(), _lib.F32, M, Kb, 32, 0, 0, 0, None,
-                      aq.data_ptr(), Kp, Kp, sa.data_ptr(), None, st)
-            _lib.call("axs6_nf5_pack_rows", bt.data_ptr(), _lib.F32, N, Kb, 32, 0, 0, 0, None,
-                      bq.data_ptr(), Kp, Kp, sb.data_ptr(), None, st)
-            _lib.call("axs6_gemm_f16_nt", aq.data_ptr(), Kp, bq.data_ptr(), Kp, M, N, Kp,
-                      sa.data_ptr(), sb.data_ptr(), None, out.data_ptr(), N, _lib.F32, st)
-    return out.reshape(*a.shape[:-1], N)
+    N = B.shape[-1]
+    if B.dim() == 2:
+        # every row of a against one right operand: a single GEMM over the rows
+        out = _matmul_2d(_rows(A, K).float(), B.float().t(), 1, N)[0].reshape(*A.shape[:-1], N)
+    else:
+        batch = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
+        M = A.shape[-2]
+        count = math.prod(batch)
+        a3 = A.float().expand(*batch, M, K).reshape(count * M, K)
+        bt = B.float().transpose(-1, -2).expand(*batch, N, K).reshape(count * N, K)
+        out = _matmul_2d(a3, bt, count, N).reshape(*batch, M, N)
+    if a_vec:
+        out = out.squeeze(-2)
+    if b_vec:
+        out = out.squeeze(-1)
+    return out
 
 
 def last_forward_kernel_times(X, W, b, reps: int = 20) -> dict:

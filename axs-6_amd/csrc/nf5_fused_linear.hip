@@ -285,6 +285,18 @@ template <int DT, int WM, int TN, int NW, bool XL = false>
 void launch_cfg(const FusedK& k, bool qx, hipStream_t st) {
     const int tiles = ((k.M + 16 * WM - 1) / (16 * WM)) * ((k.N + 16 * TN - 1) / (16 * TN));
     const size_t xl_bytes = XL ? (size_t)k.M * (k.K + 4) * sizeof(float) : 0;
+    if constexpr (XL) {
+        // up to kXlBytes of dynamic LDS beside ~20 KiB static (148 KiB of the
+        // CU's 160 KiB): raise the per-kernel limit once
+        static bool attr_set = false;
+        if (!attr_set) {
+            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, true, XL>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kXlBytes);
+            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, false, XL>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kXlBytes);
+            attr_set = true;
+        }
+    }
     if (qx) fused_linear_kernel<DT, WM, TN, NW, true, XL><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
     else fused_linear_kernel<DT, WM, TN, NW, false, XL><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
 }

@@ -13,7 +13,8 @@
 //                     row exponents sw folded in per column) and the
 //                     tensor-wide shift G of the dW operand (max over rows of
 //                     the row maxima + sx[m]) -- block exponents only, no FQ
-//                     values, streamed over tiles with per-row atomicMax;
+//                     values, streamed over 2-D tiles that store per-tile
+//                     row maxima, folded per row in order by a second kernel;
 //   pack_t(dY):       one pass over 64x64 tiles computes dYq once and writes
 //                     A1 [M, Np] = dYq * 2^(sw[n] - t[m]) (row-major, for dX),
 //                     A2T [N, Mp] = (dYq * 2^(sx[m] - G))^T (for dW, transposed

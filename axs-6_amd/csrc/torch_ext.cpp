@@ -16,7 +16,9 @@
 //
 // Semantics (as the Python wrappers documented them before this extension):
 //   * input (*, K) and weight (N, K) on one GPU; float32, bfloat16 or float16
-//     are computed in their own type, any other dtype in float32;
+//     are computed in their own type, any other floating dtype in float32
+//     and returned (Y, dX) in its own type;
+//   * a bias broadcasts as in F.linear (N values, or one); other lengths raise;
 //   * a K or N that is not a multiple of 4 (float32) or 8 (bfloat16, float16)
 //     is zero-padded on the device to one (NF5 pads the last block with
 //     zeros, so nothing changes); other ragged lengths go to the kernels as
@@ -96,6 +98,24 @@ at::Tensor pad_rows(const at::Tensor& t, int64_t mult) {
 at::Tensor dense(const at::Tensor& t) {
     at::Tensor c = t.contiguous();
     return reinterpret_cast<uintptr_t>(c.data_ptr()) % 16 == 0 ? c : c.clone(at::MemoryFormat::Contiguous);
+}
+
+// The bias as F.linear broadcasts it over the N output features: one value,
+// or N values as (N,) or (1, N); anything else raises, as F.linear does (a
+// shorter bias would otherwise be read past its end by the kernels).
+at::Tensor bias_vector(const at::Tensor& bias, int64_t N, const char* fn) {
+    const int64_t n = bias.numel();
+    if (n == 1 && N != 1) return bias.reshape({1}).expand({N});
+    TORCH_CHECK(n == N && (bias.dim() == 1 || (bias.dim() == 2 && bias.size(0) == 1)), fn, ": bias of shape ",
+                bias.sizes(), " does not broadcast to the ", N, " output features");
+    return bias.reshape({N});
+}
+
+// Floating dtypes other than the three computed natively (float64) come back
+// in their own type, as the reference's F.linear on their fake-quantized
+// values returns them; the kernels compute them in float32.
+at::Tensor to_input_dtype(const at::Tensor& y, at::ScalarType in) {
+    return (y.scalar_type() != in && at::isFloatingType(in)) ? y.to(in) : y;
 }
 
 std::vector<int64_t> lead_shape(at::IntArrayRef shape, int64_t last) {
@@ -223,7 +243,7 @@ Fwd linear_fwd_impl(const at::Tensor& input, const at::Tensor& weight, const std
     const int64_t M = x2.size(0), Kb = x2.size(1), Nb = w2.size(0);
     at::Tensor b;
     if (bias && bias->defined()) {
-        b = bias->to(at::kFloat);
+        b = bias_vector(*bias, N, fn).to(at::kFloat);
         if (Nb != N) b = at::constant_pad_nd(b, {0, Nb - N});
         b = b.contiguous();
     }
@@ -248,7 +268,7 @@ Fwd linear_fwd_impl(const at::Tensor& input, const at::Tensor& weight, const std
                  "axs6_nf5_linear_forward");
     }
     if (Nb != N) y = y.narrow(1, 0, N).contiguous();   // N off the vector multiple: F.linear's dense output
-    r.out = y.reshape(lead_shape(input.sizes(), N));
+    r.out = to_input_dtype(y.reshape(lead_shape(input.sizes(), N)), input.scalar_type());
     r.M = M; r.N = Nb; r.K = Kb; r.n_true = N; r.k_true = K; r.dtype = dtype;
     return r;
 }
@@ -259,7 +279,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> linear_bwd_impl(
     const at::Tensor& grad_output, const at::Tensor& xq, const at::Tensor& sx, const at::Tensor& wq,
     const at::Tensor& sw, int64_t M, int64_t N, int64_t K, int64_t n_true, int64_t k_true, at::ScalarType dtype,
     at::IntArrayRef x_shape, at::ScalarType w_dtype, int64_t bs, bool quantize_grad, bool need_x, bool need_w,
-    bool need_b, std::optional<int64_t> seed) {
+    bool need_b, std::optional<int64_t> seed, std::optional<at::ScalarType> x_dtype) {
     const auto opts = xq.options();
     TORCH_CHECK(grad_output.device() == xq.device(), "axs_linear backward: grad_output is on ", grad_output.device(),
                 ", the saved operands on ", xq.device());
@@ -293,6 +313,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> linear_bwd_impl(
     if (dx.defined()) {
         if (K != k_true) dx = dx.narrow(1, 0, k_true);
         dx = dx.reshape(lead_shape(x_shape, k_true));
+        if (x_dtype) dx = to_input_dtype(dx, *x_dtype);
     }
     if (dw.defined()) {
         dw = dw.narrow(0, 0, n_true).narrow(1, 0, k_true);
@@ -315,6 +336,7 @@ struct LinearFunction : public torch::autograd::Function<LinearFunction> {
         d["M"] = r.M; d["N"] = r.N; d["K"] = r.K; d["n_true"] = r.n_true; d["k_true"] = r.k_true;
         d["dtype"] = (int64_t)r.dtype;
         d["w_dtype"] = (int64_t)weight.scalar_type();
+        d["x_dtype"] = (int64_t)input.scalar_type();
         d["x_shape"] = input.sizes().vec();
         d["bs"] = bs;
         d["quantize_grad"] = quantize_grad;
@@ -335,7 +357,7 @@ struct LinearFunction : public torch::autograd::Function<LinearFunction> {
             g, saved[0], saved[1], saved[2], saved[3], d["M"].toInt(), d["N"].toInt(), d["K"].toInt(),
             d["n_true"].toInt(), d["k_true"].toInt(), (at::ScalarType)d["dtype"].toInt(), x_shape,
             (at::ScalarType)d["w_dtype"].toInt(), d["bs"].toInt(), d["quantize_grad"].toBool(), need_x, need_w,
-            need_b, std::nullopt);
+            need_b, std::nullopt, (at::ScalarType)d["x_dtype"].toInt());
         return {dx, dw, db, at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
     }
 };
@@ -373,7 +395,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("grad_output"), py::arg("xq"), py::arg("sx"), py::arg("wq"), py::arg("sw"), py::arg("M"),
           py::arg("N"), py::arg("K"), py::arg("n_true"), py::arg("k_true"), py::arg("dtype"), py::arg("x_shape"),
           py::arg("w_dtype"), py::arg("block_size"), py::arg("quantize_grad"), py::arg("need_x"), py::arg("need_w"),
-          py::arg("need_b"), py::arg("seed") = py::none());
+          py::arg("need_b"), py::arg("seed") = py::none(), py::arg("x_dtype") = py::none());
     m.def("graph_counter", &graph_counter, "the device's dither counter for graph-recorded stochastic calls",
           py::arg("index"));
     m.def("next_seed", &next_seed, "a dither seed from torch's default CPU generator");

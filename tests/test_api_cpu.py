@@ -199,3 +199,25 @@ def test_axstensor_properties():
                   torch.zeros(2, 4, 32, dtype=torch.uint8), 32, torch.Size([2, 128]), 4)
     assert t.effective_bits_per_value == pytest.approx(6 + 10 / 32)
     assert t.memory_bytes == (256 * 6 + 8 * 10 + 7) // 8
+
+
+def test_bias_vector_broadcasts_like_f_linear():
+    """The fused path's bias check (host logic, no device work): one value or
+    N values as (N,) / (1, N) are accepted and expanded to N float32 values,
+    as F.linear broadcasts them; other lengths raise instead of reaching the
+    kernel, which reads N values."""
+    import torch.nn.functional as F
+
+    from axs.unified.hip_linear import _bias_vector
+
+    x, w = torch.randn(3, 4), torch.randn(5, 4)
+    for b in (torch.randn(5), torch.randn(1), torch.randn(()), torch.randn(1, 5)):
+        v = _bias_vector(b, 5, "t")
+        assert v.shape == (5,) and v.dtype == torch.float32 and v.is_contiguous()
+        assert torch.equal(F.linear(x, w, b), F.linear(x, w, v))
+    assert _bias_vector(None, 5, "t") is None
+    for b in (torch.randn(3), torch.randn(6), torch.randn(5, 1), torch.randn(2, 5)):
+        with pytest.raises(RuntimeError):
+            F.linear(x, w, b)
+        with pytest.raises(RuntimeError, match="does not broadcast"):
+            _bias_vector(b, 5, "t")

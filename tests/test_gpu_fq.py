@@ -261,10 +261,13 @@ def test_config1_golden():
     oe, oc, os_ = oracle.quantize(x.numpy(), 32)
     assert np.array_equal(e, oe) and np.array_equal(c, oc) and np.array_equal(s, os_)
     assert bits_equal(fq, oracle.fake_quantize(x.numpy(), 32))
-    if sha(x.numpy()) == str(g["input_sha"]):
-        assert np.array_equal(e, g["exps"])
-        assert sha(c) == str(g["codes_sha"]) and sha(s) == str(g["signs_sha"])
-        assert sha(fq) == str(g["fq_sha"])
+    # the fixture's hashes hold for the reference's own input: torch's CPU
+    # randn stream must reproduce it (it does for this torch build; a
+    # different stream is a test-environment error, not a skip)
+    assert sha(x.numpy()) == str(g["input_sha"]), "torch.randn(seed 0) no longer gives the config-1 input"
+    assert np.array_equal(e, g["exps"])
+    assert sha(c) == str(g["codes_sha"]) and sha(s) == str(g["signs_sha"])
+    assert sha(fq) == str(g["fq_sha"])
 
 
 # 101 columns: ragged rows (general kernel); 128: whole blocks (vector kernel)

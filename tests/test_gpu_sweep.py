@@ -178,10 +178,15 @@ def test_linear_sweep(i):
     seed = 777 + i
     dx, dw, db = hip_linear.backward(dy.to(DEV), saved, bs, qgrad, True, True, has_bias, seed=seed)
     assert dx.shape == (M, K) and dw.shape == (N, K)
-    if qgrad and N % 4:
-        return   # dY is padded before its stochastic draws: parity covered where N % 4 == 0
-    d2 = (oracle.fake_quantize(dy.numpy(), bs, oracle.uniform(seed, 0, dy.numel())) if qgrad
-          else dy.numpy()).astype(np.float64)
+    if qgrad:
+        # dY rows are zero-padded to whole 16-byte vectors (N4 columns) before
+        # the draws, so element (m, n) takes counter m * N4 + n; the padding
+        # zeros leave every block maximum unchanged
+        n4 = -(-N // 4) * 4
+        dyp = np.pad(dy.numpy(), ((0, 0), (0, n4 - N)))
+        d2 = oracle.fake_quantize(dyp, bs, oracle.uniform(seed, 0, dyp.size))[:, :N].astype(np.float64)
+    else:
+        d2 = dy.numpy().astype(np.float64)
     assert oracle.rel_l2(dx.cpu().numpy(), d2 @ wq) < 1e-3
     assert oracle.rel_l2(dw.cpu().numpy(), d2.T @ xq) < 1e-3
     if has_bias:
