@@ -13,7 +13,7 @@ namespace axs6 {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 2;  // 16-byte vectors in flight per thread
+constexpr int kUnroll = 3;  // 16-byte vectors in flight per thread (fq_vec_kernel)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
