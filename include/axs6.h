@@ -220,34 +220,6 @@ int axs6_nf5_linear_forward(const void* x, const void* w, const float* bias, voi
                             int64_t M, int64_t N, int64_t K, int32_t block_size, int32_t quantize_input,
                             void* xq_f16, int32_t* x_shift, void* wq_f16, int32_t* w_shift, void* stream);
 
-/* Device workspace (bytes) of axs6_nf5_linear_forward_stream at this shape,
- * or 0 when the shape does not run there (its 256x256 output tiles must fit
- * one workgroup per CU, K <= 32768, operands under 2 GiB). */
-size_t axs6_nf5_linear_forward_stream_workspace(int64_t M, int64_t N, int64_t K, int32_t dtype);
-
-/* Y[M, N] = FQ(X)[M, K] . FQ(W)[N, K]^T + bias in one launch whose workgroups
- * pack X and W into fp16 512-wide K-chunks while they contract the previous
- * chunk (a power-of-two shift per row and chunk, accumulators rescaled when a
- * row's shift rises): the forward without saved operands.  Same operands,
- * result and K/N rules as axs6_nf5_linear_forward (Y bit-identical to it
- * where the shifts keep every packed value in fp16's normal range).
- * workspace: 256-byte aligned, axs6_nf5_linear_forward_stream_workspace(...)
- * bytes (the packed chunks and their shifts).  Returns AXS6_ERR_UNSUPPORTED
- * for shapes outside that workspace function's rule.  Every workgroup of a
- * launch must be resident together: launches on one device that overlap in
- * time can starve each other's workgroups, which then time out (after about
- * a second), write NaN and raise the flag axs6_nf5_linear_stream_error reads.
- * Replaces: accelerated_linear (axs/unified/backend.py:540) for outputs above
- *           the fused threshold, i.e. F.linear of the fake-quantized operands
- *           (axs/unified/functional_unified.py:116-123) without autograd. */
-int axs6_nf5_linear_forward_stream(const void* x, const void* w, const float* bias, void* y, int32_t dtype,
-                                   int64_t M, int64_t N, int64_t K, int32_t block_size, int32_t quantize_input,
-                                   void* workspace, size_t workspace_bytes, void* stream);
-
-/* Reads and clears the device flag set by a timed-out streamed forward
- * (synchronous; *flag = 0 when none timed out). */
-int axs6_nf5_linear_stream_error(int32_t* flag);
-
 /* Y[M, N] = FQ(X)[M, K] . FQ(W)[N, K]^T + bias in one launch, for small
  * outputs: each 32-wide K tile of X and W is NF5 fake-quantized as it is
  * loaded (the block scale and LUT step of axs6_nf5_fake_quantize, nearest
