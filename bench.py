@@ -72,12 +72,12 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def load_traffic(name: str):
+def load_traffic(name: str, key: str = "traffic_bytes_per_launch"):
     """HBM bytes per launch measured by rocprofv3 --pmc (profiles/<name>)."""
     path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
-            return json.load(f).get("traffic_bytes_per_launch")
+            return json.load(f).get(key)
     except (OSError, ValueError):
         return None
 
@@ -421,12 +421,42 @@ def bench_fused(reps: int = 100, warmup: int = 10):
     return out
 
 
+def _graph_ms(fn, steps: int, replays: int = 3) -> float:
+    """Device ms per call of `fn` as replays of a HIP graph of `steps` calls
+    (captured after one call on a side stream; one untimed replay first), so
+    host launch time is not mixed in; HIP events on the launch stream."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(steps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) / (replays * steps)
+
+
 def bench_linear_train(reps: int = 5, warmup: int = 2):
     """quantized linear forward + backward (stochastic FQ of
-    dY, dX, dW and db) at each [M, K, N]; FLOPs per step = 6*M*N*K.  Device
-    time per step from HIP events on torch's current stream around `reps`
-    steps through hip_linear (the kernels run ~0.1-3 ms per step, so the host
-    launch cost is hidden)."""
+    dY, dX, dW and db) at each [M, K, N]; FLOPs per step = 6*M*N*K.  The
+    step's device time from replays of a HIP graph of steps through hip_linear
+    (graph-recorded stochastic calls draw a fresh dither per replay from the
+    device counter), so the small shapes' host launch time is not mixed in;
+    the eager steps (HIP events around `reps` steps) reported beside it."""
     import torch
 
     from axs.unified import hip_linear
@@ -458,14 +488,20 @@ def bench_linear_train(reps: int = 5, warmup: int = 2):
             torch.cuda.synchronize()
             return e0.elapsed_time(e1) / reps
 
-        ms_step = timed(step)
-        ms_fwd = timed(fwd)
+        eager_step = timed(step)
+        eager_fwd = timed(fwd)
+        n_graph = 20 if M * N * K < (1 << 33) else 4
+        ms_step = _graph_ms(step, n_graph)
+        ms_fwd = _graph_ms(fwd, n_graph)
         flops = 6.0 * M * N * K
         rows.append({"shape_mkn": [M, K, N], "ms_per_step": round(ms_step, 4), "fwd_ms": round(ms_fwd, 4),
                      "bwd_ms": round(ms_step - ms_fwd, 4),
                      "tflops": round(flops / (ms_step * 1e-3) / 1e12, 1),
-                     "frac_of_peak": round(flops / (ms_step * 1e-3) / 1e12 / BF16_DENSE_PEAK_TFLOPS, 4)})
-        log(f"linear fwd+bwd {M}x{K}x{N}: {ms_step:.3f} ms/step ({rows[-1]['tflops']} TFLOP/s)")
+                     "frac_of_peak": round(flops / (ms_step * 1e-3) / 1e12 / BF16_DENSE_PEAK_TFLOPS, 4),
+                     "timing": f"HIP-graph replays of {n_graph} steps",
+                     "eager_ms_per_step": round(eager_step, 4), "eager_fwd_ms": round(eager_fwd, 4)})
+        log(f"linear fwd+bwd {M}x{K}x{N}: {ms_step:.3f} ms/step graph, {eager_step:.3f} eager "
+            f"({rows[-1]['tflops']} TFLOP/s)")
         del X, W, b, dY
     return {"metric": "AXS-6 linear fwd+bwd TFLOP/s (config 4, 6*M*N*K per step)", "shapes": rows}
 
@@ -656,8 +692,8 @@ def cpu_baseline_linear():
 
 
 def pmc_pass() -> int:
-    """A short run for rocprofv3 counter collection: 5 NF5 fake-quantize
-    launches at 8192x4096 f32, 3 linear forwards at 4096^3, 5 fused
+    """A short run for rocprofv3 counter collection: 8 NF5 fake-quantize
+    launches at 8192x4096 f32 over 4 rotating inputs, 3 linear forwards at 4096^3, 5 fused
     small-output linears at M=1, K=N=4096 and, as the calibration reference
     for HBM byte counters, 5 plain device copies of a known 128 MiB (torch's
     copy kernel: 128 MiB read + 128 MiB written)."""
@@ -667,9 +703,10 @@ def pmc_pass() -> int:
     from axs.unified.hip_kernels import hip_fused_fake_quantize
 
     g = torch.Generator(device="cuda").manual_seed(3)
-    x = torch.randn(*FQ_SHAPE, device="cuda", generator=g)
-    for _ in range(5):
-        hip_fused_fake_quantize(x, 32, "nearest")
+    # HBM-cold like the bench's FQ leg: FQ_ROTATE inputs in turn, each output kept
+    xs = [torch.randn(*FQ_SHAPE, device="cuda", generator=g) for _ in range(FQ_ROTATE)]
+    outs = [hip_fused_fake_quantize(xs[i % FQ_ROTATE], 32, "nearest") for i in range(2 * FQ_ROTATE)]
+    del outs, xs
     M, K, N = LIN_SHAPE
     X = torch.randn(M, K, device="cuda", generator=g)
     W = torch.randn(N, K, device="cuda", generator=g) * K ** -0.5
@@ -822,7 +859,7 @@ def main() -> int:
                              "gemm_only": {"achieved": round(gemm_tf, 1) if gemm_tf else None,
                                            "frac": round(gemm_tf / BF16_DENSE_PEAK_TFLOPS, 4) if gemm_tf else None,
                                            "traffic": load_traffic("linear_4096_traffic.json")},
-                             "traffic": None},
+                             "traffic": load_traffic("linear_4096_traffic.json", "forward_traffic_bytes")},
             }
             lb = bench_linear(max(a.steps // 2, 10), max(a.warmup // 2, 3), dtype=torch.bfloat16)
             tb = lb["flops"] / (lb["wall_ms"] * 1e-3) / 1e12
