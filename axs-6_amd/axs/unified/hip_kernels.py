@@ -80,8 +80,9 @@ def next_seed() -> int:
 
 # Per-device uint64 counters for stochastic calls recorded in a HIP graph.
 # A recorded call keeps the seed drawn at capture time; the library adds the
-# counter's value, read when the kernel runs, and a recorded increment after
-# the call advances it -- so every replay draws fresh dither values.
+# counter's value, read when the kernel runs, and one recorded increment per
+# graph (after its first stochastic call) advances it -- so every replay draws
+# fresh dither values.
 _graph_counters: dict[int, torch.Tensor] = {}
 
 
@@ -95,6 +96,13 @@ def _graph_counter(device: torch.device) -> torch.Tensor:
         ctr = _lib.ext().graph_counter(idx)
         _graph_counters[idx] = ctr
     return ctr
+
+
+def advance_graph_counter(device: torch.device) -> None:
+    """Records the device counter's advance after a graph-recorded stochastic
+    call, once per capture (axs._C.graph_counter_advance)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    _lib.ext().graph_counter_advance(idx)
 
 
 def prepare_graph_capture(device: torch.device | int | None = None) -> None:
@@ -111,7 +119,7 @@ def stochastic_seed(device: torch.device, seed: int | None = None) -> tuple[int,
     Eagerly, a fresh host draw (or ``seed``) and no device term.  While the
     current stream is capturing a graph and no explicit ``seed`` is given, the
     draw is fixed at capture time and the per-device counter is added on the
-    device; the caller advances the counter after its launch."""
+    device; the caller calls advance_graph_counter after its launch."""
     s = next_seed() if seed is None else int(seed)
     if seed is None and torch.cuda.is_current_stream_capturing():
         ctr = _graph_counter(device)
@@ -201,7 +209,7 @@ def hip_quantize(
                       block_size, int(stochastic), s, 0, exps.data_ptr(), codes.data_ptr(),
                       signs.data_ptr(), _lib.ptr(fq), sdev, _lib.stream_of(x))
             if ctr is not None:
-                ctr.add_(1)
+                advance_graph_counter(x.device)
     if fq is not None:
         fq = fq.reshape(tensor.shape)
         if fq.dtype != tensor.dtype:

@@ -61,17 +61,23 @@ __device__ __forceinline__ int kslot(int q, int t) {
     return Elem<DT>::V == 4 ? (t < 4 ? 4 * q + t : 16 + 4 * q + (t - 4)) : 8 * q + t;
 }
 
+// The loads are unconditional (the caller passes a row and K tile inside the
+// operand): a load under a branch -- a lane mask for rows past M or N, or a
+// wave-uniform one for tiles past the wave's range -- leaves the compiler's
+// wait-count insertion two paths with different loads outstanding, and it then
+// waits for every load, the next tile's included, before the current tile is
+// used, which serialises each K step behind a full memory round trip.
 template <int DT>
-__device__ __forceinline__ void load8(const typename Elem<DT>::S* row, int kt, int q, bool live, u32x4 (&v)[2]) {
+__device__ __forceinline__ void load8(const typename Elem<DT>::S* row, int kt, int q, u32x4 (&v)[2]) {
     using S = typename Elem<DT>::S;
     constexpr int V = Elem<DT>::V;
     if constexpr (V == 4) {
         const S* p = row + kt * kFBK + 4 * q;
-        v[0] = live ? *reinterpret_cast<const u32x4*>(p) : u32x4{0u, 0u, 0u, 0u};
-        v[1] = live ? *reinterpret_cast<const u32x4*>(p + 16) : u32x4{0u, 0u, 0u, 0u};
+        v[0] = *reinterpret_cast<const u32x4*>(p);
+        v[1] = *reinterpret_cast<const u32x4*>(p + 16);
     } else {
         const S* p = row + kt * kFBK + 8 * q;
-        v[0] = live ? *reinterpret_cast<const u32x4*>(p) : u32x4{0u, 0u, 0u, 0u};
+        v[0] = *reinterpret_cast<const u32x4*>(p);
     }
 }
 
@@ -148,7 +154,7 @@ __device__ __forceinline__ void stage_x(const FusedK& k, float* xl, const float*
     }
 }
 
-template <int DT, int WM, int TN, int NW, bool QX, bool XL>
+template <int DT, int WM, int TN, int NW, bool QX, bool XL, int PF = 1>
 __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
     using E = Elem<DT>;
     using S = typename E::S;
@@ -189,20 +195,24 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
 
     // PF K tiles are loaded ahead of the one being quantized and multiplied
     // (a ring of PF + 1 register buffers, rotated by full unrolling).  One is
-    // best: measured against 2 and 3 tiles ahead, and against two tiles
-    // quantized per iteration, all slower (the loop is bound by each tile's
-    // FQ and accumulation chain, not by loads in flight: 24-26 us for
-    // M 1, K = N = 4096 in every variant, 36 -> 41-58 us at M 32)
-    constexpr int PF = 1;
+    // best: at M 1, K = N = 4096, 15.0 us against 16.5 / 17.6 / 23.4 us for
+    // 2 / 3 / 7 tiles ahead, and the loads alone (no FQ, no MFMA) take as
+    // long: this read pattern -- 64-byte pieces of 16 rows per instruction --
+    // streams the weight at ~4.5 TB/s and slows with more of it in flight
+    // (whole-row reads of the same bytes take 10.4-11.5 us)
     u32x4 xv[PF + 1][WM][2], wv[PF + 1][TN][2];
+    // rows past M or N read row 0 and tiles past the wave's range the last K
+    // tile (both loaded unconditionally, see load8): an output element takes
+    // only its own row of each operand, and the rows past M or N are not
+    // stored; a tile past the range is never multiplied
     auto load_tile = [&](int kt, u32x4 (&xd)[WM][2], u32x4 (&wd)[TN][2]) {
-        const bool in = kt < kt1;
+        const int ktl = kt < nkt ? kt : nkt - 1;
         if constexpr (!XL) {
 #pragma unroll
-            for (int i = 0; i < WM; ++i) load8<DT>(xrow[i], kt, q, in && xlive[i], xd[i]);
+            for (int i = 0; i < WM; ++i) load8<DT>(xrow[i], ktl, q, xd[i]);
         }
 #pragma unroll
-        for (int j = 0; j < TN; ++j) load8<DT>(wrow[j], kt, q, in && wlive[j], wd[j]);
+        for (int j = 0; j < TN; ++j) load8<DT>(wrow[j], ktl, q, wd[j]);
     };
 #pragma unroll
     for (int p = 0; p < PF; ++p) load_tile(kt0 + p, xv[p], wv[p]);
@@ -219,8 +229,7 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto step = [&](int kt, u32x4 (&xc)[WM][2], u32x4 (&wc)[TN][2], u32x4 (&xl)[WM][2], u32x4 (&wl)[TN][2]) {
-        load_tile(kt + PF, xl, wl);                // tiles past the range load nothing
+    auto step = [&](int kt, u32x4 (&xc)[WM][2], u32x4 (&wc)[TN][2]) {
         float xf[WM][8], wf[TN][8];
         if constexpr (XL) {
             // lanes of rows past M read row 0: an output row takes only its own A row, and
@@ -251,12 +260,16 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[i][t], wf[j][t], acc[i][j], 0, 0, 0);
     };
     // the ring position of tile kt is (kt - kt0) % (PF + 1); unrolling the
-    // loop by PF + 1 keeps every buffer index a constant
+    // loop by PF + 1 keeps every buffer index a constant.  Every iteration
+    // issues the loads of PF + 1 tiles whether or not its steps run (only the
+    // multiplications are conditional), so each loop path has the same loads
+    // outstanding and a step waits for its own tile only
     int kt = kt0;
     for (; kt < kt1; kt += PF + 1) {
 #pragma unroll
         for (int p = 0; p <= PF; ++p) {
-            if (kt + p < kt1) step(kt + p, xv[p], wv[p], xv[(p + PF) % (PF + 1)], wv[(p + PF) % (PF + 1)]);
+            load_tile(kt + p + PF, xv[(p + PF) % (PF + 1)], wv[(p + PF) % (PF + 1)]);
+            if (kt + p < kt1) step(kt + p, xv[p], wv[p]);
         }
     }
 
@@ -281,7 +294,7 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
     }
 }
 
-template <int DT, int WM, int TN, int NW, bool XL = false>
+template <int DT, int WM, int TN, int NW, bool XL = false, int PF = 1>
 void launch_cfg(const FusedK& k, bool qx, hipStream_t st) {
     const int tiles = ((k.M + 16 * WM - 1) / (16 * WM)) * ((k.N + 16 * TN - 1) / (16 * TN));
     const size_t xl_bytes = XL ? (size_t)k.M * (k.K + 4) * sizeof(float) : 0;
@@ -290,15 +303,15 @@ void launch_cfg(const FusedK& k, bool qx, hipStream_t st) {
         // CU's 160 KiB): raise the per-kernel limit once
         static bool attr_set = false;
         if (!attr_set) {
-            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, true, XL>,
+            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, true, XL, PF>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kXlBytes);
-            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, false, XL>,
+            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, false, XL, PF>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kXlBytes);
             attr_set = true;
         }
     }
-    if (qx) fused_linear_kernel<DT, WM, TN, NW, true, XL><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
-    else fused_linear_kernel<DT, WM, TN, NW, false, XL><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
+    if (qx) fused_linear_kernel<DT, WM, TN, NW, true, XL, PF><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
+    else fused_linear_kernel<DT, WM, TN, NW, false, XL, PF><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
 }
 
 // Tile and K split by shape: one 16-row block for M <= 16 (decode), else

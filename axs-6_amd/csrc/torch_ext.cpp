@@ -30,8 +30,9 @@
 //   * dW is float32 and then cast to the weight's dtype; db is float32;
 //   * the stochastic rounding of dY draws its seed from torch's default CPU
 //     generator (torch.randint(0, 2**62, (1,))), and while the current stream
-//     records a graph it adds a per-device counter read on the device and
-//     advanced after the call, so graph replays draw fresh dither values.
+//     records a graph it adds a per-device counter read on the device, which
+//     the graph advances once (after its first such call), so replays draw
+//     fresh dither values.
 #include <torch/extension.h>
 
 #include <c10/core/DeviceGuard.h>
@@ -150,6 +151,30 @@ at::Tensor graph_counter(int64_t index) {
     return t;
 }
 
+// The capture (by its id) for which each device's counter advance has been
+// recorded.  One advance per recorded graph is enough: a recorded call keys
+// its dither with its own capture-time draw plus the counter, so calls that
+// read the counter before and after the graph's one advance still get keys
+// that differ from each other and from every other replay's, and each
+// stochastic call of a graph no longer records a launch of its own.
+std::unordered_map<int, unsigned long long>* g_advanced = new std::unordered_map<int, unsigned long long>();
+
+// Records the counter's advance after a graph-recorded stochastic call on
+// `device`, unless this capture already holds one.
+void advance_counter(int64_t device) {
+    at::Tensor c = graph_counter(device);
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    unsigned long long id = 0;
+    const hipStream_t st = c10::hip::getCurrentHIPStream((c10::DeviceIndex)device).stream();
+    if (hipStreamGetCaptureInfo(st, &status, &id) == hipSuccess && status == hipStreamCaptureStatusActive) {
+        std::lock_guard<std::mutex> lk(g_counter_mu);
+        auto it = g_advanced->find((int)device);
+        if (it != g_advanced->end() && it->second == id) return;
+        (*g_advanced)[(int)device] = id;
+    }
+    c.add_(1);
+}
+
 int64_t next_seed() {
     return at::randint(0, (int64_t)1 << 62, {1}, at::TensorOptions().dtype(at::kLong)).item<int64_t>();
 }
@@ -195,7 +220,7 @@ at::Tensor fq(const at::Tensor& tensor, int64_t bs, bool stochastic, std::option
         check_rc(axs6_nf5_fake_quantize(x.data_ptr(), y.data_ptr(), dtype_code(x.scalar_type()), rows, cols,
                                         (int32_t)bs, stochastic ? 1 : 0, s.seed, 0, s.dev, stream_of(x)),
                  "axs6_nf5_fake_quantize");
-        if (s.counter.defined()) s.counter.add_(1);
+        if (s.counter.defined()) advance_counter(x.device().index());
     }
     return y.scalar_type() == orig ? y : y.to(orig);
 }
@@ -304,7 +329,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> linear_bwd_impl(
                      need_x ? dx.data_ptr() : nullptr, need_w ? dw.data_ptr<float>() : nullptr,
                      need_b ? db.data_ptr<float>() : nullptr, ws.data_ptr(), ws_bytes, s.dev, stream_of(dy)),
                  "axs6_nf5_linear_backward");
-        if (s.counter.defined()) s.counter.add_(1);
+        if (s.counter.defined()) advance_counter(dy.device().index());
     } else {
         // no rows (M == 0): the reference's dYq^T X and sum over rows give zeros
         if (dw.defined()) dw.zero_();
@@ -398,5 +423,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("need_b"), py::arg("seed") = py::none(), py::arg("x_dtype") = py::none());
     m.def("graph_counter", &graph_counter, "the device's dither counter for graph-recorded stochastic calls",
           py::arg("index"));
+    m.def("graph_counter_advance", &advance_counter,
+          "records the device's counter advance after a graph-recorded stochastic call (once per capture)",
+          py::arg("device"));
     m.def("next_seed", &next_seed, "a dither seed from torch's default CPU generator");
 }

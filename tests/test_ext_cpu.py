@@ -12,7 +12,8 @@ def test_extension_loads_and_exports():
     from axs import _lib
 
     C = _lib.ext()
-    for name in ("fq", "fq_ste", "linear", "linear_fwd", "linear_bwd", "graph_counter", "next_seed"):
+    for name in ("fq", "fq_ste", "linear", "linear_fwd", "linear_bwd", "graph_counter", "graph_counter_advance",
+                 "next_seed"):
         assert callable(getattr(C, name)), name
 
 

@@ -196,3 +196,42 @@ def test_graph_replays_draw_fresh_dither():
         assert int(ctr.item()) == c + 1
         seen.append(got)
     assert not np.array_equal(seen[0], seen[1])
+
+
+def test_graph_counter_advances_once_per_graph():
+    """Two stochastic calls recorded in one graph: the graph advances the
+    device counter once, after its first stochastic call, so per replay the
+    first call keys its dither with (its capture seed + c) and the second with
+    (its seed + c + 1); both bit-exact against the oracle, and the counter
+    moves by one per replay."""
+    import numpy as np
+
+    import oracle
+    from axs.unified import hip_kernels
+
+    g = torch.Generator().manual_seed(4)
+    xh = [torch.randn(64, 256, generator=g), torch.randn(32, 128, generator=g)]
+    xs = [t.cuda() for t in xh]
+    hip_kernels.prepare_graph_capture(xs[0].device)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for x in xs:
+            hip_kernels.hip_fused_fake_quantize(x, 32, "stochastic")
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    torch.manual_seed(31)
+    seeds = [hip_kernels.next_seed(), hip_kernels.next_seed()]
+    torch.manual_seed(31)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [hip_kernels.hip_fused_fake_quantize(x, 32, "stochastic") for x in xs]
+    ctr = hip_kernels._graph_counters[xs[0].device.index]
+    for _ in range(3):
+        c = int(ctr.item())
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (o, x) in enumerate(zip(outs, xh)):
+            want = oracle.fake_quantize(x.numpy(), 32, oracle.uniform(seeds[i] + c + i, 0, x.numel()))
+            assert np.array_equal(o.cpu().numpy().view(np.uint32), want.view(np.uint32)), f"call {i}"
+        assert int(ctr.item()) == c + 1
