@@ -29,6 +29,7 @@
 #include <limits.h>
 
 #include "gemm_tile.h"
+#include "partials.h"
 
 namespace axs6 {
 namespace {
@@ -243,6 +244,9 @@ struct SplitReduceK {
     const float* partial; int splits; int64_t stride; int M; int N;
     const int32_t* row_exp; const int32_t* col_exp; const int32_t* glob_exp; int glob_add;
     const float* bias; void* out; int64_t ldo; int out_dtype;
+    // an independent fixed-order column sum riding in the same launch: the
+    // workgroups past the split reduction's (GemmArgs::red_*)
+    int64_t split_blocks; const float* red_partial; int64_t red_chunks; int64_t red_cols; float* red_out;
 };
 
 // A workgroup takes 64 groups of four output columns; its four waves sum four
@@ -251,6 +255,10 @@ struct SplitReduceK {
 constexpr int kSplitGroups = 64, kSplitRanges = 4;
 
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(SplitReduceK k) {
+    if ((int64_t)blockIdx.x >= k.split_blocks) {   // uniform per workgroup
+        reduce_partials_block(k.red_partial, k.red_chunks, k.red_cols, k.red_out, blockIdx.x - k.split_blocks);
+        return;
+    }
     __shared__ float4 part[kSplitRanges][kSplitGroups];
     const int n4 = (k.N + 3) / 4;
     const int lg = threadIdx.x % kSplitGroups, q = threadIdx.x / kSplitGroups;
@@ -400,6 +408,13 @@ TailCut tail_cut(int64_t M, int64_t N) {
 
 static int launch_gemm_one(const GemmArgs& a, hipStream_t st, bool cut);
 
+bool gemm_splits(const GemmArgs& a) {
+    if (!a.split_partial || a.M == 0 || a.N == 0) return false;
+    const TailCut c = tail_cut(a.M, a.N);
+    return !(c.rows || c.cols) && gemm_split_count(a.M, a.N, a.Kp) > 1 &&
+           a.split_bytes >= gemm_split_bytes(a.M, a.N, a.Kp);
+}
+
 int launch_gemm_f16(const GemmArgs& a, hipStream_t st) { return launch_gemm_one(a, st, true); }
 
 static int launch_gemm_one(const GemmArgs& a, hipStream_t st, bool cut) {
@@ -468,10 +483,13 @@ static int launch_gemm_one(const GemmArgs& a, hipStream_t st, bool cut) {
         default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 4>(k, splits, st); break;   // kCfgBig
     }
     if (rc || !split) return rc;
-    SplitReduceK r{a.split_partial, splits, a.M * a.N, (int)a.M, (int)a.N, a.row_exp, a.col_exp, a.glob_exp,
-                   a.glob_add, a.bias, a.out, a.ldo, a.out_dtype};
     const int64_t groups = a.M * ((a.N + 3) / 4);
-    splitk_reduce_kernel<<<dim3((unsigned)((groups + kSplitGroups - 1) / kSplitGroups)), 256, 0, st>>>(r);
+    const int64_t sblocks = (groups + kSplitGroups - 1) / kSplitGroups;
+    const int64_t rblocks = a.red_out && a.red_cols > 0 ? (a.red_cols + kRedCols - 1) / kRedCols : 0;
+    SplitReduceK r{a.split_partial, splits, a.M * a.N, (int)a.M, (int)a.N, a.row_exp, a.col_exp, a.glob_exp,
+                   a.glob_add, a.bias, a.out, a.ldo, a.out_dtype,
+                   sblocks, a.red_partial, a.red_chunks, a.red_cols, a.red_out};
+    splitk_reduce_kernel<<<dim3((unsigned)(sblocks + rblocks)), 256, 0, st>>>(r);
     return check_launch("gemm_splitk_reduce");
 }
 

@@ -49,6 +49,9 @@ struct PackTArgs {
     const int32_t* colx_r;          // nullable (0)
     const int32_t* shift_r;         // required with out_r
     float* partial;                 // nullable
+    // nullable: per-band maxima of the statistics pass (row_stats_final_bands),
+    // folded into the tensor-wide maximum in place of *gmax and written to gmax_out
+    const int32_t* gtile = nullptr; int64_t ngtile = 0; int32_t* gmax_out = nullptr;
 };
 int launch_pack_t(const PackTArgs& a, const DeviceTables& t, hipStream_t st);
 
@@ -63,10 +66,20 @@ struct RowStatsArgs {
     const int32_t* rowx;            // nullable (0)
     int32_t* gmax;                  // nullable
     int32_t* scratch;               // [2 * row_stats_col_tiles(cols) * rows]
+    // with gtile and row_stats_final_bands(...) > 0: shift is written by the one
+    // pass, gmax is not, and gtile[band] receives each band's maximum (see PackTArgs)
+    int32_t* gtile = nullptr;
 };
+// Row bands of the one-pass statistics (rows of at most 256 values), 0 when
+// the rows are longer (two passes: tiles, then a folding launch).
+int64_t row_stats_final_bands(int64_t rows, int64_t cols, int dtype);
 // column tiles of the statistics pass: its scratch holds two ints per tile and row
 int64_t row_stats_col_tiles(int64_t cols);
-int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t st);
+struct TransposeF16;
+// With ta (and tb), the transposes of launch_transpose_f16 (without db) run
+// in the statistics launch when they take 128 x 128 tiles, else after it.
+int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t st,
+                     const TransposeF16* ta = nullptr, const TransposeF16* tb = nullptr);
 
 int64_t pack_global_chunks(int64_t rows);
 
@@ -100,8 +113,13 @@ struct GemmArgs {
     const float* bias;
     void* out; int64_t ldo; int out_dtype;
     float* split_partial = nullptr; size_t split_bytes = 0;
+    // when the GEMM splits K: red_out[c] = sum over red_chunks rows of
+    // red_partial[., c] (launch_reduce_partials) in the split reduction's launch
+    const float* red_partial = nullptr; int64_t red_chunks = 0; int64_t red_cols = 0; float* red_out = nullptr;
 };
 int launch_gemm_f16(const GemmArgs& g, hipStream_t st);
+// Whether launch_gemm_f16(g) splits K (and so runs a reduction launch after the GEMM).
+bool gemm_splits(const GemmArgs& g);
 int gemm_split_count(int64_t M, int64_t N, int64_t Kp);
 size_t gemm_split_bytes(int64_t M, int64_t N, int64_t Kp);
 

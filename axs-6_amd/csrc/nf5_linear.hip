@@ -36,10 +36,11 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct BwdLayout {
     bool dx, dw, db;   // which gradients the layout serves
-    size_t gmax, t, stats, a1, wqt, a2t, xqt, partial, splitk, splitk_bytes, total;
+    size_t gmax, t, stats, gtile, a1, wqt, a2t, xqt, partial, splitk, splitk_bytes, total;
+    int64_t bands;   // row bands of the one-pass statistics (0: two passes)
 };
 
-BwdLayout bwd_layout(int64_t M, int64_t N, int64_t K, bool dx, bool dw, bool db) {
+BwdLayout bwd_layout(int64_t M, int64_t N, int64_t K, bool dx, bool dw, bool db, int dtype) {
     const int64_t Kp = pad_to(K, kGemmK), Np = pad_to(N, kGemmK), Mp = pad_to(M, kGemmK);
     BwdLayout L{};
     L.dx = dx;
@@ -50,6 +51,8 @@ BwdLayout bwd_layout(int64_t M, int64_t N, int64_t K, bool dx, bool dw, bool db)
     L.gmax = take(sizeof(int32_t));
     L.t = take(sizeof(int32_t) * (size_t)M);
     L.stats = take(2 * sizeof(int32_t) * (size_t)row_stats_col_tiles(N) * (size_t)M);
+    L.bands = (dx || dw) ? row_stats_final_bands(M, N, dtype) : 0;
+    L.gtile = L.bands ? take(sizeof(int32_t) * (size_t)L.bands) : 0;
     L.a1 = dx ? take(2 * (size_t)M * Np) : 0;
     L.wqt = dx ? take(2 * (size_t)Kp * Np) : 0;
     L.a2t = dw ? take(2 * (size_t)N * Mp) : 0;
@@ -172,7 +175,7 @@ extern "C" int axs6_nf5_linear_forward(const void* x, const void* w, const float
 extern "C" size_t axs6_nf5_linear_backward_workspace(int64_t M, int64_t N, int64_t K, int32_t need_dx,
                                                      int32_t need_dw, int32_t need_db) {
     if (M < 0 || N < 0 || K < 0) return 0;
-    return bwd_layout(M, N, K, need_dx != 0 && K > 0, need_dw != 0 && K > 0, need_db != 0).total;
+    return bwd_layout(M, N, K, need_dx != 0 && K > 0, need_dw != 0 && K > 0, need_db != 0, AXS6_F32).total;
 }
 
 namespace axs6 {
@@ -196,7 +199,7 @@ int bwd_check(const char* fn, const BwdCall& c, bool* run, BwdLayout* L) {
     if (!c.dy) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null dy", fn);
     if ((need_dx && (!c.wq_f16 || !c.w_shift)) || (need_dw && (!c.xq_f16 || !c.x_shift)))
         return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: packed operands from the forward are required", fn);
-    *L = bwd_layout(c.M, c.N, c.K, need_dx, need_dw, need_db);
+    *L = bwd_layout(c.M, c.N, c.K, need_dx, need_dw, need_db, c.dtype);
     *run = true;
     return AXS6_OK;
 }
@@ -220,43 +223,60 @@ int bwd_run(const BwdCall& c, const BwdLayout& L, char* ws) {
     int32_t* tshift = (int32_t*)(ws + L.t);
     const bool fq = c.quantize_grad != 0;
 
-    if (need_dx || need_dw) {
-        RowStatsArgs s{dy, dtype, M, N, block_size, need_dx ? w_shift : nullptr, tshift,
-                       need_dw ? x_shift : nullptr, need_dw ? gmax : nullptr, (int32_t*)(ws + L.stats)};
-        if ((rc = launch_row_stats(s, t, st))) return rc;
-    }
-    if (need_dx || need_dw || need_db) {
-        PackTArgs p{dy, dtype, M, N, block_size, fq, fq, c.seed, c.offset, c.seed_dev, x_shift, need_dw ? gmax : nullptr,
-                    need_dw ? (_Float16*)(ws + L.a2t) : nullptr, Mp,
-                    need_dx ? (_Float16*)(ws + L.a1) : nullptr, Np, w_shift, tshift,
-                    need_db ? (float*)(ws + L.partial) : nullptr};
-        if ((rc = launch_pack_t(p, t, st))) return rc;
-    }
-    // contraction-contiguous copies of the forward's operands, one launch
     _Float16* wqt = need_dx ? (_Float16*)(ws + L.wqt) : nullptr;
     _Float16* xqt = need_dw ? (_Float16*)(ws + L.xqt) : nullptr;
+    float* partial = need_db ? (float*)(ws + L.partial) : nullptr;
+    float* splitk = L.splitk_bytes ? (float*)(ws + L.splitk) : nullptr;
+    GemmArgs gx{(const _Float16*)(ws + L.a1), Np, wqt, Np, M, K, Np, tshift, nullptr, nullptr, 0, nullptr,
+                c.dx, K, dtype, splitk, L.splitk_bytes};
+    GemmArgs gw{(const _Float16*)(ws + L.a2t), Mp, xqt, Mp, N, K, Mp, nullptr, nullptr, gmax, -15, nullptr, c.dw, K,
+                AXS6_F32, splitk, L.splitk_bytes};
+    // contraction-contiguous copies of the forward's operands (WqT for dX,
+    // XqT for dW): they depend only on the forward, so they ride in the
+    // statistics launch -- unless db needs the launch after the packing pass
+    // (below) and the dW GEMM has no split-K reduction launch to carry it
     const TransposeF16 tw{(const _Float16*)c.wq_f16, N, Kp, Kp, wqt, Kp, Np, Np};
     const TransposeF16 tx{(const _Float16*)c.xq_f16, M, Kp, Kp, xqt, Kp, Mp, Mp};
-    // the bias gradient's ordered reduction of the pack's partial sums rides in
-    // the same launch (or runs alone when no operand is transposed)
-    const float* partial = need_db ? (const float*)(ws + L.partial) : nullptr;
+    const TransposeF16* t0 = need_dx ? &tw : &tx;
+    const TransposeF16* t1 = need_dx && need_dw ? &tx : nullptr;
+    const bool db_in_dw = need_db && need_dw && gemm_splits(gw);
+    const bool t_early = (need_dx || need_dw) && (!need_db || db_in_dw);
+
+    // rows of at most 256 values: one statistics launch writes the row shifts
+    // and per-band maxima, which the packing pass folds into G
+    int32_t* gtile = L.bands ? (int32_t*)(ws + L.gtile) : nullptr;
     if (need_dx || need_dw) {
-        if ((rc = launch_transpose_f16(need_dx ? tw : tx, need_dx && need_dw ? &tx : nullptr, st, partial,
-                                       pack_global_chunks(M), N, db)))
-            return rc;
-    } else if (need_db && (rc = launch_reduce_partials(partial, pack_global_chunks(M), N, db, st))) {
+        RowStatsArgs s{dy, dtype, M, N, block_size, need_dx ? w_shift : nullptr, tshift,
+                       need_dw ? x_shift : nullptr, need_dw ? gmax : nullptr, (int32_t*)(ws + L.stats), gtile};
+        if ((rc = launch_row_stats(s, t, st, t_early ? t0 : nullptr, t_early ? t1 : nullptr))) return rc;
+    }
+    if (need_dx || need_dw || need_db) {
+        const bool fold = gtile && need_dw;
+        PackTArgs p{dy, dtype, M, N, block_size, fq, fq, c.seed, c.offset, c.seed_dev, x_shift,
+                    need_dw && !fold ? gmax : nullptr,
+                    need_dw ? (_Float16*)(ws + L.a2t) : nullptr, Mp,
+                    need_dx ? (_Float16*)(ws + L.a1) : nullptr, Np, w_shift, tshift, partial,
+                    fold ? gtile : nullptr, fold ? L.bands : 0, fold ? gmax : nullptr};
+        if ((rc = launch_pack_t(p, t, st))) return rc;
+    }
+    // the bias gradient's ordered reduction of the pack's partial sums: in the
+    // dW GEMM's split-K reduction launch, else in the transposes' launch (or
+    // alone when no operand is transposed)
+    if (!t_early && (need_dx || need_dw)) {
+        if ((rc = launch_transpose_f16(*t0, t1, st, partial, pack_global_chunks(M), N, db))) return rc;
+    } else if (need_db && !db_in_dw && !(need_dx || need_dw) &&
+               (rc = launch_reduce_partials(partial, pack_global_chunks(M), N, db, st))) {
         return rc;
     }
-    if (need_dx) {
-        GemmArgs g{(const _Float16*)(ws + L.a1), Np, wqt, Np, M, K, Np, tshift, nullptr, nullptr, 0, nullptr,
-                   c.dx, K, dtype, L.splitk_bytes ? (float*)(ws + L.splitk) : nullptr, L.splitk_bytes};
-        if ((rc = launch_gemm_f16(g, st))) return rc;
-    }
+    if (need_dx && (rc = launch_gemm_f16(gx, st))) return rc;
     if (need_dw) {
-        _Float16* a2t = (_Float16*)(ws + L.a2t);
-        GemmArgs g{a2t, Mp, xqt, Mp, N, K, Mp, nullptr, nullptr, gmax, -15, nullptr, c.dw, K, AXS6_F32,
-                   L.splitk_bytes ? (float*)(ws + L.splitk) : nullptr, L.splitk_bytes};
-        if ((rc = launch_gemm_f16(g, st))) return rc;
+        if (db_in_dw) {
+            gw.red_partial = partial;
+            gw.red_chunks = pack_global_chunks(M);
+            gw.red_cols = N;
+            gw.red_out = db;
+        }
+        if ((rc = launch_gemm_f16(gw, st))) return rc;
     }
     return AXS6_OK;
 }

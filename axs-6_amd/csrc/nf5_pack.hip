@@ -38,6 +38,7 @@
 
 #include "nf5_device.h"
 #include "linear_internal.h"
+#include "partials.h"
 
 namespace axs6 {
 namespace {
@@ -309,6 +310,9 @@ struct PackTK {
     _Float16* out_r; int64_t ld_r; const int32_t* colx_r; const int32_t* shift_r;
     float* partial;
     const float* lut; const uint8_t* band;
+    // with gtile: the tensor-wide maximum is folded here from the statistics
+    // pass's per-band maxima (instead of read from gmax) and written to gmax_out
+    const int32_t* gtile; int64_t ngtile; int32_t* gmax_out;
 };
 
 constexpr int kTile = 64;          // rows and columns of a transpose tile
@@ -335,8 +339,20 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
     const int tc = tid % TPR, tr = tid / TPR;
     const S* xs = reinterpret_cast<const S*>(k.x);
     const uint64_t key = MODE == kStochastic ? dither_key(k.seed + (k.seed_dev ? *k.seed_dev : 0ull)) : 0ull;
-    stage_tables(lut_s, band_w, k.lut, k.band);
-    const int gm = k.gmax ? *k.gmax : INT_MIN;
+    int gm = INT_MIN;
+    if (k.gtile) {
+        __shared__ int gred[kPackThreads / 64];
+        for (int64_t i = tid; i < k.ngtile; i += kPackThreads) gm = max(gm, k.gtile[i]);
+        gm = wave_max_i32(gm);
+        if ((tid & 63) == 0) gred[tid >> 6] = gm;
+        stage_tables(lut_s, band_w, k.lut, k.band);   // its barrier publishes gred
+#pragma unroll
+        for (int w = 0; w < kPackThreads / 64; ++w) gm = max(gm, gred[w]);
+        if (blockIdx.x == 0 && tid == 0 && k.gmax_out) *k.gmax_out = gm;
+    } else {
+        stage_tables(lut_s, band_w, k.lut, k.band);
+        if (k.gmax) gm = *k.gmax;
+    }
     const int G = (gm == INT_MIN) ? 0 : gm - kF16MaxExp;
 
     // persistent over tiles; consecutive workgroups take neighbouring column
@@ -569,16 +585,27 @@ __global__ __launch_bounds__(256) void stats_row_kernel(PackRowsK k) {
 // derives for a whole row in one workgroup; a row-per-workgroup pass over
 // long rows is latency-bound, this one streams.  Plain stores of per-tile
 // maxima, not atomics on a zeroed array: no initialising launch.
+//
+// Rows of at most kStatsCols columns are one tile per row band (FINAL): the
+// workgroup then holds whole rows and writes shift[r] itself, and for the
+// tensor-wide shift gtile[band] = max over its rows of (max block e1 +
+// rowx[r]) -- folded by the packing pass (pack_t) into gmax, so no folding
+// launch runs (8192 x 256 f32 forward + backward 50.8 -> 48.3 us).  Wider rows
+// in one tile per band were slower: 1024-column tiles leave too few
+// workgroups (8192 x 1024: 90.0 -> 91.5 us, 2048 x 768: 93.1 -> 97.2 us).
 struct StatsK {
     const void* x; int64_t rows; int64_t cols;
     const int32_t* colx; int32_t* tmax; int32_t* rmax;   // [ntx][rows] each
     const uint8_t* band; int32_t* gmax;                  // gmax set to INT_MIN by workgroup 0
+    int32_t* shift; const int32_t* rowx; int32_t* gtile; // FINAL: per-row shifts, per-band maxima
 };
 
 constexpr int kStatsCols = 256;   // columns of a statistics tile
 
-template <int DT, int BS, int PASSES>
-__global__ __launch_bounds__(256) void stats_tile_kernel(StatsK k, int64_t ntx) {
+// Statistics tile `bid`; band_w: LDS for the band table, gred: 4 ints of LDS.
+template <int DT, int BS, int PASSES, bool FINAL>
+__device__ __forceinline__ void stats_tile_body(const StatsK& k, int64_t ntx, int64_t bid, uint32_t* band_w,
+                                                int* gred) {
     using E = Elem<DT>;
     using S = typename E::S;
     constexpr int V = E::V;
@@ -586,13 +613,12 @@ __global__ __launch_bounds__(256) void stats_tile_kernel(StatsK k, int64_t ntx) 
     constexpr int TPR = kTile / V;                  // threads per 64-column chunk of a row
     constexpr int RPP = 256 / TPR;                  // rows per pass
     constexpr int CH = kStatsCols / kTile;          // 64-column chunks per tile
-    __shared__ uint32_t band_w[kBandSize / 4];
     const int tid = threadIdx.x;
     if (tid < kBandSize / 4) band_w[tid] = reinterpret_cast<const uint32_t*>(k.band)[tid];
     const int tc = tid % TPR, tr = tid / TPR;
-    const int64_t ty = blockIdx.x / ntx, tx = blockIdx.x - ty * ntx;
+    const int64_t ty = bid / ntx, tx = bid - ty * ntx;
     const int64_t r0 = ty * (RPP * PASSES), c0 = tx * kStatsCols;
-    if (blockIdx.x == 0 && tid == 0 && k.gmax) *k.gmax = INT_MIN;
+    if (!FINAL && bid == 0 && tid == 0 && k.gmax) *k.gmax = INT_MIN;
     const S* xs = reinterpret_cast<const S*>(k.x);
 
     u32x4 raw[PASSES][CH];
@@ -624,6 +650,7 @@ __global__ __launch_bounds__(256) void stats_tile_kernel(StatsK k, int64_t ntx) 
     }
     __syncthreads();
     const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+    int gband = INT_MIN;   // FINAL: max over this thread's rows of (max e1 + rowx)
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const int64_t r = r0 + tr + RPP * p;
@@ -654,10 +681,30 @@ __global__ __launch_bounds__(256) void stats_tile_kernel(StatsK k, int64_t ntx) 
             rm = o2 > rm ? o2 : rm;
         }
         if (tc == 0 && r < k.rows) {
-            k.tmax[tx * k.rows + r] = tm;
-            k.rmax[tx * k.rows + r] = rm;
+            if constexpr (FINAL) {
+                if (k.shift) k.shift[r] = tm == INT_MIN ? 0 : tm - kF16MaxExp;
+                if (rm != INT_MIN) gband = max(gband, rm + (k.rowx ? k.rowx[r] : 0));
+            } else {
+                k.tmax[tx * k.rows + r] = tm;
+                k.rmax[tx * k.rows + r] = rm;
+            }
         }
     }
+    if constexpr (FINAL) {
+        if (k.gtile) {
+            gband = wave_max_i32(gband);
+            if ((tid & 63) == 0) gred[tid >> 6] = gband;
+            __syncthreads();
+            if (tid == 0) k.gtile[bid] = max(max(gred[0], gred[1]), max(gred[2], gred[3]));
+        }
+    }
+}
+
+template <int DT, int BS, int PASSES, bool FINAL = false>
+__global__ __launch_bounds__(256) void stats_tile_kernel(StatsK k, int64_t ntx) {
+    __shared__ uint32_t band_w[kBandSize / 4];
+    __shared__ int gred[4];
+    stats_tile_body<DT, BS, PASSES, FINAL>(k, ntx, blockIdx.x, band_w, gred);
 }
 
 // A workgroup folds 64 rows: wave w takes the column tiles w, w + 4, ...
@@ -709,43 +756,6 @@ __global__ __launch_bounds__(256) void stats_finalize_kernel(const int32_t* __re
 
 // out[c] = sum over chunks k of partial[k, c], in the order k = 0, 1, ...
 // split into 4 consecutive ranges combined in order: deterministic.
-// db[c] = sum of partial[k, c] over the chunks k, in a fixed order: a
-// workgroup takes 16 columns, its 16 thread groups 16 consecutive ranges of
-// chunks (each summed in order, eight loads in flight), then the ranges are
-// added in order.
-constexpr int kRedCols = 16, kRedRanges = 16;
-
-// out[c] = sum_k partial[k, c] for the kRedCols columns of block `bx`: 16
-// ranges of k summed by 16 thread groups, then the ranges added in order.
-__device__ __forceinline__ void reduce_partials_block(const float* __restrict__ partial, int64_t chunks,
-                                                      int64_t cols, float* __restrict__ out, int64_t bx) {
-    __shared__ float part[kRedRanges][kRedCols + 1];
-    const int lc = threadIdx.x % kRedCols, q = threadIdx.x / kRedCols;
-    const int64_t c = bx * kRedCols + lc;
-    const int64_t per = (chunks + kRedRanges - 1) / kRedRanges;
-    const int64_t k0 = q * per, k1 = (k0 + per) < chunks ? k0 + per : chunks;
-    float s = 0.0f;
-    if (c < cols) {
-        int64_t kk = k0;
-        for (; kk + 8 <= k1; kk += 8) {
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = partial[(kk + u) * cols + c];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) s += v[u];
-        }
-        for (; kk < k1; ++kk) s += partial[kk * cols + c];
-    }
-    part[q][lc] = s;
-    __syncthreads();
-    if (q == 0 && c < cols) {
-        float t = part[0][lc];
-#pragma unroll
-        for (int r = 1; r < kRedRanges; ++r) t += part[r][lc];
-        out[c] = t;
-    }
-}
-
 __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ partial, int64_t chunks,
                                                               int64_t cols, float* __restrict__ out) {
     reduce_partials_block(partial, chunks, cols, out, blockIdx.x);
@@ -825,20 +835,15 @@ constexpr int kT128 = 128;
 
 __device__ __forceinline__ int t128_slot(int oc, int k) { return oc * (kT128 / 8) + (k ^ ((oc >> 3) & 15)); }
 
-__global__ __launch_bounds__(256) void transpose128_f16_kernel(TransposeF16 j0, TransposeF16 j1, int ny0, int ny1,
-                                                               ReduceJob red) {
-    if ((int)blockIdx.y >= ny0 + ny1) {      // uniform per workgroup
-        const int64_t rb = (int64_t)(blockIdx.y - ny0 - ny1) * gridDim.x + blockIdx.x;
-        if (rb < red.blocks) reduce_partials_block(red.partial, red.chunks, red.cols, red.out, rb);
-        return;
-    }
-    const bool second = (int)blockIdx.y >= ny0;
+// Tile (bx, by) of the 128 x 128 transposes; tile: kT128 * kT128 / 8 chunks of LDS.
+__device__ __forceinline__ void transpose128_body(const TransposeF16& j0, const TransposeF16& j1, int ny0, int bx,
+                                                  int by, u32x4* tile) {
+    const bool second = by >= ny0;
     const TransposeF16 j = second ? j1 : j0;
     const uint16_t* __restrict__ in = reinterpret_cast<const uint16_t*>(j.in);
     uint16_t* __restrict__ out = reinterpret_cast<uint16_t*>(j.out);
-    __shared__ __align__(16) u32x4 tile[kT128 * kT128 / 8];   // 16-byte chunks, swizzled
     const int tid = threadIdx.x;
-    const int64_t c0 = (int64_t)blockIdx.x * kT128, r0 = (int64_t)(second ? blockIdx.y - ny0 : blockIdx.y) * kT128;
+    const int64_t c0 = (int64_t)bx * kT128, r0 = (int64_t)(second ? by - ny0 : by) * kT128;
     const int br = tid >> 4, bc = tid & 15;      // this thread's 8 x 8 block
     const int64_t r = r0 + 8 * br, c = c0 + 8 * bc;
     uint32_t w[8][4];
@@ -867,6 +872,34 @@ __global__ __launch_bounds__(256) void transpose128_f16_kernel(TransposeF16 j0, 
         const int64_t orow = c0 + oc, ocol = r0 + 8 * k;
         if (orow < j.out_rows && ocol < j.rows_pad)
             *reinterpret_cast<u32x4*>(out + orow * j.ld_out + ocol) = tile[t128_slot(oc, k)];
+    }
+}
+
+__global__ __launch_bounds__(256) void transpose128_f16_kernel(TransposeF16 j0, TransposeF16 j1, int ny0, int ny1,
+                                                               ReduceJob red) {
+    if ((int)blockIdx.y >= ny0 + ny1) {      // uniform per workgroup
+        const int64_t rb = (int64_t)(blockIdx.y - ny0 - ny1) * gridDim.x + blockIdx.x;
+        if (rb < red.blocks) reduce_partials_block(red.partial, red.chunks, red.cols, red.out, rb);
+        return;
+    }
+    __shared__ __align__(16) u32x4 tile[kT128 * kT128 / 8];   // 16-byte chunks, swizzled
+    transpose128_body(j0, j1, ny0, blockIdx.x, blockIdx.y, tile);
+}
+
+// The statistics tiles of dY (workgroups below nstats) and the 128 x 128
+// transposes of the forward's packed operands (the gx x ny tiles after them)
+// are independent: one launch for both.
+template <int DT, int BS, int PASSES, bool FINAL>
+__global__ __launch_bounds__(256) void stats_transpose_kernel(StatsK k, int64_t ntx, int64_t nstats, TransposeF16 j0,
+                                                              TransposeF16 j1, int ny0, int gx) {
+    __shared__ __align__(16) u32x4 smem[kT128 * kT128 / 8];
+    __shared__ int gred[4];
+    const int64_t b = blockIdx.x;
+    if (b < nstats) {
+        stats_tile_body<DT, BS, PASSES, FINAL>(k, ntx, b, reinterpret_cast<uint32_t*>(smem), gred);
+    } else {
+        const int64_t t = b - nstats;
+        transpose128_body(j0, j1, ny0, (int)(t % gx), (int)(t / gx), smem);
     }
 }
 
@@ -1067,7 +1100,7 @@ int launch_pack_t(const PackTArgs& a, const DeviceTables& t, hipStream_t st) {
                     !a.shift_r || (a.colx_r && (uintptr_t)a.colx_r % 16 != 0)))
         return fail(AXS6_ERR_INVALID_ARGUMENT, "pack_t: row-major output must be 16-byte aligned and hold the padded columns");
     PackTK k{a.x, a.rows, a.cols, a.block, a.seed, a.seed_dev, a.offset, a.rowx, a.gmax, a.out, a.ld_out,
-             a.out_r, a.ld_r, a.colx_r, a.shift_r, a.partial, t.lut, t.band};
+             a.out_r, a.ld_r, a.colx_r, a.shift_r, a.partial, t.lut, t.band, a.gtile, a.ngtile, a.gmax_out};
     const int64_t ntx = (a.cols + kTile - 1) / kTile, ntiles = ntx * pack_global_chunks(a.rows);
     const int mode = a.fake_quant ? (a.stochastic ? kStochastic : kNearest) : kRaw;
     if (a.dtype == AXS6_F32) dispatch_t<AXS6_F32>(k, mode, ntx, ntiles, st);
@@ -1078,27 +1111,68 @@ int launch_pack_t(const PackTArgs& a, const DeviceTables& t, hipStream_t st) {
 
 int64_t row_stats_col_tiles(int64_t cols) { return (cols + kStatsCols - 1) / kStatsCols; }
 
-int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t st) {
+int64_t row_stats_final_bands(int64_t rows, int64_t cols, int dtype) {
+    const int rpp = dtype == AXS6_F32 ? 16 : 32;   // rows of a one-pass tile (PASSES 1)
+    return cols <= kStatsCols ? (rows + rpp - 1) / rpp : 0;
+}
+
+namespace {
+bool transpose128_ok(const TransposeF16& x) {
+    return x.out_rows == 0 || x.rows_pad == 0 ||
+           (x.ld_in % 8 == 0 && x.ld_out % 8 == 0 && x.rows_pad % 8 == 0 && x.cols % 8 == 0 &&
+            (uintptr_t)x.in % 16 == 0 && (uintptr_t)x.out % 16 == 0);
+}
+}  // namespace
+
+int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t st, const TransposeF16* ta,
+                     const TransposeF16* tb) {
     if (a.cols % (a.dtype == AXS6_F32 ? 4 : 8) != 0)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "row_stats: cols must be a multiple of 4 (f32) or 8 (bf16, f16)");
     if ((uintptr_t)a.x % 16 != 0 || (a.colx && (uintptr_t)a.colx % 16 != 0))
         return fail(AXS6_ERR_INVALID_ARGUMENT, "row_stats: input and column exponents must be 16-byte aligned");
-    if (a.rows == 0) return AXS6_OK;
+    if (a.rows == 0) return ta ? launch_transpose_f16(*ta, tb, st) : AXS6_OK;
     const int64_t ntx = row_stats_col_tiles(a.cols);
-    StatsK k{a.x, a.rows, a.cols, a.colx, a.scratch, a.scratch + ntx * a.rows, t.band, a.gmax};
+    const int64_t fbands = a.gtile ? row_stats_final_bands(a.rows, a.cols, a.dtype) : 0;
+    StatsK k{a.x, a.rows, a.cols, a.colx, a.scratch, a.scratch + ntx * a.rows, t.band, a.gmax,
+             a.shift, a.rowx, a.gtile};
+    // the transposes ride in this launch when they take 128 x 128 tiles
+    // (aligned operands, as the backward's always are), else run after it
+    const TransposeF16 none{nullptr, 0, 0, 0, nullptr, 0, 0, 0};
+    const TransposeF16& j0 = ta ? *ta : none;
+    const TransposeF16& j1 = tb ? *tb : none;
+    const bool with_t = ta && transpose128_ok(j0) && transpose128_ok(j1);
+    const int64_t gx0 = j0.out_rows && j0.rows_pad ? (j0.out_rows + kT128 - 1) / kT128 : 0;
+    const int64_t gx1 = j1.out_rows && j1.rows_pad ? (j1.out_rows + kT128 - 1) / kT128 : 0;
+    const int64_t ny0 = gx0 ? (j0.rows_pad + kT128 - 1) / kT128 : 0, ny1 = gx1 ? (j1.rows_pad + kT128 - 1) / kT128 : 0;
+    const int64_t gx = gx0 > gx1 ? gx0 : gx1;
+    const TransposeF16& f0 = ny0 ? j0 : j1;   // the jobs in order: j0 (when it has tiles), then j1
+    const TransposeF16& f1 = ny0 ? j1 : j0;
+    const int fny0 = (int)(ny0 ? ny0 : ny1);
+    const int64_t tblocks = with_t ? gx * (ny0 + ny1) : 0;
     // rows per tile: 16 bytes per lane, 16 (f32) or 32 (16-bit) rows per pass;
-    // as many passes as keep >= 8192 workgroups, up to 4 (measured, f32 dY:
+    // with tiles of whole rows (rows of at most 256 values) one pass, else as
+    // many passes as keep >= 8192 workgroups, up to 4 (measured, f32 dY:
     // 8192 x 11008 66 us with 2 passes against 70 with 4; 8192 x 4096 25.6
     // with 1 against 27.4 with 4)
     const int rpp = a.dtype == AXS6_F32 ? 16 : 32;
     auto tiles = [&](int passes) { return ntx * ((a.rows + rpp * passes - 1) / (rpp * passes)); };
-    const int passes = tiles(4) >= 8192 ? 4 : (tiles(2) >= 8192 ? 2 : 1);
-    const dim3 grid((unsigned)tiles(passes));
+    const int passes = fbands ? 1 : (tiles(4) >= 8192 ? 4 : (tiles(2) >= 8192 ? 2 : 1));
+    const int64_t nstats = fbands ? fbands : tiles(passes);
+    const dim3 grid((unsigned)(nstats + tblocks));
+#define AXS6_STATS_K(DT_, BS_, P_, F_)                                                               \
+    do {                                                                                             \
+        if (with_t)                                                                                  \
+            stats_transpose_kernel<DT_, BS_, P_, F_><<<grid, 256, 0, st>>>(k, ntx, nstats, f0, f1,    \
+                                                                          fny0, (int)gx);            \
+        else                                                                                         \
+            stats_tile_kernel<DT_, BS_, P_, F_><<<grid, 256, 0, st>>>(k, ntx);                       \
+    } while (0)
 #define AXS6_STATS_P(DT_, BS_)                                                                       \
     do {                                                                                             \
-        if (passes == 4) stats_tile_kernel<DT_, BS_, 4><<<grid, 256, 0, st>>>(k, ntx);               \
-        else if (passes == 2) stats_tile_kernel<DT_, BS_, 2><<<grid, 256, 0, st>>>(k, ntx);          \
-        else stats_tile_kernel<DT_, BS_, 1><<<grid, 256, 0, st>>>(k, ntx);                           \
+        if (fbands) AXS6_STATS_K(DT_, BS_, 1, true);                                                 \
+        else if (passes == 4) AXS6_STATS_K(DT_, BS_, 4, false);                                      \
+        else if (passes == 2) AXS6_STATS_K(DT_, BS_, 2, false);                                      \
+        else AXS6_STATS_K(DT_, BS_, 1, false);                                                       \
     } while (0)
 #define AXS6_STATS(DT_)                                                                              \
     do {                                                                                             \
@@ -1111,11 +1185,16 @@ int launch_row_stats(const RowStatsArgs& a, const DeviceTables& t, hipStream_t s
     else AXS6_STATS(AXS6_F16);
 #undef AXS6_STATS
 #undef AXS6_STATS_P
+#undef AXS6_STATS_K
     int rc = check_launch("row_stats");
     if (rc) return rc;
-    stats_finalize_kernel<<<dim3((unsigned)((a.rows + kFinRows - 1) / kFinRows)), 256, 0, st>>>(
-        a.scratch, a.scratch + ntx * a.rows, a.rows, ntx, a.shift, a.rowx, a.gmax);
-    return check_launch("row_stats");
+    if (!fbands) {
+        stats_finalize_kernel<<<dim3((unsigned)((a.rows + kFinRows - 1) / kFinRows)), 256, 0, st>>>(
+            a.scratch, a.scratch + ntx * a.rows, a.rows, ntx, a.shift, a.rowx, a.gmax);
+        if ((rc = check_launch("row_stats"))) return rc;
+    }
+    if (ta && !with_t) return launch_transpose_f16(*ta, tb, st);
+    return AXS6_OK;
 }
 
 int launch_reduce_partials(const float* partial, int64_t chunks, int64_t cols, float* out, hipStream_t st) {
@@ -1129,12 +1208,7 @@ int launch_transpose_f16(const TransposeF16& a, const TransposeF16* b, hipStream
                          int64_t chunks, int64_t cols, float* db) {
     const TransposeF16 none{nullptr, 0, 0, 0, nullptr, 0, 0, 0};
     const TransposeF16& bb = b ? *b : none;
-    auto aligned = [](const TransposeF16& x) {
-        return x.out_rows == 0 || x.rows_pad == 0 ||
-               (x.ld_in % 8 == 0 && x.ld_out % 8 == 0 && x.rows_pad % 8 == 0 && x.cols % 8 == 0 &&
-                (uintptr_t)x.in % 16 == 0 && (uintptr_t)x.out % 16 == 0);
-    };
-    const int T = aligned(a) && aligned(bb) ? kT128 : kTile;
+    const int T = transpose128_ok(a) && transpose128_ok(bb) ? kT128 : kTile;
     const int64_t gx_a = a.out_rows && a.rows_pad ? (a.out_rows + T - 1) / T : 0;
     const int64_t gx_b = bb.out_rows && bb.rows_pad ? (bb.out_rows + T - 1) / T : 0;
     const int64_t ny0 = gx_a ? (a.rows_pad + T - 1) / T : 0, ny1 = gx_b ? (bb.rows_pad + T - 1) / T : 0;
