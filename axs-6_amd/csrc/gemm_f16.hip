@@ -44,8 +44,8 @@ struct GemmK {
 };
 
 template <int BM, int BN>
-__device__ __forceinline__ void tile_origin(const GemmK& g, int& m0, int& n0) {
-    tile_origin_mn<BM, BN>(g.M, g.N, (int)blockIdx.x, m0, n0);
+__device__ __forceinline__ void tile_origin(const GemmK& g, int bx, int& m0, int& n0) {
+    tile_origin_mn<BM, BN>(g.M, g.N, bx, m0, n0);
 }
 
 // The epilogue through LDS, after the K loop.  Each wave stages its 32-row
@@ -57,7 +57,7 @@ __device__ __forceinline__ void tile_origin(const GemmK& g, int& m0, int& n0) {
 // needed.
 template <int WM, int WN>
 __device__ __forceinline__ void gemm_epilogue(const GemmK& g, const WaveAcc<WM, WN>& acc, char* smem, int m0,
-                                              int n0, int wm, int wn, int wave, int lane) {
+                                              int n0, int wm, int wn, int wave, int lane, int by) {
     constexpr int LDW = WN + 4;
     constexpr int LANES_PER_ROW = WN / 4;
     static_assert(64 % LANES_PER_ROW == 0 && 32 % (64 / LANES_PER_ROW) == 0, "wave tile width");
@@ -87,7 +87,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmK& g, const WaveAcc<WM, 
         rexp_l[q] = (g.row_exp && grow < g.M) ? g.row_exp[grow] : 0;
     }
     const int esize = g.out_dtype == AXS6_F32 ? 4 : 2;
-    void* const out = reinterpret_cast<char*>(g.out) + (int64_t)blockIdx.y * g.split_stride * esize;
+    void* const out = reinterpret_cast<char*>(g.out) + (int64_t)by * g.split_stride * esize;
     const bool vec = (g.ldo % 4 == 0) && ((uintptr_t)out % (4 * esize) == 0);
     const bool nt = g.split_stride == 0;     // final output: streaming stores
     const int row0 = m0 + wm * WM;
@@ -109,8 +109,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmK& g, const WaveAcc<WM, 
 // registers are spent on staging.  Lane l of a load instruction lands at
 // byte 16*l of its 1 KiB, i.e. row l/8, slot l%8, and therefore fetches
 // logical chunk (l%8) ^ key(row) -- the same XOR layout the fragment reads use.
+// Output tile bx (before the XCD remap) and K split by of g.
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int LW>
-__global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(GemmK g) {
+__device__ __forceinline__ void gemm_lds_body(const GemmK& g, int bx, int by) {
 #if defined(__HIP_DEVICE_COMPILE__)  // LDS-DMA builtins exist only in the device pass
     constexpr int NW = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     extern __shared__ __align__(16) char smem[];
 
     int m0, n0;
-    tile_origin<BM, BN>(g, m0, n0);
+    tile_origin<BM, BN>(g, bx, m0, n0);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -158,7 +159,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     // split-K: this workgroup's range of K-steps (k_iters counts 64-half steps)
     static_assert(kGemmK % BK == 0, "K-slab must divide the padding unit");
     const int per = g.k_iters * (kGemmK / BK);
-    const int kbeg = blockIdx.y * per;
+    const int kbeg = by * per;
     const int KT = min(per, g.Kp / BK - kbeg);
 #pragma unroll
     for (int i = 0; i < A_INST; ++i) a_goff[i] += kbeg * RB;
@@ -217,8 +218,30 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
     }
 
     static_assert(NW * 32 * (WN + 4) * 4 <= STAGES * SLAB, "epilogue staging must fit in the slab LDS");
-    gemm_epilogue<WM, WN>(g, acc, smem, m0, n0, wm, wn, wave, lane);
+    gemm_epilogue<WM, WN>(g, acc, smem, m0, n0, wm, wn, wave, lane, by);
 #endif
+}
+
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int LW>
+__global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(GemmK g) {
+    gemm_lds_body<BM, BN, BK, STAGES, WGM, WGN, LW>(g, (int)blockIdx.x, (int)blockIdx.y);
+}
+
+// Two independent GEMMs of one configuration in one launch (the backward's dX
+// and dW): workgroups below n0 take g0's tiles x splits (tile-fastest, as
+// the grid of a launch of its own orders them), the rest g1's.  n0 is g0's
+// count rounded up to a multiple of 8, so both keep their own workgroup-to-XCD
+// placement; the workgroups in between exit at once.
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int LW>
+__global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_pair_kernel(GemmK g0, GemmK g1, int n0,
+                                                                                 int t0, int s0, int t1) {
+    const int b = (int)blockIdx.x;
+    if (b < n0) {
+        if (b < t0 * s0) gemm_lds_body<BM, BN, BK, STAGES, WGM, WGN, LW>(g0, b % t0, b / t0);
+    } else {
+        const int c = b - n0;
+        gemm_lds_body<BM, BN, BK, STAGES, WGM, WGN, LW>(g1, c % t1, c / t1);
+    }
 }
 
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int LW = WGM * WGN>
@@ -234,6 +257,23 @@ int run_gemm_lds(const GemmK& k, int splits, hipStream_t st) {
     gemm_f16_nt_lds_kernel<BM, BN, BK, STAGES, WGM, WGN, LW>
         <<<dim3((unsigned)tiles, (unsigned)splits), WGM * WGN * 64, lds, st>>>(k);
     return check_launch("gemm_f16_lds");
+}
+
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int LW = WGM * WGN>
+int run_gemm_lds_pair(const GemmK& k0, int s0, const GemmK& k1, int s1, hipStream_t st) {
+    const int t0 = ((k0.M + BM - 1) / BM) * ((k0.N + BN - 1) / BN);
+    const int t1 = ((k1.M + BM - 1) / BM) * ((k1.N + BN - 1) / BN);
+    const int n0 = (t0 * s0 + 7) / 8 * 8;
+    const size_t lds = (size_t)STAGES * (BM + BN) * BK * 2;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void*)gemm_f16_nt_lds_pair_kernel<BM, BN, BK, STAGES, WGM, WGN, LW>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        attr_set = true;
+    }
+    gemm_f16_nt_lds_pair_kernel<BM, BN, BK, STAGES, WGM, WGN, LW>
+        <<<dim3((unsigned)(n0 + t1 * s1)), WGM * WGN * 64, lds, st>>>(k0, k1, n0, t0, s0, t1);
+    return check_launch("gemm_f16_lds_pair");
 }
 
 // Split-K finish: out[m, n] = ldexp(sum_z partial[z, m, n], row_exp[m] +
@@ -407,6 +447,81 @@ TailCut tail_cut(int64_t M, int64_t N) {
 }  // namespace
 
 static int launch_gemm_one(const GemmArgs& a, hipStream_t st, bool cut);
+static int launch_split_reduce(const GemmArgs& a, int splits, hipStream_t st);
+
+namespace {
+
+// Kernel variant, split count and kernel arguments of a GEMM that is not cut.
+enum GemmVariant { kVarBig = 0, kVarSmall = 1, kVarNarrow = 2, kVarNarrow3 = 3 };
+struct GemmPlan { int variant; int splits; GemmK k; };
+
+int gemm_plan(const GemmArgs& a, GemmPlan* p) {
+    const int iters = (int)(a.Kp / kGemmK);
+    int splits = 1, per = iters;
+    if (a.split_partial) {
+        splits = gemm_split_count(a.M, a.N, a.Kp);
+        per = (iters + splits - 1) / splits;
+        if (a.split_bytes < gemm_split_bytes(a.M, a.N, a.Kp))
+            return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: split-K buffer of %zu bytes, need %zu", a.split_bytes,
+                        gemm_split_bytes(a.M, a.N, a.Kp));
+    }
+    const bool split = splits > 1;
+    p->k = GemmK{a.A, a.lda, a.B, a.ldb, (int)a.M, (int)a.N, (int)a.Kp,
+                 split ? nullptr : a.row_exp, split ? nullptr : a.col_exp, split ? nullptr : a.glob_exp, a.glob_add,
+                 split ? nullptr : a.bias, split ? (void*)a.split_partial : a.out, split ? a.N : a.ldo,
+                 split ? (int)AXS6_F32 : a.out_dtype, per, split ? a.M * a.N : 0};
+    p->splits = splits;
+    const int cfg = pick_cfg(a.M, a.N);
+    // a long contraction on the narrow tiles: a third slab in flight
+    // (2048 x 768, K 3072: 28.5 -> 21.3 us; at K <= 1024 it costs 3-5%)
+    p->variant = cfg == kCfgSmall ? kVarSmall
+                 : cfg == kCfgNarrow ? (per >= kNarrowDeepSteps ? kVarNarrow3 : kVarNarrow) : kVarBig;
+    return AXS6_OK;
+}
+
+int check_gemm_args(const GemmArgs& a) {
+    if (a.Kp % 64 != 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: Kp (%lld) must be a multiple of 64", (long long)a.Kp);
+    if (a.lda % 8 || a.ldb % 8 || (uintptr_t)a.A % 16 || (uintptr_t)a.B % 16)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: operands must be 16-byte aligned with ld a multiple of 8");
+    if (a.Kp > a.lda || a.Kp > a.ldb) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: Kp exceeds the leading dimension");
+    if (a.ldo < a.N) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: ldo (%lld) is smaller than N (%lld)",
+                                 (long long)a.ldo, (long long)a.N);
+    // buffer offsets are 32-bit: every operand byte (plus one tile of rows) must be addressable
+    if ((a.M + 256) * a.lda * 2 >= ((int64_t)1 << 31) || (a.N + 256) * a.ldb * 2 >= ((int64_t)1 << 31))
+        return fail(AXS6_ERR_UNSUPPORTED, "gemm: operand larger than 2 GiB");
+    if (a.M > INT_MAX || a.N > INT_MAX || a.Kp > INT_MAX)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: dimension exceeds int32");
+    return AXS6_OK;
+}
+
+}  // namespace
+
+int launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t st) {
+    const TailCut ca = tail_cut(a.M, a.N), cb = tail_cut(b.M, b.N);
+    GemmPlan pa, pb;
+    int rc;
+    const bool empty = a.M == 0 || a.N == 0 || b.M == 0 || b.N == 0;
+    if (empty || ca.rows || ca.cols || cb.rows || cb.cols || check_gemm_args(a) || check_gemm_args(b) ||
+        gemm_plan(a, &pa) || gemm_plan(b, &pb) || pa.variant != pb.variant || pa.variant == kVarBig ||
+        (pa.splits > 1 && pb.splits > 1)) {
+        // one launch each: shapes the pair cannot share, the split buffer both
+        // need, or the 256 x 256 tiles -- those launches run whole rounds of
+        // tiles, and mixing two problems' tiles in one grid measured 1% slower
+        // (8192 x 4096 x 11008 forward + backward 2.24 -> 2.26 ms)
+        if ((rc = launch_gemm_f16(a, st))) return rc;
+        return launch_gemm_f16(b, st);
+    }
+    switch (pa.variant) {
+        case kVarSmall: rc = run_gemm_lds_pair<128, 128, 64, 2, 2, 2>(pa.k, pa.splits, pb.k, pb.splits, st); break;
+        case kVarNarrow3: rc = run_gemm_lds_pair<128, 64, 64, 3, 2, 2>(pa.k, pa.splits, pb.k, pb.splits, st); break;
+        case kVarNarrow: rc = run_gemm_lds_pair<128, 64, 64, 2, 2, 2>(pa.k, pa.splits, pb.k, pb.splits, st); break;
+        default: rc = run_gemm_lds_pair<256, 256, 64, 2, 2, 4, 4>(pa.k, pa.splits, pb.k, pb.splits, st); break;
+    }
+    if (rc) return rc;
+    if (pa.splits > 1 && (rc = launch_split_reduce(a, pa.splits, st))) return rc;
+    if (pb.splits > 1 && (rc = launch_split_reduce(b, pb.splits, st))) return rc;
+    return AXS6_OK;
+}
 
 bool gemm_splits(const GemmArgs& a) {
     if (!a.split_partial || a.M == 0 || a.N == 0) return false;
@@ -419,17 +534,8 @@ int launch_gemm_f16(const GemmArgs& a, hipStream_t st) { return launch_gemm_one(
 
 static int launch_gemm_one(const GemmArgs& a, hipStream_t st, bool cut) {
     if (a.M == 0 || a.N == 0) return AXS6_OK;
-    if (a.Kp % 64 != 0) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: Kp (%lld) must be a multiple of 64", (long long)a.Kp);
-    if (a.lda % 8 || a.ldb % 8 || (uintptr_t)a.A % 16 || (uintptr_t)a.B % 16)
-        return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: operands must be 16-byte aligned with ld a multiple of 8");
-    if (a.Kp > a.lda || a.Kp > a.ldb) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: Kp exceeds the leading dimension");
-    if (a.ldo < a.N) return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: ldo (%lld) is smaller than N (%lld)",
-                                 (long long)a.ldo, (long long)a.N);
-    // buffer offsets are 32-bit: every operand byte (plus one tile of rows) must be addressable
-    if ((a.M + 256) * a.lda * 2 >= ((int64_t)1 << 31) || (a.N + 256) * a.ldb * 2 >= ((int64_t)1 << 31))
-        return fail(AXS6_ERR_UNSUPPORTED, "gemm: operand larger than 2 GiB");
-    if (a.M > INT_MAX || a.N > INT_MAX || a.Kp > INT_MAX)
-        return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: dimension exceeds int32");
+    int rc0 = check_gemm_args(a);
+    if (rc0) return rc0;
     if (cut) {
         const TailCut c = tail_cut(a.M, a.N);
         if (c.rows || c.cols) {
@@ -456,33 +562,20 @@ static int launch_gemm_one(const GemmArgs& a, hipStream_t st, bool cut) {
             return rc ? rc : launch_gemm_one(tail, st, false);
         }
     }
-    const int iters = (int)(a.Kp / kGemmK);
-    int splits = 1, per = iters;
-    if (a.split_partial) {
-        splits = gemm_split_count(a.M, a.N, a.Kp);
-        per = (iters + splits - 1) / splits;
-        if (a.split_bytes < gemm_split_bytes(a.M, a.N, a.Kp))
-            return fail(AXS6_ERR_INVALID_ARGUMENT, "gemm: split-K buffer of %zu bytes, need %zu", a.split_bytes,
-                        gemm_split_bytes(a.M, a.N, a.Kp));
+    GemmPlan p;
+    int rc = gemm_plan(a, &p);
+    if (rc) return rc;
+    switch (p.variant) {
+        case kVarSmall: rc = run_gemm_lds<128, 128, 64, 2, 2, 2>(p.k, p.splits, st); break;
+        case kVarNarrow3: rc = run_gemm_lds<128, 64, 64, 3, 2, 2>(p.k, p.splits, st); break;
+        case kVarNarrow: rc = run_gemm_lds<128, 64, 64, 2, 2, 2>(p.k, p.splits, st); break;
+        default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 4>(p.k, p.splits, st); break;   // kVarBig
     }
-    const bool split = splits > 1;
-    GemmK k{a.A, a.lda, a.B, a.ldb, (int)a.M, (int)a.N, (int)a.Kp,
-            split ? nullptr : a.row_exp, split ? nullptr : a.col_exp, split ? nullptr : a.glob_exp, a.glob_add,
-            split ? nullptr : a.bias, split ? (void*)a.split_partial : a.out, split ? a.N : a.ldo,
-            split ? (int)AXS6_F32 : a.out_dtype, per, split ? a.M * a.N : 0};
-    int rc;
-    const int cfg = pick_cfg(a.M, a.N);
-    switch (cfg) {
-        case kCfgSmall: rc = run_gemm_lds<128, 128, 64, 2, 2, 2>(k, splits, st); break;
-        case kCfgNarrow:
-            // a long contraction on the small tiles: a third slab in flight
-            // (2048 x 768, K 3072: 28.5 -> 21.3 us; at K <= 1024 it costs 3-5%)
-            if (per >= kNarrowDeepSteps) rc = run_gemm_lds<128, 64, 64, 3, 2, 2>(k, splits, st);
-            else rc = run_gemm_lds<128, 64, 64, 2, 2, 2>(k, splits, st);
-            break;
-        default: rc = run_gemm_lds<256, 256, 64, 2, 2, 4, 4>(k, splits, st); break;   // kCfgBig
-    }
-    if (rc || !split) return rc;
+    if (rc || p.splits == 1) return rc;
+    return launch_split_reduce(a, p.splits, st);
+}
+
+static int launch_split_reduce(const GemmArgs& a, int splits, hipStream_t st) {
     const int64_t groups = a.M * ((a.N + 3) / 4);
     const int64_t sblocks = (groups + kSplitGroups - 1) / kSplitGroups;
     const int64_t rblocks = a.red_out && a.red_cols > 0 ? (a.red_cols + kRedCols - 1) / kRedCols : 0;

@@ -61,12 +61,10 @@ __device__ __forceinline__ int kslot(int q, int t) {
     return Elem<DT>::V == 4 ? (t < 4 ? 4 * q + t : 16 + 4 * q + (t - 4)) : 8 * q + t;
 }
 
-// The loads are unconditional (the caller passes a row and K tile inside the
-// operand): a load under a branch -- a lane mask for rows past M or N, or a
-// wave-uniform one for tiles past the wave's range -- leaves the compiler's
-// wait-count insertion two paths with different loads outstanding, and it then
-// waits for every load, the next tile's included, before the current tile is
-// used, which serialises each K step behind a full memory round trip.
+// No lane mask on the loads (the caller passes a row inside the operand): a
+// load under a branch leaves the compiler's wait-count insertion paths with
+// different loads outstanding, and it then waits for every load, the next
+// tile's included, before the current tile is used (see the K loop).
 template <int DT>
 __device__ __forceinline__ void load8(const typename Elem<DT>::S* row, int kt, int q, u32x4 (&v)[2]) {
     using S = typename Elem<DT>::S;
@@ -154,7 +152,7 @@ __device__ __forceinline__ void stage_x(const FusedK& k, float* xl, const float*
     }
 }
 
-template <int DT, int WM, int TN, int NW, bool QX, bool XL, int PF = 1>
+template <int DT, int WM, int TN, int NW, bool QX, bool XL>
 __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
     using E = Elem<DT>;
     using S = typename E::S;
@@ -193,29 +191,25 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
         wrow[j] = ws + (int64_t)(wlive[j] ? r : 0) * k.K;
     }
 
-    // PF K tiles are loaded ahead of the one being quantized and multiplied
-    // (a ring of PF + 1 register buffers, rotated by full unrolling).  One is
-    // best: at M 1, K = N = 4096, 15.0 us against 16.5 / 17.6 / 23.4 us for
-    // 2 / 3 / 7 tiles ahead, and the loads alone (no FQ, no MFMA) take as
-    // long: this read pattern -- 64-byte pieces of 16 rows per instruction --
-    // streams the weight at ~4.5 TB/s and slows with more of it in flight
-    // (whole-row reads of the same bytes take 10.4-11.5 us)
-    u32x4 xv[PF + 1][WM][2], wv[PF + 1][TN][2];
-    // rows past M or N read row 0 and tiles past the wave's range the last K
-    // tile (both loaded unconditionally, see load8): an output element takes
-    // only its own row of each operand, and the rows past M or N are not
-    // stored; a tile past the range is never multiplied
+    // The next K tile is loaded while the current one is quantized and
+    // multiplied (two register buffers).  Deeper prefetch was slower: at M 1,
+    // K = N = 4096, 15.0 us against 16.5 / 17.6 / 23.4 us for 2 / 3 / 7 tiles
+    // ahead, and the loads alone (no FQ, no MFMA) take as long -- this read
+    // pattern (64-byte pieces of 16 rows per instruction) streams the weight
+    // at ~4.5 TB/s and slows with more of it in flight; whole-row reads of the
+    // same bytes take 10.4-11.5 us.  Rows past M or N read row 0: an output
+    // element takes only its own row of each operand, and those rows are not
+    // stored.
+    u32x4 xv[2][WM][2], wv[2][TN][2];
     auto load_tile = [&](int kt, u32x4 (&xd)[WM][2], u32x4 (&wd)[TN][2]) {
-        const int ktl = kt < nkt ? kt : nkt - 1;
         if constexpr (!XL) {
 #pragma unroll
-            for (int i = 0; i < WM; ++i) load8<DT>(xrow[i], ktl, q, xd[i]);
+            for (int i = 0; i < WM; ++i) load8<DT>(xrow[i], kt, q, xd[i]);
         }
 #pragma unroll
-        for (int j = 0; j < TN; ++j) load8<DT>(wrow[j], ktl, q, wd[j]);
+        for (int j = 0; j < TN; ++j) load8<DT>(wrow[j], kt, q, wd[j]);
     };
-#pragma unroll
-    for (int p = 0; p < PF; ++p) load_tile(kt0 + p, xv[p], wv[p]);
+    if (kt0 < kt1) load_tile(kt0, xv[0], wv[0]);
     stage_tables(lut_s, band_w, k.lut, k.band);
     if constexpr (XL) {
         stage_x<DT, QX>(k, xl_s, lut_s, band_s, NW * 64);
@@ -259,18 +253,27 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[i][t], wf[j][t], acc[i][j], 0, 0, 0);
     };
-    // the ring position of tile kt is (kt - kt0) % (PF + 1); unrolling the
-    // loop by PF + 1 keeps every buffer index a constant.  Every iteration
-    // issues the loads of PF + 1 tiles whether or not its steps run (only the
-    // multiplications are conditional), so each loop path has the same loads
-    // outstanding and a step waits for its own tile only
+    // Steady state: two tiles per iteration, both prefetches inside the
+    // wave's range; the last one or two tiles after the loop.  No load sits
+    // under a branch inside the loop: the compiler's wait-count insertion would
+    // see loop paths with different loads outstanding and wait for every
+    // load, the next tile's included, before each tile (a full memory round
+    // trip per K step; 16.3 -> 15.0 us at M 1 once removed), and loading
+    // tiles past the range unconditionally instead costs a wave of one or two
+    // tiles its time (256 x 512 x 512: 7.7 -> 10.0 us).
     int kt = kt0;
-    for (; kt < kt1; kt += PF + 1) {
-#pragma unroll
-        for (int p = 0; p <= PF; ++p) {
-            load_tile(kt + p + PF, xv[(p + PF) % (PF + 1)], wv[(p + PF) % (PF + 1)]);
-            if (kt + p < kt1) step(kt + p, xv[p], wv[p]);
-        }
+    for (; kt + 2 < kt1; kt += 2) {
+        load_tile(kt + 1, xv[1], wv[1]);
+        step(kt, xv[0], wv[0]);
+        load_tile(kt + 2, xv[0], wv[0]);
+        step(kt + 1, xv[1], wv[1]);
+    }
+    if (kt + 1 < kt1) {
+        load_tile(kt + 1, xv[1], wv[1]);
+        step(kt, xv[0], wv[0]);
+        step(kt + 1, xv[1], wv[1]);
+    } else if (kt < kt1) {
+        step(kt, xv[0], wv[0]);
     }
 
     // the NW partial tiles, added in wave order: accumulator r of block
@@ -294,7 +297,7 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
     }
 }
 
-template <int DT, int WM, int TN, int NW, bool XL = false, int PF = 1>
+template <int DT, int WM, int TN, int NW, bool XL = false>
 void launch_cfg(const FusedK& k, bool qx, hipStream_t st) {
     const int tiles = ((k.M + 16 * WM - 1) / (16 * WM)) * ((k.N + 16 * TN - 1) / (16 * TN));
     const size_t xl_bytes = XL ? (size_t)k.M * (k.K + 4) * sizeof(float) : 0;
@@ -303,15 +306,15 @@ void launch_cfg(const FusedK& k, bool qx, hipStream_t st) {
         // CU's 160 KiB): raise the per-kernel limit once
         static bool attr_set = false;
         if (!attr_set) {
-            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, true, XL, PF>,
+            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, true, XL>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kXlBytes);
-            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, false, XL, PF>,
+            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, false, XL>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kXlBytes);
             attr_set = true;
         }
     }
-    if (qx) fused_linear_kernel<DT, WM, TN, NW, true, XL, PF><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
-    else fused_linear_kernel<DT, WM, TN, NW, false, XL, PF><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
+    if (qx) fused_linear_kernel<DT, WM, TN, NW, true, XL><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
+    else fused_linear_kernel<DT, WM, TN, NW, false, XL><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
 }
 
 // Tile and K split by shape: one 16-row block for M <= 16 (decode), else

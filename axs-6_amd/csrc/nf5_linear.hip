@@ -268,14 +268,18 @@ int bwd_run(const BwdCall& c, const BwdLayout& L, char* ws) {
                (rc = launch_reduce_partials(partial, pack_global_chunks(M), N, db, st))) {
         return rc;
     }
-    if (need_dx && (rc = launch_gemm_f16(gx, st))) return rc;
-    if (need_dw) {
-        if (db_in_dw) {
-            gw.red_partial = partial;
-            gw.red_chunks = pack_global_chunks(M);
-            gw.red_cols = N;
-            gw.red_out = db;
-        }
+    if (db_in_dw) {
+        gw.red_partial = partial;
+        gw.red_chunks = pack_global_chunks(M);
+        gw.red_cols = N;
+        gw.red_out = db;
+    }
+    // dX and dW are independent: one launch when they share a configuration
+    if (need_dx && need_dw) {
+        if ((rc = launch_gemm_pair(gx, gw, st))) return rc;
+    } else if (need_dx) {
+        if ((rc = launch_gemm_f16(gx, st))) return rc;
+    } else if (need_dw) {
         if ((rc = launch_gemm_f16(gw, st))) return rc;
     }
     return AXS6_OK;
