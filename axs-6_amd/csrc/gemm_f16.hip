@@ -232,15 +232,22 @@ __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_kernel(Gemm
 // the grid of a launch of its own orders them), the rest g1's.  n0 is g0's
 // count rounded up to a multiple of 8, so both keep their own workgroup-to-XCD
 // placement; the workgroups in between exit at once.
+// A fixed-order column sum (reduce_partials_block, 256 threads) riding in a
+// GEMM launch: `blocks` workgroups after the GEMM tiles.
+struct GemmRedJob { const float* partial; int64_t chunks; int64_t cols; float* out; int blocks; };
+
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int LW>
 __global__ __launch_bounds__(WGM * WGN * 64, 1) void gemm_f16_nt_lds_pair_kernel(GemmK g0, GemmK g1, int n0,
-                                                                                 int t0, int s0, int t1) {
+                                                                                 int t0, int s0, int t1, int s1,
+                                                                                 GemmRedJob red) {
     const int b = (int)blockIdx.x;
     if (b < n0) {
         if (b < t0 * s0) gemm_lds_body<BM, BN, BK, STAGES, WGM, WGN, LW>(g0, b % t0, b / t0);
-    } else {
+    } else if (b < n0 + t1 * s1) {
         const int c = b - n0;
         gemm_lds_body<BM, BN, BK, STAGES, WGM, WGN, LW>(g1, c % t1, c / t1);
+    } else if constexpr (WGM * WGN * 64 == 256) {
+        reduce_partials_block(red.partial, red.chunks, red.cols, red.out, b - n0 - t1 * s1);
     }
 }
 
@@ -260,7 +267,7 @@ int run_gemm_lds(const GemmK& k, int splits, hipStream_t st) {
 }
 
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int LW = WGM * WGN>
-int run_gemm_lds_pair(const GemmK& k0, int s0, const GemmK& k1, int s1, hipStream_t st) {
+int run_gemm_lds_pair(const GemmK& k0, int s0, const GemmK& k1, int s1, const GemmRedJob& red, hipStream_t st) {
     const int t0 = ((k0.M + BM - 1) / BM) * ((k0.N + BN - 1) / BN);
     const int t1 = ((k1.M + BM - 1) / BM) * ((k1.N + BN - 1) / BN);
     const int n0 = (t0 * s0 + 7) / 8 * 8;
@@ -272,7 +279,7 @@ int run_gemm_lds_pair(const GemmK& k0, int s0, const GemmK& k1, int s1, hipStrea
         attr_set = true;
     }
     gemm_f16_nt_lds_pair_kernel<BM, BN, BK, STAGES, WGM, WGN, LW>
-        <<<dim3((unsigned)(n0 + t1 * s1)), WGM * WGN * 64, lds, st>>>(k0, k1, n0, t0, s0, t1);
+        <<<dim3((unsigned)(n0 + t1 * s1 + red.blocks)), WGM * WGN * 64, lds, st>>>(k0, k1, n0, t0, s0, t1, s1, red);
     return check_launch("gemm_f16_lds_pair");
 }
 
@@ -496,14 +503,26 @@ int check_gemm_args(const GemmArgs& a) {
 
 }  // namespace
 
-int launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t st) {
+namespace {
+// Whether a and b run as one pair launch (plans filled when they do).
+bool pair_plans(const GemmArgs& a, const GemmArgs& b, GemmPlan* pa, GemmPlan* pb) {
     const TailCut ca = tail_cut(a.M, a.N), cb = tail_cut(b.M, b.N);
+    const bool empty = a.M == 0 || a.N == 0 || b.M == 0 || b.N == 0;
+    return !(empty || ca.rows || ca.cols || cb.rows || cb.cols || check_gemm_args(a) || check_gemm_args(b) ||
+             gemm_plan(a, pa) || gemm_plan(b, pb) || pa->variant != pb->variant || pa->variant == kVarBig ||
+             (pa->splits > 1 && pb->splits > 1));
+}
+}  // namespace
+
+bool gemm_pairs(const GemmArgs& a, const GemmArgs& b) {
+    GemmPlan pa, pb;
+    return pair_plans(a, b, &pa, &pb);
+}
+
+int launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t st) {
     GemmPlan pa, pb;
     int rc;
-    const bool empty = a.M == 0 || a.N == 0 || b.M == 0 || b.N == 0;
-    if (empty || ca.rows || ca.cols || cb.rows || cb.cols || check_gemm_args(a) || check_gemm_args(b) ||
-        gemm_plan(a, &pa) || gemm_plan(b, &pb) || pa.variant != pb.variant || pa.variant == kVarBig ||
-        (pa.splits > 1 && pb.splits > 1)) {
+    if (!pair_plans(a, b, &pa, &pb)) {
         // one launch each: shapes the pair cannot share, the split buffer both
         // need, or the 256 x 256 tiles -- those launches run whole rounds of
         // tiles, and mixing two problems' tiles in one grid measured 1% slower
@@ -511,11 +530,14 @@ int launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t st) {
         if ((rc = launch_gemm_f16(a, st))) return rc;
         return launch_gemm_f16(b, st);
     }
-    switch (pa.variant) {
-        case kVarSmall: rc = run_gemm_lds_pair<128, 128, 64, 2, 2, 2>(pa.k, pa.splits, pb.k, pb.splits, st); break;
-        case kVarNarrow3: rc = run_gemm_lds_pair<128, 64, 64, 3, 2, 2>(pa.k, pa.splits, pb.k, pb.splits, st); break;
-        case kVarNarrow: rc = run_gemm_lds_pair<128, 64, 64, 2, 2, 2>(pa.k, pa.splits, pb.k, pb.splits, st); break;
-        default: rc = run_gemm_lds_pair<256, 256, 64, 2, 2, 4, 4>(pa.k, pa.splits, pb.k, pb.splits, st); break;
+    // b's reduction job rides in its split reduction when b splits, else here
+    const bool red_here = pb.splits == 1 && b.red_out && b.red_cols > 0;
+    const GemmRedJob red{b.red_partial, b.red_chunks, b.red_cols, b.red_out,
+                         red_here ? (int)((b.red_cols + kRedCols - 1) / kRedCols) : 0};
+    switch (pa.variant) {   // the small-tile variants: 256 threads, as the reduction takes
+        case kVarSmall: rc = run_gemm_lds_pair<128, 128, 64, 2, 2, 2>(pa.k, pa.splits, pb.k, pb.splits, red, st); break;
+        case kVarNarrow3: rc = run_gemm_lds_pair<128, 64, 64, 3, 2, 2>(pa.k, pa.splits, pb.k, pb.splits, red, st); break;
+        default: rc = run_gemm_lds_pair<128, 64, 64, 2, 2, 2>(pa.k, pa.splits, pb.k, pb.splits, red, st); break;
     }
     if (rc) return rc;
     if (pa.splits > 1 && (rc = launch_split_reduce(a, pa.splits, st))) return rc;

@@ -121,9 +121,11 @@ int launch_gemm_f16(const GemmArgs& g, hipStream_t st);
 // Whether launch_gemm_f16(g) splits K (and so runs a reduction launch after the GEMM).
 bool gemm_splits(const GemmArgs& g);
 // a and b (independent; at most one of them splitting K, since split-K partials
-// share one buffer) in one launch when they take the same kernel configuration,
-// else one launch each; each split's reduction follows.
+// share one buffer) in one launch when they take the same small-tile kernel
+// configuration (gemm_pairs), else one launch each; each split's reduction
+// follows.  b's red_* job runs in b's split reduction, or in the pair launch.
 int launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t st);
+bool gemm_pairs(const GemmArgs& a, const GemmArgs& b);
 int gemm_split_count(int64_t M, int64_t N, int64_t Kp);
 size_t gemm_split_bytes(int64_t M, int64_t N, int64_t Kp);
 

@@ -239,7 +239,8 @@ int bwd_run(const BwdCall& c, const BwdLayout& L, char* ws) {
     const TransposeF16 tx{(const _Float16*)c.xq_f16, M, Kp, Kp, xqt, Kp, Mp, Mp};
     const TransposeF16* t0 = need_dx ? &tw : &tx;
     const TransposeF16* t1 = need_dx && need_dw ? &tx : nullptr;
-    const bool db_in_dw = need_db && need_dw && gemm_splits(gw);
+    // db rides in the dW GEMM's split reduction, or in the dX + dW pair launch
+    const bool db_in_dw = need_db && need_dw && (gemm_splits(gw) || (need_dx && gemm_pairs(gx, gw)));
     const bool t_early = (need_dx || need_dw) && (!need_db || db_in_dw);
 
     // rows of at most 256 values: one statistics launch writes the row shifts
@@ -260,8 +261,8 @@ int bwd_run(const BwdCall& c, const BwdLayout& L, char* ws) {
         if ((rc = launch_pack_t(p, t, st))) return rc;
     }
     // the bias gradient's ordered reduction of the pack's partial sums: in the
-    // dW GEMM's split-K reduction launch, else in the transposes' launch (or
-    // alone when no operand is transposed)
+    // dW GEMM's split-K reduction launch or the dX + dW pair launch, else in
+    // the transposes' launch (or alone when no operand is transposed)
     if (!t_early && (need_dx || need_dw)) {
         if ((rc = launch_transpose_f16(*t0, t1, st, partial, pack_global_chunks(M), N, db))) return rc;
     } else if (need_db && !db_in_dw && !(need_dx || need_dw) &&
