@@ -23,6 +23,7 @@ from axs.unified.backend import (
     set_backend,
 )
 from axs.unified.functional_unified import (
+    axs_linear_group_unified,
     axs_linear_unified,
     axs_matmul_unified,
     fake_quantize_unified,
@@ -70,6 +71,7 @@ __all__ = [
     "REVERSE_NF5_LUT",
     "fake_quantize_unified",
     "axs_linear_unified",
+    "axs_linear_group_unified",
     "axs_matmul_unified",
     "AXSLinearUnified",
     "AXS6Linear",

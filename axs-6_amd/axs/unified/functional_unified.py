@@ -94,6 +94,44 @@ def axs_linear_unified(
     return hip_linear.linear_autograd(input, weight, bias, block_size, quantize_input, quantize_grad)
 
 
+def axs_linear_group_unified(
+    input: torch.Tensor,
+    weights: list[torch.Tensor] | tuple[torch.Tensor, ...],
+    biases: list[torch.Tensor | None] | tuple[torch.Tensor | None, ...] | None = None,
+    block_size: int = DEFAULT_BLOCK_SIZE,
+    quantize_input: bool = True,
+    quantize_grad: bool = True,
+) -> tuple[torch.Tensor, ...]:
+    """Several quantized linears of one input -- ``(axs_linear_unified(input,
+    w_i, b_i) for each i)``, e.g. the q/k/v projections of self-attention --
+    as one: the weights stacked along the output dim, so the input is packed
+    once and forward and backward each run one linear (one GEMM per
+    direction instead of one per weight).  Each output equals its own
+    ``axs_linear_unified`` forward bit for bit (same operand rows, same
+    contraction order); in the backward the input gradient is the contraction
+    over all stacked outputs at once, and the stochastic rounding of the
+    output gradient draws one stream for the stacked rows (both within the
+    linear's tolerance).  This function is this library's; the reference runs
+    the projections one by one (``modules_unified.py:235-243``)."""
+    weights = list(weights)
+    if not weights:
+        return ()
+    biases = [None] * len(weights) if biases is None else list(biases)
+    if len(biases) != len(weights):
+        raise ValueError(f"axs_linear_group_unified: {len(weights)} weights but {len(biases)} biases")
+    if len(weights) == 1:
+        return (axs_linear_unified(input, weights[0], biases[0], block_size, quantize_input, quantize_grad),)
+    sizes = [w.shape[0] for w in weights]
+    w = torch.cat(weights, 0)
+    if all(b is None for b in biases):
+        b = None
+    else:
+        b = torch.cat([bi if bi is not None else torch.zeros(n, dtype=w.dtype, device=w.device)
+                       for bi, n in zip(biases, sizes)])
+    y = axs_linear_unified(input, w, b, block_size, quantize_input, quantize_grad)
+    return tuple(y.split(sizes, dim=-1))
+
+
 def axs_matmul_unified(
     a: torch.Tensor,
     b: torch.Tensor,

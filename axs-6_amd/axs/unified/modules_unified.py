@@ -27,7 +27,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from axs.core import DEFAULT_BLOCK_SIZE
-from axs.unified.functional_unified import axs_linear_unified, fake_quantize_unified
+from axs.unified.functional_unified import axs_linear_group_unified, axs_linear_unified, fake_quantize_unified
 
 
 class AXSLinearUnified(nn.Module):
@@ -148,11 +148,27 @@ class AXSMultiheadAttentionUnified(nn.Module):
         self.out_proj = AXSLinearUnified(embed_dim, embed_dim, bias=bias, block_size=block_size)
         self.scale = self.head_dim ** -0.5
 
+    def _projections(self, query, key, value):
+        """q, k, v: in self-attention (one input tensor) the three projections
+        run as one grouped linear (the input packed once, one GEMM per
+        direction), else one by one as the reference does -- also when a
+        projection has hooks, which see only calls of the module itself."""
+        p = (self.q_proj, self.k_proj, self.v_proj)
+        grouped = (query is key and key is value and all(type(m) is AXSLinearUnified for m in p)
+                   and not any(m._warmup_active or m._forward_hooks or m._forward_pre_hooks for m in p)
+                   and len({(m.block_size, m.quantize_input, m.quantize_grad) for m in p}) == 1)
+        if not grouped:
+            return self.q_proj(query), self.k_proj(key), self.v_proj(value)
+        m = p[0]
+        return axs_linear_group_unified(query, [x.weight for x in p], [x.bias for x in p], m.block_size,
+                                        m.quantize_input, m.quantize_grad)
+
     def forward(self, query, key, value, attn_mask=None):
         B, T = query.shape[0], query.shape[1]
-        q = self.q_proj(query).reshape(B, T, self.num_heads, self.head_dim).transpose(1, 2)
-        k = self.k_proj(key).reshape(B, key.shape[1], self.num_heads, self.head_dim).transpose(1, 2)
-        v = self.v_proj(value).reshape(B, value.shape[1], self.num_heads, self.head_dim).transpose(1, 2)
+        qp, kp, vp = self._projections(query, key, value)
+        q = qp.reshape(B, T, self.num_heads, self.head_dim).transpose(1, 2)
+        k = kp.reshape(B, key.shape[1], self.num_heads, self.head_dim).transpose(1, 2)
+        v = vp.reshape(B, value.shape[1], self.num_heads, self.head_dim).transpose(1, 2)
         scores = torch.matmul(q, k.transpose(-2, -1)) * self.scale
         if attn_mask is not None:
             scores = scores + attn_mask

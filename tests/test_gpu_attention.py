@@ -143,3 +143,59 @@ def test_attention_stagewise_parity(B, T, E, H):
         eb = (m.bias.grad.detach().double().cpu() - want_b).norm().item() / scale
         print(f"  d{n}_proj W {ew:.2e} b {eb:.2e}", flush=True)
         assert ew <= 1e-3 and eb <= 1e-3, n
+
+
+@pytest.mark.parametrize("bias", [True, False, "some"])
+def test_linear_group_matches_separate(bias):
+    """axs_linear_group_unified (weights stacked, input packed once): each
+    forward output equals its own axs_linear_unified bit for bit; the
+    backward (nearest dY) gives dX = sum_i dY_i FQ(W_i), dW_i = dY_i^T FQ(X)
+    and db_i = sum dY_i within the linear's rel-L2 1e-3 (db 1e-5) of fp64."""
+    from axs.unified import axs_linear_group_unified, axs_linear_unified
+
+    g = torch.Generator().manual_seed(11)
+    M, K, sizes = 300, 256, (256, 128, 96)
+    x = torch.randn(M, K, generator=g)
+    ws = [torch.randn(n, K, generator=g) * K ** -0.5 for n in sizes]
+    bs = [torch.randn(n, generator=g) for n in sizes]
+    if bias is False:
+        bs = [None] * 3
+    elif bias == "some":
+        bs[1] = None
+    xd = x.to(DEV).requires_grad_(True)
+    wd = [w.to(DEV).requires_grad_(True) for w in ws]
+    bd = [None if b is None else b.to(DEV).requires_grad_(True) for b in bs]
+    ys = axs_linear_group_unified(xd, wd, bd, 32, True, False)
+    assert [tuple(y.shape) for y in ys] == [(M, n) for n in sizes]
+    for y, w, b in zip(ys, wd, bd):
+        sep = axs_linear_unified(xd.detach(), w.detach(), None if b is None else b.detach(), 32, True, False)
+        assert torch.equal(y.detach(), sep), "grouped forward differs from the separate one"
+    dys = [torch.randn(M, n, generator=g) for n in sizes]
+    torch.autograd.backward(ys, [d.to(DEV) for d in dys])
+    xq = _fq64(x)
+    dx = sum(d.double() @ _fq64(w) for d, w in zip(dys, ws))
+    assert _rel(xd.grad, dx) <= 1e-3
+    for d, w, b in zip(dys, wd, bd):
+        assert _rel(w.grad, d.double().T @ xq) <= 1e-3
+        if b is not None:
+            assert _rel(b.grad, d.double().sum(0)) <= 1e-5
+
+
+def test_self_attention_groups_projections():
+    """Self-attention runs q/k/v as one grouped linear: the output equals the
+    one-by-one projections' (forced by a hook on q_proj) bit for bit."""
+    import axs.unified as u
+
+    torch.manual_seed(5)
+    mha = u.AXSMultiheadAttentionUnified(128, 4).to(DEV)
+    x = torch.randn(2, 32, 128, generator=torch.Generator().manual_seed(6)).to(DEV)
+    calls = []
+    orig = u.functional_unified.axs_linear_unified
+    torch.manual_seed(7)
+    y_grouped = mha(x, x, x)
+    h = mha.q_proj.register_forward_hook(lambda m, i, o: calls.append(1))
+    torch.manual_seed(7)
+    y_sep = mha(x, x, x)
+    h.remove()
+    assert calls == [1] and orig is u.functional_unified.axs_linear_unified
+    assert torch.equal(y_grouped, y_sep)
