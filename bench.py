@@ -513,7 +513,10 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
     is forward + cross-entropy + backward + AdamW through the Python API.
     Reported: ms/step over the steps after `warmup`, the loss curve at a few
     points, the same with the step recorded in a HIP graph and replayed
-    (graph_ms_per_step), the same for the unquantized fp32 model, and the CPU
+    (graph_ms_per_step, with torch's fused AdamW; graph_multi_tensor_adamw_*
+    with its capturable multi-tensor form, which adds two per-parameter
+    broadcast divisions per step), the same for the unquantized fp32 model,
+    and the CPU
     reference restatement's ms/step over `ref_steps` steps (host cores)."""
     import torch
 
@@ -530,10 +533,15 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
     model = minigpt.build_axs(0, "cuda")
     losses, ms = minigpt.train(model, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize)
     torch.manual_seed(5)
-    g_losses, g_ms = minigpt.train_graphed(minigpt.build_axs(0, "cuda"), x.cuda(), y.cuda(), steps, warmup=3)
+    g_losses, g_ms = minigpt.train_graphed(minigpt.build_axs(0, "cuda"), x.cuda(), y.cuda(), steps, warmup=3,
+                                           fused=True)
+    torch.manual_seed(5)
+    _, gm_ms = minigpt.train_graphed(minigpt.build_axs(0, "cuda"), x.cuda(), y.cuda(), steps, warmup=3)
     fp32 = minigpt.base_model(0).cuda()
     fp_losses, fp_ms = minigpt.train(fp32, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize)
-    fg_losses, fg_ms = minigpt.train_graphed(minigpt.base_model(0).cuda(), x.cuda(), y.cuda(), steps, warmup=3)
+    fg_losses, fg_ms = minigpt.train_graphed(minigpt.base_model(0).cuda(), x.cuda(), y.cuda(), steps, warmup=3,
+                                             fused=True)
+    _, fgm_ms = minigpt.train_graphed(minigpt.base_model(0).cuda(), x.cuda(), y.cuda(), steps, warmup=3)
     pipe = bench_pipeline(minigpt, x, y, steps=min(steps, 100), warmup=warmup)
     pts = [0, steps // 4, steps // 2, 3 * steps // 4, steps - 1]
     out = {
@@ -542,7 +550,10 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
         "loss": {str(i): round(losses[i], 4) for i in pts},
         "graph_ms_per_step": round(g_ms, 3),
         "graph_loss": {str(i): round(g_losses[i], 4) for i in pts},
+        "graph_optimizer": "AdamW(fused=True)",
+        "graph_multi_tensor_adamw_ms_per_step": round(gm_ms, 3),
         "fp32_model": {"ms_per_step": round(fp_ms, 3), "graph_ms_per_step": round(fg_ms, 3),
+                       "graph_multi_tensor_adamw_ms_per_step": round(fgm_ms, 3),
                        "loss": {str(i): round(fp_losses[i], 4) for i in pts}},
         "pipeline": pipe,
     }

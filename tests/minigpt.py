@@ -209,12 +209,14 @@ def build_reference(seed: int = 0, quantize_grad: bool = True, c: GPTConfig | No
 # ---- training loop ----------------------------------------------------------
 
 def train(model: nn.Module, x: torch.Tensor, y: torch.Tensor, steps: int, lr: float = 3e-4,
-          warmup: int = 0, sync=None, capturable: bool = False) -> tuple[list[float], float]:
+          warmup: int = 0, sync=None, capturable: bool = False, fused: bool = False) -> tuple[list[float], float]:
     """AdamW steps on one batch.  Returns (loss per step, ms per timed step).
     The first ``warmup`` steps are untimed but part of the curve.
     ``capturable`` selects AdamW's device-side step arithmetic (the form a
-    graph-replayed step uses)."""
-    opt = torch.optim.AdamW(model.parameters(), lr=lr, capturable=capturable)
+    graph-replayed step uses); ``fused`` selects torch's fused AdamW (one
+    multi-tensor update kernel, device-side step counts) instead of the
+    default multi-tensor form."""
+    opt = torch.optim.AdamW(model.parameters(), lr=lr, capturable=capturable, fused=fused)
     losses = []
     t0 = None
     for i in range(steps):
@@ -235,16 +237,18 @@ def train(model: nn.Module, x: torch.Tensor, y: torch.Tensor, steps: int, lr: fl
 
 
 def train_graphed(model: nn.Module, x: torch.Tensor, y: torch.Tensor, steps: int, lr: float = 3e-4,
-                  warmup: int = 3) -> tuple[list[float], float]:
+                  warmup: int = 3, fused: bool = False) -> tuple[list[float], float]:
     """The same AdamW training, with the step recorded once in a HIP graph and
     replayed: forward, loss, backward and the optimiser update run as one
-    graph launch (AdamW with capturable state).  The first ``warmup`` steps run
+    graph launch (AdamW with capturable state; ``fused`` selects torch's fused
+    AdamW, whose one update kernel replaces the capturable multi-tensor form's
+    two per-parameter broadcast divisions).  The first ``warmup`` steps run
     eagerly on a side stream (they initialise the optimiser state and the
     allocator pools) and are part of the loss curve; the replays are timed.
     Stochastic FQ calls inside the graph read a device counter the library
     advances after each of them, so every replay draws a fresh dither.
     Returns (loss per step, ms per replayed step)."""
-    opt = torch.optim.AdamW(model.parameters(), lr=lr, capturable=True)
+    opt = torch.optim.AdamW(model.parameters(), lr=lr, capturable=True, fused=fused)
 
     def step():
         logits = model(x)
@@ -293,13 +297,15 @@ if __name__ == "__main__":
     ap.add_argument("--steps", type=int, default=15)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--graph", action="store_true", help="record the step in a HIP graph and replay it")
+    ap.add_argument("--fused-adamw", action="store_true", help="torch's fused AdamW")
     a = ap.parse_args()
     xb, yb = batch(1)
     torch.manual_seed(5)
     m = build_axs(0, "cuda")
     if a.graph:
-        losses, ms = train_graphed(m, xb.cuda(), yb.cuda(), a.steps, warmup=a.warmup)
+        losses, ms = train_graphed(m, xb.cuda(), yb.cuda(), a.steps, warmup=a.warmup, fused=a.fused_adamw)
     else:
-        losses, ms = train(m, xb.cuda(), yb.cuda(), a.steps, warmup=a.warmup, sync=torch.cuda.synchronize)
+        losses, ms = train(m, xb.cuda(), yb.cuda(), a.steps, warmup=a.warmup, sync=torch.cuda.synchronize,
+                           fused=a.fused_adamw)
     print(f"minigpt {'graph' if a.graph else 'eager'}: {ms:.3f} ms/step over {a.steps - a.warmup} steps, "
           f"loss {losses[0]:.4f} -> {losses[-1]:.4f}", flush=True)

@@ -131,19 +131,23 @@ def test_minigpt_graph_replay_matches_eager_training():
     """The whole training step (forward, loss, backward, AdamW) recorded in one
     HIP graph and replayed trains like the eager loop.  With nearest-rounded
     dY both compute the same thing and every kernel on the path is
-    deterministic, so the loss curves are bit-identical over 30 steps (the
-    eager loop uses AdamW's capturable arithmetic too: its default form
-    rounds differently, and NF5's quantization steps amplify that ulp-level
+    deterministic, so the loss curves are bit-identical over 30 steps, for
+    AdamW's capturable multi-tensor form and for its fused form (the eager
+    loop uses the same form as the graph: the default form rounds
+    differently, and NF5's quantization steps amplify that ulp-level
     difference to ~5e-3 of the loss within 30 steps).  With the stochastic dY
     of the default modules the two runs draw different dither streams; the
     curves then agree to the AXS-vs-fp32 curve bound."""
     x, y = minigpt.batch(1)
     xd, yd = x.cuda(), y.cuda()
-    print("[minigpt: eager vs graph-replayed, nearest dY, 30 steps]", flush=True)
-    eager, _ = minigpt.train(_nearest_dy(minigpt.build_axs(0, "cuda")), xd, yd, 30, capturable=True)
-    graphed, _ = minigpt.train_graphed(_nearest_dy(minigpt.build_axs(0, "cuda")), xd, yd, 30, warmup=3)
-    print(f"  losses {eager[0]:.5f} -> {eager[-1]:.5f}", flush=True)
-    assert graphed == eager
+    for fused in (False, True):
+        print(f"[minigpt: eager vs graph-replayed, nearest dY, 30 steps, fused AdamW {fused}]", flush=True)
+        eager, _ = minigpt.train(_nearest_dy(minigpt.build_axs(0, "cuda")), xd, yd, 30,
+                                 capturable=True, fused=fused)
+        graphed, _ = minigpt.train_graphed(_nearest_dy(minigpt.build_axs(0, "cuda")), xd, yd, 30, warmup=3,
+                                           fused=fused)
+        print(f"  losses {eager[0]:.5f} -> {eager[-1]:.5f}", flush=True)
+        assert graphed == eager
 
     print("[minigpt: eager vs graph-replayed, stochastic dY, 100 steps]", flush=True)
     torch.manual_seed(5)
