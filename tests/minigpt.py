@@ -9,7 +9,11 @@ Differences, chosen so that "every nn.Linear" is meaningful and the run is
 deterministic up to the gradient dither:
   * attention uses explicit q/k/v/o nn.Linear layers (nn.MultiheadAttention's
     fused in-projection is not an nn.Linear, and its forward reads
-    out_proj.weight directly, so converting it would quantize nothing);
+    out_proj.weight directly, so converting it would quantize nothing); the
+    q/k/v layers of the one input run as one stacked linear, as
+    nn.MultiheadAttention's in-projection does (fp32: one F.linear over the
+    stacked weights; AXS-6: the library's grouped linear, the input packed
+    once), while the CPU reference restatement runs them one by one;
   * dropout 0 and no weight tying (the head is its own nn.Linear).
 
 Two builds of the same model and initial weights:
@@ -63,11 +67,30 @@ class CausalSelfAttention(nn.Module):
         self.v_proj = nn.Linear(c.embed_dim, c.embed_dim)
         self.out_proj = nn.Linear(c.embed_dim, c.embed_dim)
 
+    def _qkv(self, x: torch.Tensor) -> tuple[torch.Tensor, ...]:
+        """The three projections of the one input as one stacked linear: a
+        plain fp32 F.linear over the stacked weights for nn.Linear layers, the
+        library's grouped quantized linear for AXS-6 ones (the input packed
+        once); the CPU reference restatement runs them one by one, as the
+        reference does.  Every layer keeps its own weight and bias."""
+        ps = (self.q_proj, self.k_proj, self.v_proj)
+        if all(type(p) is nn.Linear for p in ps):
+            y = F.linear(x, torch.cat([p.weight for p in ps]), torch.cat([p.bias for p in ps]))
+            return y.split(x.shape[-1], dim=-1)
+        if all(type(p).__name__ == "AXSLinearUnified" for p in ps) and not any(p._warmup_active for p in ps):
+            from axs.unified import axs_linear_group_unified
+
+            q = ps[0]
+            return axs_linear_group_unified(x, [p.weight for p in ps], [p.bias for p in ps], q.block_size,
+                                            q.quantize_input, q.quantize_grad)
+        return tuple(p(x) for p in ps)
+
     def forward(self, x: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
         B, T, D = x.shape
-        q = self.q_proj(x).reshape(B, T, self.h, self.hd).transpose(1, 2)
-        k = self.k_proj(x).reshape(B, T, self.h, self.hd).transpose(1, 2)
-        v = self.v_proj(x).reshape(B, T, self.h, self.hd).transpose(1, 2)
+        qp, kp, vp = self._qkv(x)
+        q = qp.reshape(B, T, self.h, self.hd).transpose(1, 2)
+        k = kp.reshape(B, T, self.h, self.hd).transpose(1, 2)
+        v = vp.reshape(B, T, self.h, self.hd).transpose(1, 2)
         # fp32 attention; the transposed operand is made contiguous before the
         # batched product
         s = torch.matmul(q, k.transpose(-2, -1).contiguous()) * (self.hd ** -0.5) + mask

@@ -181,6 +181,46 @@ def test_linear_group_matches_separate(bias):
             assert _rel(b.grad, d.double().sum(0)) <= 1e-5
 
 
+@pytest.mark.parametrize("shape", [(300, 256, (256, 128, 96)), (8192, 256, (256, 256, 256))])
+def test_linear_group_backward_is_a_reordering(shape):
+    """The grouped backward against the three separate backwards on the GPU
+    (nearest dY, same operands): the stacked statistics only move each
+    fp16 operand row by a power of two, so the products are the same; what
+    differs is the order of fp32 additions (dX: one accumulator over all
+    stacked outputs instead of three results added afterwards; dW: the
+    split-K plan of the stacked shape).  So the gradients agree to fp32
+    rounding, far inside the linear's 1e-3 against fp64: a change in what
+    is computed (a dropped group, a wrong row scale) fails here."""
+    from axs.unified import axs_linear_group_unified, axs_linear_unified
+
+    M, K, sizes = shape
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(M, K, generator=g).to(DEV)
+    ws = [(torch.randn(n, K, generator=g) * K ** -0.5).to(DEV) for n in sizes]
+    bs = [torch.randn(n, generator=g).to(DEV) for n in sizes]
+    # dY rows of very different scale per group, as q/k/v gradients have
+    dys = [(torch.randn(M, n, generator=g) * 10.0 ** (2 - 2 * i)).to(DEV) for i, n in enumerate(sizes)]
+
+    def grads(grouped):
+        xd = x.clone().requires_grad_(True)
+        wd = [w.clone().requires_grad_(True) for w in ws]
+        bd = [b.clone().requires_grad_(True) for b in bs]
+        if grouped:
+            ys = axs_linear_group_unified(xd, wd, bd, 32, True, False)
+        else:
+            ys = [axs_linear_unified(xd, w, b, 32, True, False) for w, b in zip(wd, bd)]
+        torch.autograd.backward(ys, dys)
+        return xd.grad, [w.grad for w in wd], [b.grad for b in bd]
+
+    gx, gw, gb = grads(True)
+    sx, sw, sb = grads(False)
+    assert _rel(gx, sx.double()) <= 1e-6
+    for a, b in zip(gw, sw):
+        assert _rel(a, b.double()) <= 1e-6
+    for a, b in zip(gb, sb):
+        assert _rel(a, b.double()) <= 1e-6
+
+
 def test_self_attention_groups_projections():
     """Self-attention runs q/k/v as one grouped linear: the output equals the
     one-by-one projections' (forced by a hook on q_proj) bit for bit."""

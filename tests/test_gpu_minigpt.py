@@ -30,11 +30,16 @@ STEPS = 200
 REF_STEPS = 8
 STEP_TOL = 2e-3        # relative, per step, GPU product path vs CPU reference (first REF_STEPS)
 NEAR_STEPS = 10        # nearest dY: steps compared step by step at STEP_TOL (the
-                       # runs then drift: 2.4e-3 relative at step 19, max 0.062 nats at
-                       # step ~50, back to 1e-4 once the batch is memorised)
-NEAR_CURVE_TOL = 0.015  # x initial loss, |a - b| at every step, GPU vs CPU reference, both
-                        # with nearest dY (the same arithmetic up to fp16 product rounding):
-                        # measured max gap 0.0616 nats = 1.10% at step ~50
+                       # runs then drift: 2.4e-3 relative at step 19, the largest gaps at
+                       # steps ~35-60, back to 1e-4 once the batch is memorised)
+NEAR_CURVE_TOL = 0.027  # x initial loss, |a - b| at every step, GPU vs CPU reference, both
+                        # with nearest dY.  The bound is set by how far any change in the
+                        # order of fp32 additions carries this curve, measured: the CPU
+                        # reference restatement itself, run with 2 / 3 / 4 / 6 threads
+                        # instead of the fixture's 8, misses its own fixture by 0.047 /
+                        # 0.069 / 0.053 / 0.090 nats (up to 1.61%); the GPU product path
+                        # 0.062 with q/k/v as three linears, 0.097 and 0.120 (2.15%, two
+                        # boxes) grouped.  The bound is ~1.25x the largest of these.
 CURVE_TOL = 0.025      # x initial loss, |a - b| at every step of two AXS curves with different
                        # dither streams (GPU vs CPU reference, stochastic dY: measured 0.057
                        # = 1.0%; eager vs graph-replayed: 0.099 = 1.8%)
