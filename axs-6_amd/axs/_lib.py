@@ -65,11 +65,15 @@ _SIGNATURES: dict[str, list] = {
                                  _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp, _vp],
     "axs6_nf5_linear_backward_noalloc": [_vp, _i32, _i64, _i64, _i64, _i32, _i32, _u64, _u64, _vp, _vp, _vp,
                                          _vp, _vp, _vp, _vp, _vp, _vp],
+    "axs6_layer_norm_forward": [_vp, _i32, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp],
+    "axs6_layer_norm_backward_workspace": [_i64, _i64],
+    "axs6_layer_norm_backward": [_vp, _vp, _i32, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t,
+                                 _vp],
 }
 # entry points that return a value rather than an axs6_status
 _RESTYPES = {"axs6_linear_padded_k": _i64, "axs6_nf5_linear_backward_workspace": ctypes.c_size_t,
              "axs6_nf5_wire_bytes": _i64, "axs6_nf5_block_bytes": _i64, "axs6_multi_tensor_workspace": _i64,
-             "axs6_nf5_row_stats_workspace": _i64}
+             "axs6_nf5_row_stats_workspace": _i64, "axs6_layer_norm_backward_workspace": _i64}
 
 
 class LibraryError(RuntimeError):

@@ -26,8 +26,12 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from axs import _lib
 from axs.core import DEFAULT_BLOCK_SIZE
 from axs.unified.functional_unified import axs_linear_group_unified, axs_linear_unified, fake_quantize_unified
+
+# input dtypes whose LayerNorm runs on the HIP kernels
+_LN_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 
 class AXSLinearUnified(nn.Module):
@@ -79,7 +83,13 @@ AXS6Linear = AXSLinearUnified
 
 
 class AXSLayerNormUnified(nn.Module):
-    """LayerNorm without output quantization (the next linear quantizes its input)."""
+    """LayerNorm without output quantization (the next linear quantizes its
+    input), ``modules_unified.py:120-144``.  On the GPU, for float32, bfloat16
+    or float16 input with parameters of the same dtype, forward and backward
+    run on this library's HIP kernels (one autograd node; the statistics and
+    the parameter gradients in float32, reduced in a fixed order); CPU tensors
+    and other dtype combinations take ``F.layer_norm``, as the reference does
+    everywhere."""
 
     def __init__(self, normalized_shape: int | list[int], eps: float = 1e-5) -> None:
         super().__init__()
@@ -91,6 +101,9 @@ class AXSLayerNormUnified(nn.Module):
         self.bias = nn.Parameter(torch.zeros(self.normalized_shape))
 
     def forward(self, input: torch.Tensor) -> torch.Tensor:
+        if (input.is_cuda and input.dtype in _LN_DTYPES and self.weight.dtype == input.dtype
+                and self.bias.dtype == input.dtype):
+            return _lib.ext().layer_norm(input, self.weight, self.bias, len(self.normalized_shape), self.eps)
         return F.layer_norm(input, self.normalized_shape, self.weight, self.bias, self.eps)
 
 

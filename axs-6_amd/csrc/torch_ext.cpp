@@ -402,6 +402,90 @@ py::tuple linear_fwd(const at::Tensor& input, const at::Tensor& weight, const st
     return py::make_tuple(r.out, r.xq, r.sx, r.wq, r.sw, r.M, r.N, r.K, r.n_true, r.k_true, r.dtype);
 }
 
+// ---- LayerNorm (AXSLayerNormUnified) ---------------------------------------------
+
+// F.layer_norm over the last `ndim` dims (modules_unified.py:141-144) as one
+// autograd node over axs6_layer_norm_forward / _backward: float32, bfloat16
+// or float16 input with weight and bias of the same dtype (or absent).
+struct LayerNormFunction : public torch::autograd::Function<LayerNormFunction> {
+    static at::Tensor forward(AutogradContext* ctx, const at::Tensor& input, const at::Tensor& weight,
+                              const at::Tensor& bias, int64_t ndim, double eps, bool has_weight, bool has_bias) {
+        const char* fn = "axs6_layer_norm_forward";
+        require_device(input, fn);
+        const int dt = dtype_code(input.scalar_type());
+        TORCH_CHECK(dt >= 0, "layer_norm: input dtype ", input.scalar_type(), " is not float32, bfloat16 or float16");
+        TORCH_CHECK(ndim >= 1 && ndim <= input.dim(), "layer_norm: normalized_shape of ", ndim,
+                    " dims for an input of ", input.dim());
+        int64_t cols = 1;
+        for (int64_t d = input.dim() - ndim; d < input.dim(); ++d) cols *= input.size(d);
+        const int64_t rows = cols ? input.numel() / cols : 0;
+        for (const at::Tensor* p : {&weight, &bias}) {
+            if ((p == &weight && !has_weight) || (p == &bias && !has_bias)) continue;
+            TORCH_CHECK(p->device() == input.device() && p->scalar_type() == input.scalar_type() &&
+                            p->numel() == cols,
+                        "layer_norm: weight and bias must be ", cols, " values of the input's dtype and device");
+        }
+        c10::DeviceGuard guard(input.device());
+        at::Tensor x = input.contiguous();
+        at::Tensor w = has_weight ? weight.contiguous() : at::Tensor();
+        at::Tensor b = has_bias ? bias.contiguous() : at::Tensor();
+        at::Tensor y = at::empty_like(x);
+        at::Tensor mean = at::empty({rows}, x.options().dtype(at::kFloat));
+        at::Tensor rstd = at::empty({rows}, x.options().dtype(at::kFloat));
+        check_rc(axs6_layer_norm_forward(x.data_ptr(), dt, rows, cols, has_weight ? w.data_ptr() : nullptr,
+                                         has_bias ? b.data_ptr() : nullptr, (float)eps, y.data_ptr(),
+                                         mean.data_ptr<float>(), rstd.data_ptr<float>(), stream_of(x)),
+                 fn);
+        ctx->save_for_backward({x, has_weight ? w : at::Tensor(), mean, rstd});
+        auto& d = ctx->saved_data;
+        d["rows"] = rows; d["cols"] = cols; d["has_weight"] = has_weight; d["has_bias"] = has_bias;
+        d["nshape"] = input.sizes().slice(input.dim() - ndim).vec();
+        return y;
+    }
+
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        const char* fn = "axs6_layer_norm_backward";
+        variable_list none(7);
+        if (!grads[0].defined()) return none;
+        const auto saved = ctx->get_saved_variables();
+        const at::Tensor& x = saved[0];
+        auto& d = ctx->saved_data;
+        const int64_t rows = d["rows"].toInt(), cols = d["cols"].toInt();
+        const bool has_w = d["has_weight"].toBool(), has_b = d["has_bias"].toBool();
+        const bool need_w = has_w && ctx->needs_input_grad(1), need_b = has_b && ctx->needs_input_grad(2);
+        c10::DeviceGuard guard(x.device());
+        at::Tensor dy = grads[0].to(x.scalar_type()).contiguous();
+        at::Tensor dx = at::empty_like(x);
+        const auto f32 = x.options().dtype(at::kFloat);
+        at::Tensor dw = need_w ? at::empty({cols}, f32) : at::Tensor();
+        at::Tensor db = need_b ? at::empty({cols}, f32) : at::Tensor();
+        const int64_t ws = axs6_layer_norm_backward_workspace(rows, cols);
+        TORCH_CHECK(ws >= 0, fn, ": bad shape");
+        at::Tensor work = at::empty({ws > 0 ? ws : 1}, x.options().dtype(at::kByte));
+        check_rc(axs6_layer_norm_backward(dy.data_ptr(), x.data_ptr(), dtype_code(x.scalar_type()), rows, cols,
+                                          saved[2].data_ptr<float>(), saved[3].data_ptr<float>(),
+                                          has_w ? saved[1].data_ptr() : nullptr, dx.data_ptr(),
+                                          need_w ? dw.data_ptr<float>() : nullptr,
+                                          need_b ? db.data_ptr<float>() : nullptr, work.data_ptr(), (size_t)ws,
+                                          stream_of(x)),
+                 fn);
+        variable_list out(7);
+        out[0] = dx;
+        const auto nshape = d["nshape"].toIntVector();
+        if (need_w) out[1] = dw.to(x.scalar_type()).view(nshape);
+        if (need_b) out[2] = db.to(x.scalar_type()).view(nshape);
+        return out;
+    }
+};
+
+at::Tensor layer_norm(const at::Tensor& input, const std::optional<at::Tensor>& weight,
+                      const std::optional<at::Tensor>& bias, int64_t ndim, double eps) {
+    // absent parameters travel as empty tensors (see linear())
+    const bool hw = weight && weight->defined(), hb = bias && bias->defined();
+    const at::Tensor empty = at::empty({0}, input.options());
+    return LayerNormFunction::apply(input, hw ? *weight : empty, hb ? *bias : empty, ndim, eps, hw, hb);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -410,6 +494,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("stochastic"), py::arg("seed") = py::none());
     m.def("fq_ste", &fq_ste, "NF5 fake-quantize with the straight-through gradient (autograd node)",
           py::arg("tensor"), py::arg("block_size"), py::arg("stochastic"));
+    m.def("layer_norm", &layer_norm,
+          "F.layer_norm over the last `ndim` dims on the HIP kernels (autograd node)", py::arg("input"),
+          py::arg("weight"), py::arg("bias"), py::arg("ndim"), py::arg("eps"));
     m.def("linear", &linear, "FQ(input) FQ(weight)^T + bias with the quantized backward (autograd node)",
           py::arg("input"), py::arg("weight"), py::arg("bias"), py::arg("block_size"), py::arg("quantize_input"),
           py::arg("quantize_grad"));

@@ -303,6 +303,26 @@ int axs6_multi_tensor_unscale_clip(void* const* grads, const int64_t* numel, con
                                    float loss_scale, float max_norm, int32_t clip, float* partials,
                                    int64_t partials_len, float* result, void* stream);
 
+/* ---- LayerNorm -------------------------------------------------------------
+ * F.layer_norm of AXSLayerNormUnified.forward (axs/unified/modules_unified.py:
+ * 141-144) and its autograd backward, over rows of `cols` contiguous values
+ * (the normalized dims flattened); x, y, dy, dx, gamma, beta of `dtype`,
+ * statistics and parameter gradients in float32:
+ *   mean = sum x / cols, var = sum (x - mean)^2 / cols, rstd = 1 / sqrt(var + eps),
+ *   y = (x - mean) * rstd * gamma + beta                 (gamma, beta NULL: 1, 0);
+ *   dx = rstd * (g - (sum g + xhat * sum g * xhat) / cols), g = dy * gamma,
+ *   dgamma = sum over rows of dy * xhat, dbeta = sum over rows of dy.
+ * mean and rstd (rows floats each) are written by the forward when not NULL
+ * and read by the backward; dgamma / dbeta may be NULL.  The backward needs
+ * axs6_layer_norm_backward_workspace(rows, cols) bytes of device workspace.
+ * Deterministic (fixed reduction orders), asynchronous, no allocation. */
+int axs6_layer_norm_forward(const void* x, int32_t dtype, int64_t rows, int64_t cols, const void* gamma,
+                            const void* beta, float eps, void* y, float* mean, float* rstd, void* stream);
+int64_t axs6_layer_norm_backward_workspace(int64_t rows, int64_t cols);
+int axs6_layer_norm_backward(const void* dy, const void* x, int32_t dtype, int64_t rows, int64_t cols,
+                             const float* mean, const float* rstd, const void* gamma, void* dx, float* dgamma,
+                             float* dbeta, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
