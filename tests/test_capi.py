@@ -102,6 +102,29 @@ def test_invalid_arguments_rejected_without_device():
     assert rc == 1
 
 
+def test_layer_norm_arguments_rejected_without_device():
+    rc, msg = _status("axs6_layer_norm_forward", 16, 7, 4, 8, None, None, 1e-5, 16, None, None, None)
+    assert rc == 1 and "dtype" in msg
+    rc, msg = _status("axs6_layer_norm_forward", 16, 0, -1, 8, None, None, 1e-5, 16, None, None, None)
+    assert rc == 1 and "negative" in msg
+    rc, msg = _status("axs6_layer_norm_forward", None, 0, 4, 8, None, None, 1e-5, None, None, None, None)
+    assert rc == 1 and "null" in msg
+    rc, msg = _status("axs6_layer_norm_forward", 16, 0, 4, 8, None, None, -1.0, 16, None, None, None)
+    assert rc == 1 and "eps" in msg
+    # element-misaligned pointers (2 bytes into a float32 buffer)
+    rc, msg = _status("axs6_layer_norm_forward", 18, 0, 4, 8, None, None, 1e-5, 16, None, None, None)
+    assert rc == 1 and "aligned" in msg
+    # empty rows or columns: nothing to do
+    assert _status("axs6_layer_norm_forward", None, 0, 0, 8, None, None, 1e-5, None, None, None, None)[0] == 0
+    ws = _lib.lib().axs6_layer_norm_backward_workspace(1000, 256)
+    assert ws == 63 * 2 * 256 * 4   # one partial row pair per 16 rows
+    assert _lib.lib().axs6_layer_norm_backward_workspace(-1, 4) == -1
+    rc, msg = _status("axs6_layer_norm_backward", 16, 16, 0, 1000, 256, 16, 16, None, 16, 16, 16, 16, ws - 4, None)
+    assert rc == 1 and "workspace" in msg
+    rc, msg = _status("axs6_layer_norm_backward", None, 16, 0, 1000, 256, 16, 16, None, 16, 16, 16, 16, ws, None)
+    assert rc == 1 and "null" in msg
+
+
 def test_error_raises_runtime_error():
     with pytest.raises(RuntimeError, match="block_size"):
         _lib.call("axs6_nf5_fake_quantize", 1, 1, 0, 4, 32, 17, 0, 0, 0, None, None)
