@@ -320,6 +320,11 @@ constexpr int kTileLd = kTile + 8; // LDS row stride (halves) of the transposed 
 
 // C32: every dither counter offset .. offset + rows*cols - 1 has the same high
 // word (the common case), so the draw needs only the 32-bit low word.
+// One 64 x 64 tile per workgroup (tile blockIdx.x, column tiles fastest): its
+// loads -- the tile of x, the column exponents and the rows' shifts -- go out
+// first, so their latency overlaps the staging of the tables and the fold of
+// the tensor-wide maximum.  Tiles wholly inside x (all but the last row band
+// and column tile) skip the bounds tests; both forms compute the same values.
 template <int DT, int MODE, int BS, bool C32>
 __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t ntx, int64_t ntiles) {
     using E = Elem<DT>;
@@ -337,7 +342,50 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
 
     const int tid = threadIdx.x;
     const int tc = tid % TPR, tr = tid / TPR;
-    const S* xs = reinterpret_cast<const S*>(k.x);
+    const int64_t t = blockIdx.x;
+    if (t >= ntiles) return;   // workgroup-uniform (the grid is the tile count)
+    const int64_t ty = t / ntx, tx = t - ty * ntx;
+    const bool full = (ty + 1) * kTile <= k.rows && (tx + 1) * kTile <= k.cols;   // workgroup-uniform
+    const int64_t c0 = tx * kTile, r0 = ty * kTile;
+    const int64_t c = c0 + tc * V;
+    const bool cin = full || c < k.cols;            // cols % V == 0: vectors are whole
+    const int64_t rt = r0 + tr;                     // this thread's row in pass 0
+    const S* xp = reinterpret_cast<const S*>(k.x) + rt * k.cols + c;
+    const int64_t x_pass = (int64_t)RPP * k.cols;
+
+    // ---- the tile's loads ----
+    u32x4 raw[PASSES];
+    if (full) {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) raw[p] = *reinterpret_cast<const u32x4*>(xp + p * x_pass);
+    } else {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int64_t r = rt + RPP * p;
+            raw[p] = (cin && r < k.rows) ? *reinterpret_cast<const u32x4*>(xp + p * x_pass) : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    // the column exponents of this thread's V columns, the rows' shifts and exponents
+    int cx[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) cx[e] = 0;
+    if (k.out_r && cin && k.colx_r) {
+#pragma unroll
+        for (int h = 0; h < V / 4; ++h) {
+            const u32x4 c4 = *(reinterpret_cast<const u32x4*>(k.colx_r + c) + h);
+            cx[4 * h] = (int)c4.x; cx[4 * h + 1] = (int)c4.y; cx[4 * h + 2] = (int)c4.z; cx[4 * h + 3] = (int)c4.w;
+        }
+    }
+    int shr[PASSES], rxv[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int64_t r = rt + RPP * p;
+        const bool rin = full || r < k.rows;
+        shr[p] = (k.out_r && rin) ? k.shift_r[r] : 0;
+        rxv[p] = (k.rowx && cin && rin) ? k.rowx[r] : INT_MIN;
+    }
+
+    // ---- tables and the tensor-wide maximum ----
     const uint64_t key = MODE == kStochastic ? dither_key(k.seed + (k.seed_dev ? *k.seed_dev : 0ull)) : 0ull;
     int gm = INT_MIN;
     if (k.gtile) {
@@ -354,47 +402,14 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
         if (k.gmax) gm = *k.gmax;
     }
     const int G = (gm == INT_MIN) ? 0 : gm - kF16MaxExp;
+    int shx[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) shx[p] = rxv[p] == INT_MIN ? -G : rxv[p] - G;
 
-    // persistent over tiles; consecutive workgroups take neighbouring column
-    // tiles of one 64-row band, so a band of x streams through once.  Tiles
-    // wholly inside x (all but the last row band and column tile) run a copy
-    // of the body without bounds tests; both copies compute the same values.
+    // ---- FQ and the two operands ----
     const uint32_t kh = (uint32_t)key ^ ((uint32_t)(k.offset >> 32) * 0x9E3779B9u + (uint32_t)(key >> 32));
-    auto tile_body = [&](auto full_tag, int64_t ty, int64_t tx) {
+    auto tile_body = [&](auto full_tag) {
         constexpr bool FULL = decltype(full_tag)::value;
-        const int64_t c0 = tx * kTile, r0 = ty * kTile;
-        const int64_t c = c0 + tc * V;
-        const bool cin = FULL || c < k.cols;        // cols % V == 0: vectors are whole
-        const int64_t rt = r0 + tr;                 // this thread's row in pass 0
-        const S* xp = xs + rt * k.cols + c;
-        const int64_t x_pass = (int64_t)RPP * k.cols;
-
-        u32x4 raw[PASSES];
-#pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-            const int64_t r = rt + RPP * p;
-            raw[p] = (FULL || (cin && r < k.rows)) ? *reinterpret_cast<const u32x4*>(xp + p * x_pass)
-                                                   : u32x4{0u, 0u, 0u, 0u};
-        }
-        // per-tile operands of the two outputs, loaded once: the column
-        // exponents of this thread's V columns, the rows' shifts and exponents
-        int cx[V];
-#pragma unroll
-        for (int e = 0; e < V; ++e) cx[e] = 0;
-        if (k.out_r && cin && k.colx_r) {
-#pragma unroll
-            for (int h = 0; h < V / 4; ++h) {
-                const u32x4 c4 = *(reinterpret_cast<const u32x4*>(k.colx_r + c) + h);
-                cx[4 * h] = (int)c4.x; cx[4 * h + 1] = (int)c4.y; cx[4 * h + 2] = (int)c4.z; cx[4 * h + 3] = (int)c4.w;
-            }
-        }
-        int shr[PASSES], shx[PASSES];
-#pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-            const int64_t r = rt + RPP * p;
-            shr[p] = (k.out_r && (FULL || r < k.rows)) ? k.shift_r[r] : 0;
-            shx[p] = (k.rowx && cin && (FULL || r < k.rows)) ? k.rowx[r] - G : -G;
-        }
         // dither counters offset + r * cols + c (low words: pass p adds p * RPP * cols)
         const uint32_t lo0 = (uint32_t)k.offset + (uint32_t)rt * (uint32_t)k.cols + (uint32_t)c;
         const uint32_t lo_pass = (uint32_t)RPP * (uint32_t)k.cols;
@@ -461,9 +476,9 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
         }
         __syncthreads();
         if (k.partial && tid < kTile && (FULL || c0 + tid < k.cols)) {
-            float s = 0.0f;
-            for (int q = 0; q < RPP; ++q) s += csum[q][tid];
-            k.partial[ty * k.cols + c0 + tid] = s;
+            float sum = 0.0f;
+            for (int q = 0; q < RPP; ++q) sum += csum[q][tid];
+            k.partial[ty * k.cols + c0 + tid] = sum;
         }
         if (k.out) {
             // 64 output rows (columns c of x) of 64 halves = 8 chunks of 16 bytes each
@@ -475,13 +490,9 @@ __global__ __launch_bounds__(kPackThreads) void pack_t_kernel(PackTK k, int64_t 
                         *reinterpret_cast<const u32x4*>(&tile[oc * kTileLd + j * 8]);
             }
         }
-        __syncthreads();   // tile and csum are rewritten by the next tile
     };
-    for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
-        const int64_t ty = t / ntx, tx = t - ty * ntx;
-        if ((ty + 1) * kTile <= k.rows && (tx + 1) * kTile <= k.cols) tile_body(std::true_type{}, ty, tx);
-        else tile_body(std::false_type{}, ty, tx);
-    }
+    if (full) tile_body(std::true_type{});
+    else tile_body(std::false_type{});
 }
 
 // Rows longer than pack_rows_kernel holds in registers take two launches: this
@@ -967,8 +978,9 @@ void dispatch_rows(const PackRowsK& k, const PackRowsK& k2, int64_t rows, int mo
 
 template <int DT, int BS>
 void dispatch_t_bs(const PackTK& k, int mode, int64_t ntx, int64_t ntiles, hipStream_t st) {
-    // one tile per workgroup: independent workgroups overlap their load,
-    // compute and store phases better than a persistent loop (measured)
+    // one tile per workgroup (the kernel takes tile blockIdx.x): independent
+    // workgroups overlap their load, compute and store phases better than a
+    // persistent loop (measured)
     const dim3 grid((unsigned)ntiles);
     // one high word for every counter of the call: the 32-bit dither path
     const bool c32 = (k.offset >> 32) == ((k.offset + (uint64_t)(k.rows * k.cols) - 1) >> 32);
