@@ -511,12 +511,13 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
     batch 64) with every nn.Linear converted to the AXS-6 linear, AdamW lr 3e-4,
     fp32 master weights, one fixed synthetic batch (tests/minigpt.py).  A step
     is forward + cross-entropy + backward + AdamW through the Python API.
-    Reported: ms/step over the steps after `warmup`, the loss curve at a few
+    Reported: ms/step over the steps after `warmup` (torch's fused AdamW;
+    multi_tensor_adamw_ms_per_step with its default multi-tensor form, whose
+    extra launches dominate a host-bound eager step), the loss curve at a few
     points, the same with the step recorded in a HIP graph and replayed
-    (graph_ms_per_step, with torch's fused AdamW; graph_multi_tensor_adamw_*
-    with its capturable multi-tensor form, which adds two per-parameter
-    broadcast divisions per step), the same for the unquantized fp32 model,
-    and the CPU
+    (graph_ms_per_step, fused AdamW; graph_multi_tensor_adamw_* with the
+    capturable multi-tensor form, which adds two per-parameter broadcast
+    divisions per step), the same for the unquantized fp32 model, and the CPU
     reference restatement's ms/step over `ref_steps` steps (host cores)."""
     import torch
 
@@ -531,14 +532,21 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
     torch.cuda.synchronize()
     torch.manual_seed(5)
     model = minigpt.build_axs(0, "cuda")
-    losses, ms = minigpt.train(model, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize)
+    losses, ms = minigpt.train(model, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize,
+                               capturable=True, fused=True)
+    torch.manual_seed(5)
+    _, mt_ms = minigpt.train(minigpt.build_axs(0, "cuda"), x.cuda(), y.cuda(), steps, warmup=warmup,
+                             sync=torch.cuda.synchronize)
     torch.manual_seed(5)
     g_losses, g_ms = minigpt.train_graphed(minigpt.build_axs(0, "cuda"), x.cuda(), y.cuda(), steps, warmup=3,
                                            fused=True)
     torch.manual_seed(5)
     _, gm_ms = minigpt.train_graphed(minigpt.build_axs(0, "cuda"), x.cuda(), y.cuda(), steps, warmup=3)
     fp32 = minigpt.base_model(0).cuda()
-    fp_losses, fp_ms = minigpt.train(fp32, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize)
+    fp_losses, fp_ms = minigpt.train(fp32, x.cuda(), y.cuda(), steps, warmup=warmup, sync=torch.cuda.synchronize,
+                                     capturable=True, fused=True)
+    _, fpm_ms = minigpt.train(minigpt.base_model(0).cuda(), x.cuda(), y.cuda(), steps, warmup=warmup,
+                              sync=torch.cuda.synchronize)
     fg_losses, fg_ms = minigpt.train_graphed(minigpt.base_model(0).cuda(), x.cuda(), y.cuda(), steps, warmup=3,
                                              fused=True)
     _, fgm_ms = minigpt.train_graphed(minigpt.base_model(0).cuda(), x.cuda(), y.cuda(), steps, warmup=3)
@@ -547,12 +555,15 @@ def bench_minigpt(steps: int = 200, warmup: int = 5, ref_steps: int = 3):
     out = {
         "metric": "MiniGPT AXS-6 training ms/step (config 5)",
         "ms_per_step": round(ms, 3), "steps": steps, "warmup": warmup,
+        "optimizer": "AdamW(fused=True) in every leg; *_multi_tensor_adamw_* with torch's default form",
+        "multi_tensor_adamw_ms_per_step": round(mt_ms, 3),
         "loss": {str(i): round(losses[i], 4) for i in pts},
         "graph_ms_per_step": round(g_ms, 3),
         "graph_loss": {str(i): round(g_losses[i], 4) for i in pts},
         "graph_optimizer": "AdamW(fused=True)",
         "graph_multi_tensor_adamw_ms_per_step": round(gm_ms, 3),
-        "fp32_model": {"ms_per_step": round(fp_ms, 3), "graph_ms_per_step": round(fg_ms, 3),
+        "fp32_model": {"ms_per_step": round(fp_ms, 3), "multi_tensor_adamw_ms_per_step": round(fpm_ms, 3),
+                       "graph_ms_per_step": round(fg_ms, 3),
                        "graph_multi_tensor_adamw_ms_per_step": round(fgm_ms, 3),
                        "loss": {str(i): round(fp_losses[i], 4) for i in pts}},
         "pipeline": pipe,
