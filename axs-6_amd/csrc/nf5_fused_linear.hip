@@ -29,7 +29,10 @@
 //     workgroup first quantizes its rows of X once into LDS -- every
 //     workgroup needs all of X, and quantizing it per K tile with the 16-row
 //     block of the MFMA spent as much VALU on X (mostly rows past M) as on W
-//     -- and the K loop then reads FQ(X) from LDS and quantizes only W.
+//     -- and the K loop then reads FQ(X) from LDS and quantizes only W;
+//   * at one or two rows of X whose FQ fits 48 KiB of LDS, the streamed
+//     decode form (fused_decode_kernel) replaces it: a wave per weight row,
+//     VALU products, whole-row loads.
 // Unlike the packed fp16 path there is no row shift and no rounding of the
 // operands: the products are those of fp32 FQ values, as in the reference's
 // fused kernel.  For 16-bit inputs the FQ values stay fp32 too, as in the
@@ -297,6 +300,280 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
     }
 }
 
+// ---- streamed decode form (M <= 2) ----------------------------------------
+//
+// One weight row per wave (K split over KS waves when the weight is short or
+// very tall), streamed in steps of 512 values with two steps prefetched in a
+// register ring; FQ(X) once per workgroup in LDS.  Lane l takes the 8
+// consecutive values 8l .. 8l+7 of a step, so an NF5 block is a DPP quad and
+// a wave's loads cover 2 KiB (f32) of one row: the whole-row read pattern the
+// MFMA form's 16-row fragments cannot have (it streams the weight ~25% slower).
+// The contraction is VALU FMAs against FQ(X) from LDS: at M <= 2 a 16-row
+// MFMA block would be 7/8 or more padding, and the FQ, not the products, is
+// the VALU work.  Per block the quantized magnitudes are taken unscaled
+// (+-lut, exact zeros masked) and the block's 2^e1 is applied once to the
+// lane's partial sum: (lut 2^e1) x = (lut x) 2^e1 exactly for the normal
+// blocks this covers; other blocks (NaN, inf, tiny, overflowing scale) take
+// the full FQ values with e1 = 0.
+constexpr int kDecStep = 512;               // values of a row per wave step (8 per lane)
+constexpr int kDecWaves = 8;                // waves per workgroup
+constexpr int kDecPf = 2;                   // steps prefetched ahead
+constexpr int kDecXBytes = 48 * 1024;       // LDS for FQ(X): three workgroups per CU
+
+template <int DT> constexpr int dec_loads() { return Elem<DT>::V == 4 ? 2 : 1; }
+
+// The 8 values of one lane at p (16-byte aligned).
+template <int DT>
+__device__ __forceinline__ void dec_load(const typename Elem<DT>::S* p, u32x4 (&v)[dec_loads<DT>()]) {
+    v[0] = *reinterpret_cast<const u32x4*>(p);
+    if constexpr (dec_loads<DT>() == 2) v[1] = *reinterpret_cast<const u32x4*>(p + 4);
+}
+
+// The same from a weight row through a buffer resource of `bytes` bytes from
+// `base`: lanes past the row's end read zeros (the buffer's range check), so
+// a step past K needs neither a clamp nor a mask.
+template <int DT>
+__device__ __forceinline__ void dec_load_row(const char* base, int bytes, int voff, u32x4 (&v)[dec_loads<DT>()]) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, bytes, 0x00020000);
+    v[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+    if constexpr (dec_loads<DT>() == 2)
+        v[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, 0, 0));
+}
+
+template <int DT>
+__device__ __forceinline__ void dec_unpack(const u32x4 (&v)[dec_loads<DT>()], float (&f)[8]) {
+    using E = Elem<DT>;
+    if constexpr (E::V == 4) {
+        float a[4], b[4];
+        E::unpack(v[0], a);
+        E::unpack(v[1], b);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { f[e] = a[e]; f[4 + e] = b[e]; }
+    } else {
+        E::unpack(v[0], f);
+    }
+}
+
+__device__ __forceinline__ float dec_wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+template <int DT, int MR, int KS, bool QX>
+__global__ __launch_bounds__(kDecWaves * 64) void fused_decode_kernel(FusedK k) {
+    using E = Elem<DT>;
+    using S = typename E::S;
+    constexpr int L = dec_loads<DT>();
+    constexpr int NB = kDecPf + 1;
+    constexpr int ES = sizeof(S);
+    static_assert(kDecWaves % KS == 0, "waves per row");
+    __shared__ float lut_s[kLutSize];
+    __shared__ uint32_t band_w[kBandSize / 4];
+    __shared__ float part_s[kDecWaves * MR];
+    extern __shared__ __align__(16) float xq_s[];   // FQ(X) in the lanes' read order
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int SP = (k.K + kDecStep - 1) / kDecStep;       // steps per row
+    const int ks = wave % KS;
+    const int j0 = ks * SP / KS;
+    const int SW = (ks + 1) * SP / KS - j0;               // this wave's steps (>= 1: SP >= KS)
+    const int nw = (int)blockIdx.x * (kDecWaves / KS) + wave / KS;
+    const bool live = nw < k.N;
+    const int n = live ? nw : k.N - 1;                    // rows past N stream row N-1, unstored
+    const char* wrow = reinterpret_cast<const char*>(k.w) + (int64_t)n * k.K * ES;
+    const int voff = lane * 8 * ES;
+
+    // The tables and this thread's first chunk of X are loaded first, then
+    // the weight prefetch, and only then is FQ(X) computed: loads queued
+    // behind the weight's would delay the prologue by their latency.
+    float4 lutv = make_float4(0.f, 0.f, 0.f, 0.f);
+    uint32_t bandv = 0;
+    if (tid < kLutSize / 4) lutv = reinterpret_cast<const float4*>(k.lut)[tid];
+    if (tid < kBandSize / 4) bandv = reinterpret_cast<const uint32_t*>(k.band)[tid];
+    // X chunk c: row m, step j, lane slot l -> x[m, 512 j + 8 l .. + 7],
+    // stored as float4 ((m SP + j) 2 + h) 64 + l (h: first / second four)
+    const S* xs = reinterpret_cast<const S*>(k.x);
+    const int nchunk = MR * SP * 64;
+    auto x_load = [&](int c, u32x4 (&v)[L], bool& valid) {
+        const int m = c / (SP * 64), j = (c / 64) % SP, l = c % 64;
+        const int o = j * kDecStep + 8 * l;
+        valid = c < nchunk && m < k.M && o < k.K;
+        dec_load<DT>(xs + (valid ? (int64_t)m * k.K + o : 0), v);
+    };
+    u32x4 xv[L];
+    bool xvalid;
+    x_load(tid, xv, xvalid);
+
+    u32x4 buf[NB][L];
+    int pf = 0;                                           // steps prefetched so far
+    auto prefetch = [&](u32x4 (&b)[L]) {
+        const int j = j0 + (pf < SW ? pf : SW - 1);       // past the range: reload the last step
+        const int done = j * kDecStep;
+        dec_load_row<DT>(wrow + (int64_t)done * ES, (k.K - done) * ES, voff, b);
+        ++pf;
+    };
+#pragma unroll
+    for (int u = 0; u < kDecPf; ++u) prefetch(buf[u]);
+
+    if (tid < kLutSize / 4) reinterpret_cast<float4*>(lut_s)[tid] = lutv;
+    if (tid < kBandSize / 4) band_w[tid] = bandv;
+    __syncthreads();
+    auto x_stage = [&](int c, const u32x4 (&v)[L], bool valid) {
+        float f[8];
+        dec_unpack<DT>(v, f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = valid ? f[e] : 0.0f;
+        if constexpr (QX) {
+            uint32_t mx = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t a = __float_as_uint(f[e]) & 0x7fffffffu;
+                mx = mx > a ? mx : a;
+            }
+            mx = group_umax<4>(mx);
+            const FqScale s = fq_scale(mx, band_s);
+            const float d[8] = {};
+            fq_vector<8>(f, s, lut_s, false, d);
+        }
+        if (c < nchunk) {
+            const int m = c / (SP * 64), j = (c / 64) % SP, l = c % 64;
+            float4* dst = reinterpret_cast<float4*>(xq_s) + ((m * SP + j) * 2) * 64 + l;
+            dst[0] = make_float4(f[0], f[1], f[2], f[3]);
+            dst[64] = make_float4(f[4], f[5], f[6], f[7]);
+        }
+    };
+    x_stage(tid, xv, xvalid);
+    for (int c = tid + kDecWaves * 64; c < nchunk; c += kDecWaves * 64) {
+        x_load(c, xv, xvalid);
+        x_stage(c, xv, xvalid);
+    }
+    __syncthreads();
+
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
+    auto step = [&](const u32x4 (&wv)[L], int j) {
+        float f[8];
+        dec_unpack<DT>(wv, f);
+        // block maximum and minimum of |w| (v_maximum3 / v_minimum3 with |.|
+        // modifiers; the maximum propagates NaN, whose bits exceed inf's)
+        float amx = __builtin_elementwise_maximum(__builtin_fabsf(f[0]), __builtin_fabsf(f[1]));
+        float amn = __builtin_elementwise_minimum(__builtin_fabsf(f[0]), __builtin_fabsf(f[1]));
+#pragma unroll
+        for (int e = 2; e < 8; ++e) {
+            amx = __builtin_elementwise_maximum(amx, __builtin_fabsf(f[e]));
+            amn = __builtin_elementwise_minimum(amn, __builtin_fabsf(f[e]));
+        }
+        const uint32_t mx = group_umax<4>(__float_as_uint(amx));
+        // fq_scale's short form, its general form when any lane needs it
+        const int fexp = (int)(mx >> 23) - kExpBias;
+        const uint32_t kb = (mx & 0x7f800000u) + 0x00800000u;
+        int e1 = (kb - mx <= (uint32_t)band_s[fexp + 150]) ? fexp + 2 : fexp + 1;
+        const bool wide = mx != 0u && (mx < kFastMinAmaxBits || e1 >= 128);
+        if (__builtin_amdgcn_ballot_w64(wide) != 0) {
+            const FqScale s = fq_scale_general(mx, band_s);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = fq_value(f[e], s, lut_s, false, 0.0f);
+            e1 = 0;
+        } else {
+            // fq_vector's short sequence without the final 2^e1 (lut_pos: the
+            // index of |w| 1023 2^-e1)
+            e1 = mx == 0u ? 0 : e1;
+            const float c = __builtin_amdgcn_ldexpf(1023.0f, -e1);
+            float g[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float mag = lut_s[(int)(__builtin_fabsf(f[e]) * c)];
+                g[e] = __uint_as_float(__float_as_uint(mag) ^ (__float_as_uint(f[e]) & 0x80000000u));
+            }
+            // FQ(+-0) = +0 (lut[0] is not 0): masked only where a zero occurs
+            if (__builtin_amdgcn_ballot_w64(__float_as_uint(amn) == 0u) != 0) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) g[e] = f[e] != 0.0f ? g[e] : 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = g[e];
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const float4* xp = reinterpret_cast<const float4*>(xq_s) + ((m * SP + j) * 2) * 64 + lane;
+            const float4 xa = xp[0], xb = xp[64];
+            float p0 = f[0] * xa.x, p1 = f[1] * xa.y;
+            p0 = __builtin_fmaf(f[2], xa.z, p0);
+            p1 = __builtin_fmaf(f[3], xa.w, p1);
+            p0 = __builtin_fmaf(f[4], xb.x, p0);
+            p1 = __builtin_fmaf(f[5], xb.y, p1);
+            p0 = __builtin_fmaf(f[6], xb.z, p0);
+            p1 = __builtin_fmaf(f[7], xb.w, p1);
+            acc[m] += __builtin_amdgcn_ldexpf(p0 + p1, e1);
+        }
+    };
+    // NB steps per iteration so the ring's slots are compile-time; every
+    // prefetch is unconditional (a load under a branch would make the
+    // compiler wait for all outstanding loads, the ring's included).
+    for (int s0 = 0; s0 < SW; s0 += NB) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            prefetch(buf[(u + kDecPf) % NB]);
+            if (s0 + u < SW) step(buf[u], j0 + s0 + u);
+        }
+    }
+
+    float t[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) t[m] = dec_wave_sum(acc[m]);
+    if constexpr (KS > 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) part_s[wave * MR + m] = t[m];
+        }
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                float v = part_s[wave * MR + m];
+#pragma unroll
+                for (int q = 1; q < KS; ++q) v += part_s[(wave + q) * MR + m];   // fixed order
+                t[m] = v;
+            }
+        }
+    }
+    if (ks == 0 && lane == 0 && live) {
+        const float bn = k.bias ? k.bias[n] : 0.0f;
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+            if (m < k.M) reinterpret_cast<S*>(k.y)[(int64_t)m * k.N + n] = E::from_f(t[m] + bn);
+    }
+}
+
+// The streamed decode form applies for M <= 2 when FQ(X) fits kDecXBytes.
+bool decode_form_fits(const FusedK& k) {
+    const int64_t sp = (k.K + kDecStep - 1) / kDecStep;
+    return k.M <= 2 && (int64_t)k.M * sp * kDecStep * (int64_t)sizeof(float) <= kDecXBytes;
+}
+
+template <int DT, int MR, int KS>
+void launch_decode_ks(const FusedK& k, bool qx, hipStream_t st) {
+    const int sp = (k.K + kDecStep - 1) / kDecStep;
+    const size_t xl = (size_t)MR * sp * kDecStep * sizeof(float);
+    const unsigned grid = (unsigned)((k.N + kDecWaves / KS - 1) / (kDecWaves / KS));
+    if (qx) fused_decode_kernel<DT, MR, KS, true><<<grid, kDecWaves * 64, xl, st>>>(k);
+    else fused_decode_kernel<DT, MR, KS, false><<<grid, kDecWaves * 64, xl, st>>>(k);
+}
+
+// Two waves per row (each half of the steps) when the row has at least 8
+// steps and the rows alone would give too few waves (N < 2048) or too many
+// per CU round (N > 6144); measured at M = 1: 4096 x 1024 6.8 -> 5.4 us,
+// 8192 x 8192 47.4 -> 41.2 us; 4096 x 4096 12.6 (one wave) against 13.9.
+template <int DT, int MR>
+void launch_decode(const FusedK& k, bool qx, hipStream_t st) {
+    const int sp = (k.K + kDecStep - 1) / kDecStep;
+    if (sp >= 8 && (k.N < 2048 || k.N > 6144)) launch_decode_ks<DT, MR, 2>(k, qx, st);
+    else launch_decode_ks<DT, MR, 1>(k, qx, st);
+}
+
 template <int DT, int WM, int TN, int NW, bool XL = false>
 void launch_cfg(const FusedK& k, bool qx, hipStream_t st) {
     const int tiles = ((k.M + 16 * WM - 1) / (16 * WM)) * ((k.N + 16 * TN - 1) / (16 * TN));
@@ -325,6 +602,11 @@ template <int DT>
 void launch_dt(const FusedK& k, bool qx, hipStream_t st) {
     const int64_t nkt = k.K / kFBK;
     auto tiles = [&](int bm, int bn) { return ((k.M + bm - 1) / bm) * (int64_t)((k.N + bn - 1) / bn); };
+    if (decode_form_fits(k)) {
+        if (k.M == 1) launch_decode<DT, 1>(k, qx, st);
+        else launch_decode<DT, 2>(k, qx, st);
+        return;
+    }
     if (k.M <= 16) {
         const bool xl = (int64_t)k.M * (k.K + 4) * (int64_t)sizeof(float) <= kXlBytes;
         if (nkt >= 16) {

@@ -65,6 +65,61 @@ def test_fused_linear_f32_vs_fp64(lead, K, N):
     assert err <= TOL
 
 
+# The streamed decode form (M <= 2, FQ(X) within 48 KiB of LDS): one weight
+# row per wave, or two waves per row (K split) for short or very tall weights;
+# K not a multiple of its 512-value step, a single partial step, rows past N
+# in the last workgroup, zeros in W and X (the masked magnitudes), the largest
+# contractions it takes (M 1: 12288, M 2: 6144) and the first it leaves to
+# the MFMA form.
+@pytest.mark.parametrize("m,K,N", [(1, 4096, 4096), (2, 4096, 4096), (1, 4096, 1024), (2, 4096, 1024),
+                                   (1, 4000, 4000), (2, 544, 4097), (1, 32, 7), (2, 96, 13), (1, 8192, 6500),
+                                   (1, 12288, 300), (2, 6144, 300), (1, 12320, 64), (2, 6176, 64), (1, 1024, 1)])
+def test_fused_linear_decode_form(m, K, N):
+    from axs.unified import hip_linear
+
+    print(f"[fused decode m={m} K={K} N={N}]", flush=True)
+    x, w, b = _inputs((m,), K, N, 3 * K + N)
+    w[:, 5::7] = 0.0                  # zeros inside blocks
+    w[N // 2, :] = 0.0                # a zero row
+    x[:, : K // 4] = 0.0              # a zero run of X
+    y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), b.to(DEV))
+    err = oracle.rel_l2(y.cpu().numpy(), _exact(x, w, b))
+    print(f"  rel-L2 {err:.2e}", flush=True)
+    assert err <= TOL
+    # repeat: same bits (fixed reduction order)
+    assert torch.equal(hip_linear.fused_forward(x.to(DEV), w.to(DEV), b.to(DEV)), y)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3])
+def test_fused_linear_special_blocks(m):
+    """Blocks the short FQ sequence does not cover take the general one
+    (m 1, 2: the decode form's per-step fallback; m 3: the MFMA form): a NaN
+    block (the whole row's output NaN), an inf block, a row of 1e-33 values
+    (every block's e1 below -100), a row scaled by 1e30, a block with
+    subnormals beside normal values."""
+    from axs.unified import hip_linear
+
+    K, N = 2048, 1024
+    x, w, b = _inputs((m,), K, N, 77, outliers=False)
+    w[3, 100] = float("nan")
+    w[4, 64:96] = w[4, 64:96].abs()
+    w[4, 70] = float("inf")
+    w[5] *= 1e-33
+    w[6] *= 1e30
+    w[7, 0:32] = 1e-41
+    w[7, 3] = 0.5
+    y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), b.to(DEV)).cpu().numpy().astype(np.float64)
+    want = _exact(x, w, b)
+    assert np.array_equal(np.isnan(y), np.isnan(want)), (np.isnan(y).sum(), np.isnan(want).sum())
+    assert np.array_equal(np.isinf(y), np.isinf(want))
+    assert np.array_equal(np.sign(y[np.isinf(y)]), np.sign(want[np.isinf(want)]))
+    assert np.isnan(y[:, 3]).all()
+    fin = np.isfinite(want).all(axis=0)
+    for c in (5, 6, 7):                # the special rows, each against its own scale
+        assert fin[c] and oracle.rel_l2(y[:, c], want[:, c]) <= TOL, c
+    assert oracle.rel_l2(y[:, fin], want[:, fin]) <= TOL
+
+
 @pytest.mark.parametrize("K", [33, 50, 100, 127, 255])
 def test_fused_linear_ragged_k(K):
     from axs.unified import hip_linear
@@ -77,14 +132,14 @@ def test_fused_linear_ragged_k(K):
 def test_fused_linear_raw_input_and_no_bias():
     from axs.unified import hip_linear
 
-    for m in (96, 3):
+    for m in (96, 3, 2, 1):
         x, w, b = _inputs((m,), 1024, 768, 9)
         y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), None, quantize_input=False)
         assert oracle.rel_l2(y.cpu().numpy(), _exact(x, w, None, quantize_input=False)) <= TOL, m
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m", [48, 4])
+@pytest.mark.parametrize("m", [48, 4, 2, 1])
 def test_fused_linear_16bit(dt, m):
     from axs.unified import hip_linear
 
@@ -116,8 +171,9 @@ def test_fused_linear_fq_is_bit_exact_with_the_fq_kernel():
     y = hip_linear.fused_forward(x.to(DEV), eye.to(DEV), None)
     want = oracle.fake_quantize(x.numpy(), 32)
     assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
-    # at most 16 rows: FQ(X) staged once in LDS (decode form), same bits
-    for m in (1, 5, 16):
+    # at most 16 rows: FQ(X) staged once in LDS (the streamed decode form at
+    # 1 and 2 rows, the MFMA form's LDS staging up to 16), same bits
+    for m in (1, 2, 5, 16):
         ym = hip_linear.fused_forward(x[:m].to(DEV), eye.to(DEV), None)
         assert np.array_equal(ym.cpu().numpy().view(np.uint32), want[:m].view(np.uint32)), m
 
