@@ -47,7 +47,11 @@ typedef float f32x4f __attribute__((ext_vector_type(4)));
 
 constexpr int kFBK = 32;             // K per tile = one NF5 block
 constexpr int kFRed = 32 * 1024;     // bytes of LDS for the partial tiles
-constexpr int kXlBytes = 128 * 1024; // LDS for FQ(X) in the XL form: M * (K + 4) floats
+// LDS for FQ(X) in the XL form, M * (K + 4) floats: what the 160 KiB of a CU
+// leaves beside the form's static 20.3 KiB (tables and 16 waves' partial
+// tiles).  8 x 4096 (128.1 KiB) fits: 32.6 -> 17 us against the form that
+// quantizes X in every K tile.
+constexpr int kXlBytes = 139 * 1024;
 
 struct FusedK {
     const void* x; const void* w; const float* bias; void* y;
@@ -579,8 +583,8 @@ void launch_cfg(const FusedK& k, bool qx, hipStream_t st) {
     const int tiles = ((k.M + 16 * WM - 1) / (16 * WM)) * ((k.N + 16 * TN - 1) / (16 * TN));
     const size_t xl_bytes = XL ? (size_t)k.M * (k.K + 4) * sizeof(float) : 0;
     if constexpr (XL) {
-        // up to kXlBytes of dynamic LDS beside ~20 KiB static (148 KiB of the
-        // CU's 160 KiB): raise the per-kernel limit once
+        // up to kXlBytes of dynamic LDS beside ~20 KiB static (159.3 KiB of
+        // the CU's 160 KiB): raise the per-kernel limit once
         static bool attr_set = false;
         if (!attr_set) {
             (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, true, XL>,

@@ -49,10 +49,12 @@ def _exact(x, w, b, quantize_input=True):
                                       ((128,), 1024, 1024), ((256,), 512, 512), ((362,), 4096, 362),
                                       ((64,), 256, 2048), ((512,), 4096, 256), ((5,), 96, 13), ((3, 7), 160, 33),
                                       ((2, 4, 8), 32, 64),
-                                      # the decode form's largest LDS stagings: 16 x (2016 + 4) and
-                                      # 1 x (32736 + 4) floats, just under its 128 KiB (~148 KiB with
-                                      # the static LDS); 16 x 2048 is the first shape past it
-                                      ((16,), 2016, 1024), ((1,), 32736, 64)])
+                                      # the MFMA decode form's largest LDS stagings: 16 x (2208 + 4),
+                                      # 8 x (4096 + 4) and 1 x (35552 + 4) floats, just under its
+                                      # 139 KiB (159.3 KiB with the static LDS); 16 x 2240 is the first
+                                      # shape past it
+                                      ((16,), 2208, 1024), ((16,), 2240, 1024), ((8,), 4096, 2048),
+                                      ((1,), 35552, 64)])
 def test_fused_linear_f32_vs_fp64(lead, K, N):
     from axs.unified import hip_linear
 
