@@ -567,14 +567,16 @@ void launch_decode_ks(const FusedK& k, bool qx, hipStream_t st) {
     else fused_decode_kernel<DT, MR, KS, false><<<grid, kDecWaves * 64, xl, st>>>(k);
 }
 
-// Two waves per row (each half of the steps) when the row has at least 8
-// steps and the rows alone would give too few waves (N < 2048) or too many
-// per CU round (N > 6144); measured at M = 1: 4096 x 1024 6.8 -> 5.4 us,
-// 8192 x 8192 47.4 -> 41.2 us; 4096 x 4096 12.6 (one wave) against 13.9.
+// Two waves per row (each half of the steps) when the rows alone would give
+// too few waves (N < 2048, at least 8 steps a row) or the row is long (16
+// steps or more); measured at M = 1 (K x N): 4096 x 1024 6.8 -> 5.4 us,
+// 8192 x 8192 47.4 -> 41.2 us, 8192 x 16000 97.3 -> 87.1 us; one wave per
+// row at 4096 x 4096 12.6 against 13.9 us, 4096 x 32000 89.8 against
+// 106.3 us, 4096 x 128000 324 against 362 us.
 template <int DT, int MR>
 void launch_decode(const FusedK& k, bool qx, hipStream_t st) {
     const int sp = (k.K + kDecStep - 1) / kDecStep;
-    if (sp >= 8 && (k.N < 2048 || k.N > 6144)) launch_decode_ks<DT, MR, 2>(k, qx, st);
+    if ((sp >= 8 && k.N < 2048) || sp >= 16) launch_decode_ks<DT, MR, 2>(k, qx, st);
     else launch_decode_ks<DT, MR, 1>(k, qx, st);
 }
 
