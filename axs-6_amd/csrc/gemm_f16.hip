@@ -41,6 +41,7 @@ struct GemmK {
     const float* bias; void* out; int64_t ldo; int out_dtype;
     int k_iters;            // 64-half K-steps per blockIdx.y (all of them without split-K)
     int64_t split_stride;   // elements between the split outputs (0 without split-K)
+    int nt;                 // final output with nontemporal stores (gemm_streams_output)
 };
 
 template <int BM, int BN>
@@ -89,17 +90,31 @@ __device__ __forceinline__ void gemm_epilogue(const GemmK& g, const WaveAcc<WM, 
     const int esize = g.out_dtype == AXS6_F32 ? 4 : 2;
     void* const out = reinterpret_cast<char*>(g.out) + (int64_t)by * g.split_stride * esize;
     const bool vec = (g.ldo % 4 == 0) && ((uintptr_t)out % (4 * esize) == 0);
-    const bool nt = g.split_stride == 0;     // final output: streaming stores
     const int row0 = m0 + wm * WM;
-    if (g.out_dtype == AXS6_F32)
-        epilogue_store<AXS6_F32, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
-                                                      vec, nt, lane);
-    else if (g.out_dtype == AXS6_BF16)
-        epilogue_store<AXS6_BF16, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
-                                                       vec, nt, lane);
-    else
-        epilogue_store<AXS6_F16, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0, gcol,
-                                                      vec, nt, lane);
+    // the hint is a template argument (a run-time flag inside the store would
+    // let the compiler merge the two stores and drop it); g.nt is uniform
+    if (g.out_dtype == AXS6_F32) {
+        if (g.nt)
+            epilogue_store<AXS6_F32, true, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0,
+                                                        gcol, vec, lane);
+        else
+            epilogue_store<AXS6_F32, false, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0,
+                                                         gcol, vec, lane);
+    } else if (g.out_dtype == AXS6_BF16) {
+        if (g.nt)
+            epilogue_store<AXS6_BF16, true, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0,
+                                                         gcol, vec, lane);
+        else
+            epilogue_store<AXS6_BF16, false, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N,
+                                                          row0, gcol, vec, lane);
+    } else {
+        if (g.nt)
+            epilogue_store<AXS6_F16, true, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0,
+                                                        gcol, vec, lane);
+        else
+            epilogue_store<AXS6_F16, false, WM, WN, LDW>(acc, ws, rexp_l, cexp, cbias, out, g.ldo, g.M, g.N, row0,
+                                                         gcol, vec, lane);
+    }
 }
 
 // Multi-stage variant: operand tiles go from HBM straight into LDS
@@ -462,6 +477,30 @@ namespace {
 enum GemmVariant { kVarBig = 0, kVarSmall = 1, kVarNarrow = 2, kVarNarrow3 = 3 };
 struct GemmPlan { int variant; int splits; GemmK k; };
 
+// Whether a GEMM's final output goes out with nontemporal stores (the `nt`
+// bit) instead of plain ones.  A plain store leaves the line dirty in the
+// 256 MiB last-level cache, and its write-back to HBM then lands in
+// whichever later kernel evicts it (the backward's first dY pass read 361 MB
+// in 100.7 us after the forward's 361 MB plain output, against 67-71 us
+// alone); nt stores write through while the GEMM, not HBM, is busy, and keep
+// the output out of the L2 the operand tiles use.  Measured forward +
+// backward, in one process against plain stores: [8192, 4096, 11008]
+// 2186-2221 -> 2097-2109 us, [8192, 11008, 4096] 2087-2116 -> 2057-2067 us,
+// [2048, 768, 3072] 83.4-84.7 -> 81.1-82.7 us.  The exception: one round of
+// 256 x 256 tiles (at most one per CU) writes its whole output after the
+// last K-step with nothing to overlap, and there the write-through is
+// exposed (4096^3 forward 140.3-141.5 us plain against 143.2-144.1 us); and
+// outputs under 4 MiB, which neither cache pressure nor write-back makes
+// costly (64 x 1000 x 1000: 37.0 us plain against 37.7 us).  Split-K
+// partials, read back at once by the reduction, stay plain.
+bool gemm_streams_output(const GemmArgs& a, bool split) {
+    if (split) return false;
+    if ((int64_t)a.M * a.N * (a.out_dtype == AXS6_F32 ? 4 : 2) < ((int64_t)4 << 20)) return false;
+    int bm, bn;
+    cfg_tile(pick_cfg(a.M, a.N), &bm, &bn);
+    return !(bm == 256 && tiles_of(a.M, a.N, bm, bn) <= 256);
+}
+
 int gemm_plan(const GemmArgs& a, GemmPlan* p) {
     const int iters = (int)(a.Kp / kGemmK);
     int splits = 1, per = iters;
@@ -476,7 +515,8 @@ int gemm_plan(const GemmArgs& a, GemmPlan* p) {
     p->k = GemmK{a.A, a.lda, a.B, a.ldb, (int)a.M, (int)a.N, (int)a.Kp,
                  split ? nullptr : a.row_exp, split ? nullptr : a.col_exp, split ? nullptr : a.glob_exp, a.glob_add,
                  split ? nullptr : a.bias, split ? (void*)a.split_partial : a.out, split ? a.N : a.ldo,
-                 split ? (int)AXS6_F32 : a.out_dtype, per, split ? a.M * a.N : 0};
+                 split ? (int)AXS6_F32 : a.out_dtype, per, split ? a.M * a.N : 0,
+                 gemm_streams_output(a, split) ? 1 : 0};
     p->splits = splits;
     const int cfg = pick_cfg(a.M, a.N);
     // a long contraction on the narrow tiles: a third slab in flight

@@ -123,45 +123,48 @@ __device__ __forceinline__ void store4(void* out, int64_t ldo, int N, int out_dt
     }
 }
 
+// A store with the nontemporal hint (the `nt` bit) when NT, else a plain one.
+// The choice is a template argument: with a run-time flag the compiler
+// merges the two stores of the branch into one and drops the hint.
+template <bool NT, typename T>
+__device__ __forceinline__ void st_hint(T v, T* p) {
+    if constexpr (NT) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
 // store4 with the output type fixed at compile time; `full` = the 4 columns
-// exist and the row segment is aligned for one vector store.  `nt`: a
-// nontemporal (streaming) store -- the final output is not read again by
-// this GEMM, and keeping it out of the L2 leaves room for the operand tiles
-// of the tiles still running (8192 x 11008 x 4096: 531 -> 483 us; 8192 x
-// 4096 x 11008: 501 -> 455 us).  Split-K partials, which the reduction
-// reads back at once, use plain stores.
-template <int OUT>
+// exist and the row segment is aligned for one vector store.  NT: nontemporal
+// stores.  A plain store leaves the line dirty in the last-level cache
+// (256 MiB), and its write-back to HBM then lands in whichever later kernel
+// evicts it: a 361 MB read after a 360 MB plain fill took 109 us against
+// 69 us after the same fill with nt stores (the fill 53 against 67 us).  The
+// GEMM's caller picks per launch (gemm_streams_output).
+template <int OUT, bool NT>
 __device__ __forceinline__ void store4t(void* out, int64_t ldo, int N, int row, int col, const float (&v)[4],
-                                        bool full, bool nt) {
+                                        bool full) {
     const int64_t o = (int64_t)row * ldo + col;
     if (full) {
         if constexpr (OUT == AXS6_F32) {
             const f32x4m w = {v[0], v[1], v[2], v[3]};
-            f32x4m* p = reinterpret_cast<f32x4m*>(reinterpret_cast<float*>(out) + o);
-            if (nt) __builtin_nontemporal_store(w, p);
-            else *p = w;
+            st_hint<NT>(w, reinterpret_cast<f32x4m*>(reinterpret_cast<float*>(out) + o));
         } else if constexpr (OUT == AXS6_BF16) {
             typedef uint32_t u32x2g __attribute__((ext_vector_type(2)));
             const u32x2g w = {(uint32_t)to_bf16(v[0]) | ((uint32_t)to_bf16(v[1]) << 16),
                               (uint32_t)to_bf16(v[2]) | ((uint32_t)to_bf16(v[3]) << 16)};
-            u32x2g* p = reinterpret_cast<u32x2g*>(reinterpret_cast<uint16_t*>(out) + o);
-            if (nt) __builtin_nontemporal_store(w, p);
-            else *p = w;
+            st_hint<NT>(w, reinterpret_cast<u32x2g*>(reinterpret_cast<uint16_t*>(out) + o));
         } else {
             typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
             const f16x4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-            f16x4* p = reinterpret_cast<f16x4*>(reinterpret_cast<_Float16*>(out) + o);
-            if (nt) __builtin_nontemporal_store(h, p);
-            else *p = h;
+            st_hint<NT>(h, reinterpret_cast<f16x4*>(reinterpret_cast<_Float16*>(out) + o));
         }
         return;
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         if (col + t >= N) break;
-        if constexpr (OUT == AXS6_F32) reinterpret_cast<float*>(out)[o + t] = v[t];
-        else if constexpr (OUT == AXS6_BF16) reinterpret_cast<uint16_t*>(out)[o + t] = to_bf16(v[t]);
-        else reinterpret_cast<_Float16*>(out)[o + t] = (_Float16)v[t];
+        if constexpr (OUT == AXS6_F32) st_hint<NT>(v[t], reinterpret_cast<float*>(out) + o + t);
+        else if constexpr (OUT == AXS6_BF16) st_hint<NT>(to_bf16(v[t]), reinterpret_cast<uint16_t*>(out) + o + t);
+        else st_hint<NT>((_Float16)v[t], reinterpret_cast<_Float16*>(out) + o + t);
     }
 }
 
@@ -170,10 +173,10 @@ __device__ __forceinline__ void store4t(void* out, int64_t ldo, int N, int row, 
 // 4 consecutive columns per lane for all PASSES row groups and their row
 // exponents at once -- one LDS wait per block row instead of two per row
 // group -- and write them with the output type fixed at compile time.
-template <int OUT, int WM, int WN, int LDW>
+template <int OUT, bool NT, int WM, int WN, int LDW>
 __device__ __forceinline__ void epilogue_store(const WaveAcc<WM, WN>& acc, float* ws, const int (&rexp_l)[WM / 64],
                                                const int (&cexp)[4], const float (&cbias)[4], void* out, int64_t ldo,
-                                               int M, int N, int row0, int gcol, bool vec, bool nt, int lane) {
+                                               int M, int N, int row0, int gcol, bool vec, int lane) {
     constexpr int LANES_PER_ROW = WN / 4;
     constexpr int ROWS_PER_PASS = 64 / LANES_PER_ROW;
     constexpr int PASSES = 32 / ROWS_PER_PASS;
@@ -200,7 +203,7 @@ __device__ __forceinline__ void epilogue_store(const WaveAcc<WM, WN>& acc, float
                               __builtin_amdgcn_ldexpf(q[p].y, rx[p] + cexp[1]) + cbias[1],
                               __builtin_amdgcn_ldexpf(q[p].z, rx[p] + cexp[2]) + cbias[2],
                               __builtin_amdgcn_ldexpf(q[p].w, rx[p] + cexp[3]) + cbias[3]};
-                store4t<OUT>(out, ldo, N, grow, gcol, v, full, nt);
+                store4t<OUT, NT>(out, ldo, N, grow, gcol, v, full);
             }
         }
     }
