@@ -111,7 +111,8 @@ def test_fused_linear_special_blocks(m):
     w[7, 0:32] = 1e-41
     w[7, 3] = 0.5
     y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), b.to(DEV)).cpu().numpy().astype(np.float64)
-    want = _exact(x, w, b)
+    with np.errstate(invalid="ignore", over="ignore"):   # the NaN and inf blocks' products
+        want = _exact(x, w, b)
     assert np.array_equal(np.isnan(y), np.isnan(want)), (np.isnan(y).sum(), np.isnan(want).sum())
     assert np.array_equal(np.isinf(y), np.isinf(want))
     assert np.array_equal(np.sign(y[np.isinf(y)]), np.sign(want[np.isinf(want)]))
@@ -120,6 +121,41 @@ def test_fused_linear_special_blocks(m):
     for c in (5, 6, 7):                # the special rows, each against its own scale
         assert fin[c] and oracle.rel_l2(y[:, c], want[:, c]) <= TOL, c
     assert oracle.rel_l2(y[:, fin], want[:, fin]) <= TOL
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [1, 2, 3])
+def test_fused_linear_special_blocks_16bit(dt, m):
+    """The same special blocks with 16-bit operands (FQ of the upcast values,
+    Y rounded to the dtype): a NaN block, an inf block, a row far above and a
+    row far below unit scale (f16: within its range), subnormals beside normal
+    values."""
+    from axs.unified import hip_linear
+
+    K, N = 2048, 1024
+    x, w, b = _inputs((m,), K, N, 78, outliers=False)
+    big, small, sub = (1e30, 1e-33, 1e-41) if dt == torch.bfloat16 else (1e3, 1e-3, 1e-7)
+    w[3, 100] = float("nan")
+    w[4, 64:96] = w[4, 64:96].abs()
+    w[4, 70] = float("inf")
+    w[5] *= small
+    w[6] *= big
+    w[7, 0:32] = sub
+    w[7, 3] = 0.5
+    x, w = x.to(dt), w.to(dt)
+    y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), b.to(DEV)).cpu()
+    assert y.dtype == dt
+    y = y.double().numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = _exact(x.float(), w.float(), b)
+    assert np.array_equal(np.isnan(y), np.isnan(want)), (np.isnan(y).sum(), np.isnan(want).sum())
+    assert np.array_equal(np.isinf(y), np.isinf(want))
+    assert np.isnan(y[:, 3]).all()
+    fin = np.isfinite(want).all(axis=0)
+    tol = 4e-3 if dt == torch.bfloat16 else 5e-4
+    for c in (5, 6, 7):
+        assert fin[c] and oracle.rel_l2(y[:, c], want[:, c]) <= tol, c
+    assert oracle.rel_l2(y[:, fin], want[:, fin]) <= tol
 
 
 @pytest.mark.parametrize("K", [33, 50, 100, 127, 255])
