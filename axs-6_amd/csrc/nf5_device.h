@@ -431,6 +431,17 @@ __device__ __forceinline__ float dither_step32(uint32_t lo, uint32_t kh) {
     return dither_from_hash(dither_mix(lo ^ kh));
 }
 
+// Nontemporal (streaming) load and store: the `nt` bit, for data a kernel
+// reads or writes once.  A plain store leaves its line dirty in the 256 MiB
+// last-level cache and a later kernel pays the write-back when it evicts it;
+// a streaming kernel that writes through pays it itself, while its own HBM
+// stream is running.  Call sites use these unconditionally: a plain and an
+// nt store on the two sides of one branch get merged and lose the hint.
+template <typename T>
+__device__ __forceinline__ T ld_stream(const T* p) { return __builtin_nontemporal_load(p); }
+template <typename T>
+__device__ __forceinline__ void st_stream(T v, T* p) { __builtin_nontemporal_store(v, p); }
+
 // Stages the LUT (and the band table) in LDS; needs at least 256 threads.
 __device__ __forceinline__ void stage_tables(float* lut_s, uint32_t* band_w, const float* lut_g,
                                              const uint8_t* band_g) {

@@ -466,13 +466,13 @@ __global__ __launch_bounds__(kThreads) void quantize_vec_kernel(
     int64_t vi = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     // the first vector's HBM load goes out before the tables are staged (the
     // two latencies overlap); later ones one iteration ahead
-    u32x4 cur = vi < n_vec ? xv[vi] : u32x4{0u, 0u, 0u, 0u};
+    u32x4 cur = vi < n_vec ? ld_stream(xv + vi) : u32x4{0u, 0u, 0u, 0u};
     reinterpret_cast<uint32_t*>(rev_s)[threadIdx.x] = reinterpret_cast<const uint32_t*>(rev_g)[threadIdx.x];
     stage_tables(lut_s, band_w, lut_g, band_g);
     const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
     for (; vi < span; vi += step) {
         const bool live = vi < n_vec;
-        const u32x4 nxt = vi + step < n_vec ? xv[vi + step] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 nxt = vi + step < n_vec ? ld_stream(xv + vi + step) : u32x4{0u, 0u, 0u, 0u};
         float f[V];
         E::unpack(cur, f);
         cur = nxt;
@@ -489,17 +489,18 @@ __global__ __launch_bounds__(kThreads) void quantize_vec_kernel(
         for (int e = 0; e < V; ++e) d[e] = STOCH ? dither_step(dv, e) : 0.0f;
         uint32_t cw[2], sw[2];                         // V bytes of codes and signs
         const int ex = quant_values<V, STOCH>(f, m, d, lut_s, band_s, rev_s, fq != nullptr, cw, sw);
+        // the outputs are written once: streaming stores
         if (live) {
             if constexpr (V == 4) {
-                reinterpret_cast<uint32_t*>(codes)[vi] = cw[0];
-                if (signs) reinterpret_cast<uint32_t*>(signs)[vi] = sw[0];
+                st_stream(cw[0], reinterpret_cast<uint32_t*>(codes) + vi);
+                if (signs) st_stream(sw[0], reinterpret_cast<uint32_t*>(signs) + vi);
             } else {
-                reinterpret_cast<u32x2*>(codes)[vi] = u32x2{cw[0], cw[1]};
-                if (signs) reinterpret_cast<u32x2*>(signs)[vi] = u32x2{sw[0], sw[1]};
+                st_stream(u32x2{cw[0], cw[1]}, reinterpret_cast<u32x2*>(codes) + vi);
+                if (signs) st_stream(u32x2{sw[0], sw[1]}, reinterpret_cast<u32x2*>(signs) + vi);
             }
-            if (vi % G == 0) exps[vi / G] = (uint8_t)ex;
+            if (vi % G == 0) st_stream((uint8_t)ex, exps + vi / G);
         }
-        if (fq && live) reinterpret_cast<u32x4*>(fq)[vi] = E::pack(f);
+        if (fq && live) st_stream(E::pack(f), reinterpret_cast<u32x4*>(fq) + vi);
     }
 }
 
@@ -584,8 +585,8 @@ __global__ __launch_bounds__(kThreads) void dequantize_vec_kernel(const uint8_t*
     __syncthreads();
     const int sh = bs == 8 ? 1 : (bs == 16 ? 2 : 3);    // groups of 4 per block: 2^sh
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kThreads) {
-        const uint32_t cw = reinterpret_cast<const uint32_t*>(codes)[i];
-        const uint32_t sw = signs ? reinterpret_cast<const uint32_t*>(signs)[i] : 0u;
+        const uint32_t cw = ld_stream(reinterpret_cast<const uint32_t*>(codes) + i);
+        const uint32_t sw = signs ? ld_stream(reinterpret_cast<const uint32_t*>(signs) + i) : 0u;
         const float scale = pow2_float((int)exps[i >> sh] - kExpBias);
         float v[4];
 #pragma unroll
@@ -596,7 +597,7 @@ __global__ __launch_bounds__(kThreads) void dequantize_vec_kernel(const uint8_t*
         u32x4 w;
         w.x = __float_as_uint(v[0]); w.y = __float_as_uint(v[1]);
         w.z = __float_as_uint(v[2]); w.w = __float_as_uint(v[3]);
-        reinterpret_cast<u32x4*>(y)[i] = w;
+        st_stream(w, reinterpret_cast<u32x4*>(y) + i);
     }
 }
 

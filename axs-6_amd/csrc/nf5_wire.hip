@@ -157,12 +157,12 @@ template <int DT>
 __device__ __forceinline__ void load_group(const typename Elem<DT>::S* x, int64_t q, float (&f)[4]) {
     using E = Elem<DT>;
     if constexpr (DT == AXS6_F32) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(x + q * 4);
+        const u32x4 v = ld_stream(reinterpret_cast<const u32x4*>(x + q * 4));
         f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
         f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
     } else {
         typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        const u32x2 v = *reinterpret_cast<const u32x2*>(x + q * 4);
+        const u32x2 v = ld_stream(reinterpret_cast<const u32x2*>(x + q * 4));
         using S = typename E::S;
         f[0] = E::to_f(__builtin_bit_cast(S, (uint16_t)(v.x & 0xffffu)));
         f[1] = E::to_f(__builtin_bit_cast(S, (uint16_t)(v.x >> 16)));
@@ -273,7 +273,7 @@ __global__ __launch_bounds__(kThreads) void wire_pack_vec_kernel(const typename 
         const int nbytes = left < U * TB ? (int)left : U * TB;
         for (int c = tid; c * 16 < nbytes; c += kThreads) {
             if (c * 16 + 16 <= nbytes) {
-                *reinterpret_cast<u32x4*>(buf + base + c * 16) = *reinterpret_cast<const u32x4*>(recs + c * 16);
+                st_stream(*reinterpret_cast<const u32x4*>(recs + c * 16), reinterpret_cast<u32x4*>(buf + base + c * 16));
             } else {
                 for (int b = c * 16; b < nbytes; ++b) buf[base + b] = recs[b];
             }
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(kThreads) void wire_unpack_vec_kernel(const uint8_t
         const int nbytes = left < U * TB ? (int)left : U * TB;
         for (int c = tid; c * 16 < nbytes; c += kThreads) {
             if (c * 16 + 16 <= nbytes) {
-                *reinterpret_cast<u32x4*>(recs + c * 16) = *reinterpret_cast<const u32x4*>(buf + base + c * 16);
+                *reinterpret_cast<u32x4*>(recs + c * 16) = ld_stream(reinterpret_cast<const u32x4*>(buf + base + c * 16));
             } else {
                 for (int b = c * 16; b < nbytes; ++b) recs[b] = buf[base + b];
             }
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(kThreads) void wire_unpack_vec_kernel(const uint8_t
                             if (c + e < rg.cols) p[e] = v[e];
                     }
                 } else {
-                    *reinterpret_cast<u32x4*>(y + q * 4) = w;
+                    st_stream(w, reinterpret_cast<u32x4*>(y + q * 4));
                 }
             }
         }

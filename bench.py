@@ -249,47 +249,76 @@ def bench_linear(steps: int, warmup: int, dtype=None):
             "kernels": kern}
 
 
+def _timed_cold(fn, n_in: int, reps: int, warmup: int, keep: int = 3) -> float:
+    """Device ms per call of fn(i), HBM-cold, from HIP-graph replays (so host
+    time per API call, which allocates its outputs, is not mixed in): call i
+    takes input set i % n_in (the caller sizes the sets past the 256 MiB
+    last-level cache) and the last `keep` results stay referenced, so each
+    call writes a different buffer of the graph's pool than the call before
+    (a result freed at once would come back at the same address)."""
+    import collections
+
+    import torch
+
+    held = collections.deque(maxlen=keep)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(warmup):
+            held.append(fn(i))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    held.clear()
+    steps = max(reps, 2 * n_in)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            held.append(fn(i))
+    graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    held.clear()
+    del graph
+    return e0.elapsed_time(e1) / (3 * steps)
+
+
 def bench_wire(reps: int = 20, warmup: int = 3):
-    """NF5 wire format (the reference's 6.25-bit gradient buffer) of one
+    """NF5 wire format (the reference's 6.25-bit gradient buffer) of an
     8192x4096 f32 tensor: quantize+pack and unpack+dequantize, one kernel each.
     Algorithmic bytes: pack 4 B read + 25/32 B written per value; unpack the
     reverse.  The same for the AXSBlock record stream (26/32 B per value).
-    HIP-event device time per call."""
+    Device time per call from HIP-graph replays, HBM-cold (_timed_cold: 3
+    rotating 128 MiB inputs, 8 rotating wire buffers)."""
     import torch
 
     from axs import blocks
     from axs.unified import distributed as d
 
     g = torch.Generator(device="cuda").manual_seed(3)
-    x = torch.randn(*FQ_SHAPE, device="cuda", generator=g)
-    buf = d.pack_gradient_to_buffer(x, 32)
-
-    def timed(fn):
-        for _ in range(warmup):
-            fn()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps
-
-    pack_ms = timed(lambda: d.pack_gradient_to_buffer(x, 32))
-    unpack_ms = timed(lambda: d.unpack_buffer_to_gradient(buf, x.shape, 32))
-    nbytes = x.numel() * 4 + buf.numel()
+    xs = [torch.randn(*FQ_SHAPE, device="cuda", generator=g) for _ in range(3)]
+    bufs = [d.pack_gradient_to_buffer(xs[i % 3] * (1.0 + i), 32) for i in range(8)]
+    shape = xs[0].shape
+    pack_ms = _timed_cold(lambda i: d.pack_gradient_to_buffer(xs[i % 3], 32), 3, reps, warmup)
+    unpack_ms = _timed_cold(lambda i: d.unpack_buffer_to_gradient(bufs[i % 8], shape, 32), 8, reps, warmup)
+    nbytes = xs[0].numel() * 4 + bufs[0].numel()
     # the AXSBlock record stream (2-byte header, 26 B per 32 values): same kernels
-    recs = blocks.encode_blocks(x, 32)
-    bpack_ms = timed(lambda: blocks.encode_blocks(x, 32))
-    bunpack_ms = timed(lambda: blocks.decode_blocks(recs, x.shape, 32))
-    bbytes = x.numel() * 4 + recs.numel()
+    recs = [blocks.encode_blocks(xs[i % 3] * (1.0 + i), 32) for i in range(8)]
+    bpack_ms = _timed_cold(lambda i: blocks.encode_blocks(xs[i % 3], 32), 3, reps, warmup)
+    bunpack_ms = _timed_cold(lambda i: blocks.decode_blocks(recs[i % 8], shape, 32), 8, reps, warmup)
+    bbytes = xs[0].numel() * 4 + recs[0].numel()
     return {"metric": "NF5 wire format GB/s @8192x4096 fp32 (quantize+pack, unpack+dequantize)",
-            "buffer_bytes": buf.numel(), "bits_per_value": round(buf.numel() * 8 / x.numel(), 4),
+            "cache": "cold: rotating inputs and freshly written outputs, past the 256 MiB last-level cache",
+            "buffer_bytes": bufs[0].numel(), "bits_per_value": round(bufs[0].numel() * 8 / xs[0].numel(), 4),
             "pack_ms": round(pack_ms, 5), "unpack_ms": round(unpack_ms, 5),
             "pack_gbs": round(nbytes / (pack_ms * 1e-3) / 1e9, 1),
             "unpack_gbs": round(nbytes / (unpack_ms * 1e-3) / 1e9, 1),
-            "axs_blocks": {"buffer_bytes": recs.numel(),
+            "axs_blocks": {"buffer_bytes": recs[0].numel(),
                            "encode_ms": round(bpack_ms, 5), "decode_ms": round(bunpack_ms, 5),
                            "encode_gbs": round(bbytes / (bpack_ms * 1e-3) / 1e9, 1),
                            "decode_gbs": round(bbytes / (bunpack_ms * 1e-3) / 1e9, 1)}}
@@ -297,37 +326,26 @@ def bench_wire(reps: int = 20, warmup: int = 3):
 
 def bench_codec(reps: int = 20, warmup: int = 3):
     """quantize_unified / dequantize_unified (the AXSTensor codec, config 1's
-    operation) on one 8192x4096 f32 tensor, block 32, nearest rounding.
+    operation) on an 8192x4096 f32 tensor, block 32, nearest rounding.
     Algorithmic bytes per value: quantize with the FQ output 4 read + 1 code +
     1 sign + 1/32 exponent + 4 FQ written = 10.03; dequantize 1 + 1 + 1/32
-    read + 4 written = 6.03.  HIP-event device time per call."""
+    read + 4 written = 6.03.  Device time per call from HIP-graph replays,
+    HBM-cold (_timed_cold: 3 rotating 128 MiB inputs, 8 rotating code sets)."""
     import torch
 
     from axs.unified.hip_kernels import hip_dequantize, hip_quantize
 
     g = torch.Generator(device="cuda").manual_seed(4)
-    x = torch.randn(*FQ_SHAPE, device="cuda", generator=g)
-    e, c, s, _ = hip_quantize(x, 32)
+    xs = [torch.randn(*FQ_SHAPE, device="cuda", generator=g) for _ in range(3)]
+    codes = [hip_quantize(xs[i % 3] * (1.0 + i), 32)[:3] for i in range(8)]
     rows, cols = FQ_SHAPE
-
-    def timed(fn):
-        for _ in range(warmup):
-            fn()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps
-
-    q_ms = timed(lambda: hip_quantize(x, 32, with_fake_quantized=True))
-    d_ms = timed(lambda: hip_dequantize(e, c, s, rows, cols, 32))
-    n = x.numel()
+    q_ms = _timed_cold(lambda i: hip_quantize(xs[i % 3], 32, with_fake_quantized=True), 3, reps, warmup)
+    d_ms = _timed_cold(lambda i: hip_dequantize(*codes[i % 8], rows, cols, 32), 8, reps, warmup)
+    n = xs[0].numel()
     q_bytes = n * (4 + 1 + 1 + 4) + n // 32
     d_bytes = n * (1 + 1 + 4) + n // 32
     return {"metric": "NF5 quantize (+FQ output) / dequantize GB/s @8192x4096 fp32, block 32",
+            "cache": "cold: rotating inputs and freshly written outputs, past the 256 MiB last-level cache",
             "quantize_ms": round(q_ms, 5), "dequantize_ms": round(d_ms, 5),
             "quantize_gbs": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
             "dequantize_gbs": round(d_bytes / (d_ms * 1e-3) / 1e9, 1)}
