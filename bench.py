@@ -368,9 +368,19 @@ def bench_configs(steps: int = 200, warmup: int = 20):
         _, gpu_ms, _ = time_steps(launch, launch, steps, warmup)
         nbytes = 2 * x.element_size() * x.numel()
         tag = "" if dt == torch.float32 else "_bf16"
-        out[f"fq_{shape[0]}x{shape[1]}{tag}"] = {"us_per_launch": round(gpu_ms * 1e3, 2),
-                                             "gbs": round(nbytes / (gpu_ms * 1e-3) / 1e9, 1),
-                                             "frac": round(nbytes / (gpu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        rates = lambda ms: {"us_per_launch": round(ms * 1e3, 2),  # noqa: E731
+                            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if x.numel() * x.element_size() >= (64 << 20):
+            # HBM-cold: 5 rotating inputs (320 MiB) and fresh outputs; the
+            # one-input replay (the last-level cache may hold it) beside it
+            xs = [x] + [torch.randn(*shape, device="cuda", generator=g).to(dt) for _ in range(4)]
+            cold_ms = _timed_cold(lambda i: hip_fused_fake_quantize(xs[i % 5], 32, "nearest"), 5, steps // 2,
+                                  warmup)
+            out[f"fq_{shape[0]}x{shape[1]}{tag}"] = {**rates(cold_ms), "cache": "cold", "warm": rates(gpu_ms)}
+            del xs
+        else:
+            out[f"fq_{shape[0]}x{shape[1]}{tag}"] = rates(gpu_ms)
     x = torch.randn(1024, 1024, device="cuda", generator=g) * 0.02
     e, c, s_, _ = hip_quantize(x, 32)
     q = lambda: hip_quantize(x, 32)  # noqa: E731
@@ -391,51 +401,56 @@ LIN_TRAIN_SHAPES = [(8192, 4096, 11008), (8192, 11008, 4096), (2048, 768, 3072),
 
 
 def bench_fused(reps: int = 100, warmup: int = 10):
-    """The single-launch fused linear (FQ in the tile loads, fp32 MFMA) at
-    outputs <= 128K elements, where accelerated_linear / triton_fused_linear
-    dispatch to it: decode-like M against a 4096 x 4096 weight and a small
-    square layer, device time per call (HIP events), beside the packing +
-    fp16-GEMM path on the same inputs."""
+    """The single-launch fused linear (FQ in the tile loads) at outputs <= 128K
+    elements, where accelerated_linear / triton_fused_linear dispatch to it:
+    decode-like M against a 4096 x 4096 weight and a small square layer,
+    device time per call from HIP-graph replays, beside the packing +
+    fp16-GEMM path on the same inputs.  fused_us replays one weight (the
+    last-level cache may hold it); for the 4096 x 4096 weights fused_cold_us
+    rotates 5 (320 MiB, past the cache)."""
     import torch
 
     from axs import _lib
     from axs.unified import hip_linear
 
-    def ev(fn):
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps
+    def stream():   # taken at call time: inside a graph capture it is the capture stream
+        return torch.cuda.current_stream().cuda_stream
 
     g = torch.Generator(device="cuda").manual_seed(9)
     out = {"metric": "fused FQ + linear (M*N <= 128K outputs), device us per call",
-           "note": "fused: one launch, FQ of each 32-wide K tile as it is loaded, fp32 MFMA; "
-                   "packed: FQ + fp16 packing of X and W, then the fp16-MFMA GEMM"}
+           "note": "fused: one launch (M <= 2: a weight row per wave, VALU products; else FQ of each 32-wide "
+                   "K tile as it is loaded, fp32 MFMA); packed: FQ + fp16 packing of X and W, then the "
+                   "fp16-MFMA GEMM; HIP-graph replays"}
     for M, K, N in ((1, 4096, 4096), (32, 4096, 4096), (128, 1024, 1024), (256, 512, 512)):
         X = torch.randn(M, K, device="cuda", generator=g)
-        W = torch.randn(N, K, device="cuda", generator=g) * K ** -0.5
+        big = N * K * 4 >= (64 << 20)
+        Ws = [torch.randn(N, K, device="cuda", generator=g) * K ** -0.5 for _ in range(5 if big else 1)]
+        W = Ws[0]
         b = torch.zeros(N, device="cuda")
         y = torch.empty(M, N, device="cuda")
-        st = _lib.stream_of(X)
-        fused = ev(lambda: _lib.call("axs6_nf5_fused_linear", X.data_ptr(), W.data_ptr(), b.data_ptr(), y.data_ptr(),
-                                     _lib.F32, M, N, K, 32, 1, st))
+
+        def fused_call(w):
+            _lib.call("axs6_nf5_fused_linear", X.data_ptr(), w.data_ptr(), b.data_ptr(), y.data_ptr(),
+                      _lib.F32, M, N, K, 32, 1, stream())
+
+        fused = _timed_cold(lambda i: fused_call(W), 1, reps, warmup)
         Kp = hip_linear.padded_k(K)
         xq = torch.empty(M, Kp, dtype=torch.float16, device="cuda")
         wq = torch.empty(N, Kp, dtype=torch.float16, device="cuda")
         sx = torch.empty(M, dtype=torch.int32, device="cuda")
         sw = torch.empty(N, dtype=torch.int32, device="cuda")
-        packed = ev(lambda: _lib.call("axs6_nf5_linear_forward", X.data_ptr(), W.data_ptr(), b.data_ptr(),
-                                      y.data_ptr(), _lib.F32, M, N, K, 32, 1, xq.data_ptr(), sx.data_ptr(),
-                                      wq.data_ptr(), sw.data_ptr(), st))
-        out[f"{M}x{K}x{N}"] = {"fused_us": round(fused * 1e3, 1), "packed_us": round(packed * 1e3, 1),
-                               "weight_gbs": round(N * K * 4 / (fused * 1e-3) / 1e9, 1)}
+        packed = _timed_cold(lambda i: _lib.call("axs6_nf5_linear_forward", X.data_ptr(), W.data_ptr(),
+                                                 b.data_ptr(), y.data_ptr(), _lib.F32, M, N, K, 32, 1,
+                                                 xq.data_ptr(), sx.data_ptr(), wq.data_ptr(), sw.data_ptr(),
+                                                 stream()), 1, reps, warmup)
+        row = {"fused_us": round(fused * 1e3, 1), "packed_us": round(packed * 1e3, 1),
+               "weight_gbs": round(N * K * 4 / (fused * 1e-3) / 1e9, 1)}
+        if big:
+            cold = _timed_cold(lambda i: fused_call(Ws[i % 5]), 5, reps, warmup)
+            row["fused_cold_us"] = round(cold * 1e3, 1)
+            row["weight_gbs_cold"] = round(N * K * 4 / (cold * 1e-3) / 1e9, 1)
+        out[f"{M}x{K}x{N}"] = row
+        del Ws, W
     return out
 
 
