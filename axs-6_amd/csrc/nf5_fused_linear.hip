@@ -641,6 +641,25 @@ void launch_dt(const FusedK& k, bool qx, hipStream_t st) {
 
 using namespace axs6;
 
+// Whether a caller does better to fake-quantize X on its own first (the
+// streaming FQ kernel, once) and run the fused kernel on FQ(X) without
+// quantize_input: the shapes whose X neither the decode form nor the MFMA
+// form's LDS staging holds, so every workgroup quantizes all of X again in
+// its K tiles, with contractions long enough (K >= 2048) for that to
+// outweigh a second launch.  f32 only: the fused kernel keeps 16-bit inputs'
+// FQ values in f32, which an FQ of the 16-bit tensor would round.  Measured
+// (graph-free pairs, f32): 16 x 4096 x 4096 33.0 -> 22.1 us, 32 x 4096 x
+// 4096 31.0 -> 28.7 us, 16 x 8192 x 512 52.2 -> 34.8 us, 362 x 4096 x 362
+// 58.4 -> 46.9 us; 128 x 1024 x 1024 11.1 against 12.3 us split (K < 2048).
+extern "C" int32_t axs6_nf5_fused_linear_split_x(int64_t M, int64_t N, int64_t K, int32_t dtype) {
+    if (dtype != AXS6_F32 || M <= 0 || N <= 0 || K < 2048 || K % 32 != 0 || K > (1 << 30) || M > (1 << 30))
+        return 0;
+    const FusedK k{nullptr, nullptr, nullptr, nullptr, (int)M, (int)N, (int)K, nullptr, nullptr};
+    if (decode_form_fits(k)) return 0;
+    const bool xl = M <= 16 && M * (K + 4) * (int64_t)sizeof(float) <= kXlBytes;
+    return xl ? 0 : 1;
+}
+
 extern "C" int axs6_nf5_fused_linear(const void* x, const void* w, const float* bias, void* y, int32_t dtype,
                                      int64_t M, int64_t N, int64_t K, int32_t block_size, int32_t quantize_input,
                                      void* stream) {

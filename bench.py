@@ -407,11 +407,13 @@ LIN_TRAIN_SHAPES = [(8192, 4096, 11008), (8192, 11008, 4096), (2048, 768, 3072),
 
 
 def bench_fused(reps: int = 100, warmup: int = 10):
-    """The single-launch fused linear (FQ in the tile loads) at outputs <= 128K
-    elements, where accelerated_linear / triton_fused_linear dispatch to it:
-    decode-like M against a 4096 x 4096 weight and a small square layer,
-    device time per call from HIP-graph replays, beside the packing +
-    fp16-GEMM path on the same inputs.  fused_us replays one weight (the
+    """The fused linear (FQ in the tile loads) at outputs <= 128K elements,
+    where accelerated_linear / triton_fused_linear dispatch to it: decode-like
+    M against a 4096 x 4096 weight and a small square layer, device time per
+    call from HIP-graph replays, beside the packing + fp16-GEMM path on the
+    same inputs.  fused_us is hip_linear.fused_forward (one launch, or the
+    FQ kernel on X first where the library advises it, split_x);
+    one_launch_us the single fused launch.  They replay one weight (the
     last-level cache may hold it); for the 4096 x 4096 weights fused_cold_us
     rotates 5 (320 MiB, past the cache)."""
     import torch
@@ -436,10 +438,16 @@ def bench_fused(reps: int = 100, warmup: int = 10):
         y = torch.empty(M, N, device="cuda")
 
         def fused_call(w):
+            # the public path (triton_fused_linear's): one launch, or FQ(X)
+            # first where axs6_nf5_fused_linear_split_x advises it
+            return hip_linear.fused_forward(X, w, b)
+
+        def one_launch(w):
             _lib.call("axs6_nf5_fused_linear", X.data_ptr(), w.data_ptr(), b.data_ptr(), y.data_ptr(),
                       _lib.F32, M, N, K, 32, 1, stream())
 
         fused = _timed_cold(lambda i: fused_call(W), 1, reps, warmup)
+        single = _timed_cold(lambda i: one_launch(W), 1, reps, warmup)
         Kp = hip_linear.padded_k(K)
         xq = torch.empty(M, Kp, dtype=torch.float16, device="cuda")
         wq = torch.empty(N, Kp, dtype=torch.float16, device="cuda")
@@ -449,8 +457,9 @@ def bench_fused(reps: int = 100, warmup: int = 10):
                                                  b.data_ptr(), y.data_ptr(), _lib.F32, M, N, K, 32, 1,
                                                  xq.data_ptr(), sx.data_ptr(), wq.data_ptr(), sw.data_ptr(),
                                                  stream()), 1, reps, warmup)
-        row = {"fused_us": round(fused * 1e3, 1), "packed_us": round(packed * 1e3, 1),
-               "weight_gbs": round(N * K * 4 / (fused * 1e-3) / 1e9, 1)}
+        row = {"fused_us": round(fused * 1e3, 1), "one_launch_us": round(single * 1e3, 1),
+               "split_x": bool(_lib.lib().axs6_nf5_fused_linear_split_x(M, N, K, _lib.F32)),
+               "packed_us": round(packed * 1e3, 1), "weight_gbs": round(N * K * 4 / (fused * 1e-3) / 1e9, 1)}
         if big:
             cold = _timed_cold(lambda i: fused_call(Ws[i % 5]), 5, reps, warmup)
             row["fused_cold_us"] = round(cold * 1e3, 1)

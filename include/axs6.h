@@ -240,6 +240,16 @@ int axs6_nf5_fused_linear(const void* x, const void* w, const float* bias, void*
                           int64_t M, int64_t N, int64_t K, int32_t block_size, int32_t quantize_input,
                           void* stream);
 
+/* 1 when the caller of axs6_nf5_fused_linear does better to fake-quantize x
+ * first (axs6_nf5_fake_quantize, nearest, into an f32 buffer) and call it on
+ * FQ(x) with quantize_input = 0 -- the same results, bit for bit: f32 inputs
+ * whose rows neither of the kernel's LDS stagings of FQ(x) holds and K >= 2048,
+ * where every workgroup would quantize all of x again; else 0.  A host-only
+ * query (no device work), the dispatch of triton_fused_linear
+ * (axs/unified/triton_kernels.py:385-482) split in two launches; the
+ * reference has no counterpart. */
+int32_t axs6_nf5_fused_linear_split_x(int64_t M, int64_t N, int64_t K, int32_t dtype);
+
 /* Device workspace (bytes) axs6_nf5_linear_backward needs for the requested
  * gradients. */
 size_t axs6_nf5_linear_backward_workspace(int64_t M, int64_t N, int64_t K, int32_t need_dx,

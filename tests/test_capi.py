@@ -175,3 +175,17 @@ def test_noalloc_backward_rejects_shapes_beyond_its_scratch_without_device():
     rc, _ = _status("axs6_nf5_linear_backward_noalloc", p, 0, 0, 64, 64, 32, 0, 0, 0, p, p, p, p, p, p, p,
                     None, None)
     assert rc == 0
+
+
+def test_fused_linear_split_x_rule_without_device():
+    """The host-only query behind fused_forward's two-launch path, (M, N, K)."""
+    f = _lib.lib().axs6_nf5_fused_linear_split_x
+    # X past both LDS stagings of FQ(X) and K >= 2048: quantize X first
+    assert f(16, 4096, 4096, _lib.F32) == 1 and f(32, 4096, 4096, _lib.F32) == 1
+    assert f(17, 300, 2080, _lib.F32) == 1 and f(9, 4096, 4096, _lib.F32) == 1
+    # the streamed decode form (M <= 2) or the MFMA form's staging holds X
+    assert f(1, 4096, 4096, _lib.F32) == 0 and f(8, 4096, 4096, _lib.F32) == 0
+    assert f(2, 4096, 8192, _lib.F32) == 0
+    # short contractions, 16-bit inputs, empty or unaligned shapes
+    assert f(128, 1024, 1024, _lib.F32) == 0 and f(16, 4096, 4096, _lib.BF16) == 0
+    assert f(0, 4096, 4096, _lib.F32) == 0 and f(16, 4096, 4100, _lib.F32) == 0

@@ -158,6 +158,30 @@ def test_fused_linear_special_blocks_16bit(dt, m):
     assert oracle.rel_l2(y[:, fin], want[:, fin]) <= tol
 
 
+@pytest.mark.parametrize("m,K,N", [(9, 4096, 4096), (16, 4096, 4096), (32, 4096, 4096), (64, 2048, 512),
+                                   (17, 2080, 300), (40, 8192, 64)])
+def test_fused_linear_split_x_is_bit_identical(m, K, N):
+    """Where the library advises it (axs6_nf5_fused_linear_split_x: f32, K >=
+    2048, X past both LDS stagings), fused_forward quantizes X with the FQ
+    kernel first and runs the fused kernel on FQ(X) without quantize_input:
+    the output equals the single launch bit for bit, and the oracle's fp64
+    product to the usual bar."""
+    from axs import _lib
+    from axs.unified import hip_linear
+
+    x, w, b = _inputs((m,), K, N, 5 * K + m)
+    assert _lib.lib().axs6_nf5_fused_linear_split_x(m, N, K, _lib.F32) == 1
+    y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), b.to(DEV))
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    one = torch.empty(m, N, device=DEV)
+    _lib.call("axs6_nf5_fused_linear", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), one.data_ptr(), _lib.F32, m, N,
+              K, 32, 1, torch.cuda.current_stream().cuda_stream)
+    assert torch.equal(y, one)
+    assert oracle.rel_l2(y.cpu().numpy(), _exact(x, w, b)) <= TOL
+    # 16-bit inputs never split (their FQ values stay f32 in the kernel)
+    assert _lib.lib().axs6_nf5_fused_linear_split_x(m, N, K, _lib.BF16) == 0
+
+
 @pytest.mark.parametrize("K", [33, 50, 100, 127, 255])
 def test_fused_linear_ragged_k(K):
     from axs.unified import hip_linear
