@@ -182,6 +182,33 @@ def test_fused_linear_split_x_is_bit_identical(m, K, N):
     assert _lib.lib().axs6_nf5_fused_linear_split_x(m, N, K, _lib.BF16) == 0
 
 
+@pytest.mark.parametrize("m,K,N", [(1, 4096, 1024), (2, 8192, 300), (16, 4096, 1024), (5, 512, 512)])
+def test_fused_linear_in_graph_replays(m, K, N):
+    """fused_forward recorded in a HIP graph (the streamed decode form, its
+    two-waves-per-row split, X quantized first, the MFMA form): every replay,
+    with eager work between them, equals the eager call bit for bit."""
+    from axs.unified import hip_linear
+
+    x, w, b = _inputs((m,), K, N, 31 * m + K)
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    eager = hip_linear.fused_forward(xd, wd, bd)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        hip_linear.fused_forward(xd, wd, bd)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = hip_linear.fused_forward(xd, wd, bd)
+    for i in range(3):
+        scratch = torch.randn(1 << 20, device=DEV) * (i + 1)     # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), i
+        del scratch
+
+
 @pytest.mark.parametrize("K", [33, 50, 100, 127, 255])
 def test_fused_linear_ragged_k(K):
     from axs.unified import hip_linear
