@@ -50,6 +50,8 @@ _SIGNATURES: dict[str, list] = {
     "axs6_nf5_linear_backward_workspace": [_i64, _i64, _i64, _i32, _i32, _i32],
     "axs6_nf5_fused_linear": [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp],
     "axs6_nf5_fused_linear_split_x": [_i64, _i64, _i64, _i32],
+    "axs6_nf5_fused_linear_split_workspace": [_i64, _i64],
+    "axs6_nf5_fused_linear_split": [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp],
     "axs6_nf5_wire_bytes": [_i64, _i64, _i32],
     "axs6_nf5_pack_wire": [_vp, _i32, _i64, _i64, _i32, _vp, _vp],
     "axs6_nf5_unpack_wire": [_vp, _i64, _i64, _i32, _vp, _vp],
@@ -74,7 +76,8 @@ _SIGNATURES: dict[str, list] = {
 # entry points that return a value rather than an axs6_status
 _RESTYPES = {"axs6_linear_padded_k": _i64, "axs6_nf5_linear_backward_workspace": ctypes.c_size_t,
              "axs6_nf5_wire_bytes": _i64, "axs6_nf5_block_bytes": _i64, "axs6_multi_tensor_workspace": _i64,
-             "axs6_nf5_row_stats_workspace": _i64, "axs6_nf5_fused_linear_split_x": ctypes.c_int32, "axs6_layer_norm_backward_workspace": _i64}
+             "axs6_nf5_row_stats_workspace": _i64, "axs6_nf5_fused_linear_split_x": ctypes.c_int32,
+             "axs6_nf5_fused_linear_split_workspace": _i64, "axs6_layer_norm_backward_workspace": _i64}
 
 
 class LibraryError(RuntimeError):

@@ -151,16 +151,17 @@ def fused_forward(input, weight, bias=None, quantize_input=True):
         qx = bool(quantize_input)
         with _on_device(x2):
             st = _lib.stream_of(x2)
-            if qx and _lib.lib().axs6_nf5_fused_linear_split_x(M, N, Kb, code):
-                # X quantized once by the FQ kernel, then the fused kernel on
-                # FQ(X): the same values, where the kernel would otherwise
-                # quantize all of X in every workgroup
-                xq = torch.empty_like(x2)
-                _lib.call("axs6_nf5_fake_quantize", x2.data_ptr(), xq.data_ptr(), code, M, Kb, 32, 0, 0, 0,
-                          None, st)
-                x2, qx = xq, False
-            _lib.call("axs6_nf5_fused_linear", x2.data_ptr(), w2.data_ptr(), _lib.ptr(b), y.data_ptr(),
-                      code, M, N, Kb, 32, int(qx), st)
+            if _lib.lib().axs6_nf5_fused_linear_split_x(M, N, Kb, code):
+                # FQ(X) written once in the contraction's read order, then the
+                # contraction on it: the same values, where the single launch
+                # would read and quantize all of X in every workgroup
+                xa = torch.empty(_lib.lib().axs6_nf5_fused_linear_split_workspace(M, Kb) // 4,
+                                 dtype=torch.float32, device=dev)
+                _lib.call("axs6_nf5_fused_linear_split", x2.data_ptr(), w2.data_ptr(), _lib.ptr(b), y.data_ptr(),
+                          xa.data_ptr(), code, M, N, Kb, 32, int(qx), st)
+            else:
+                _lib.call("axs6_nf5_fused_linear", x2.data_ptr(), w2.data_ptr(), _lib.ptr(b), y.data_ptr(),
+                          code, M, N, Kb, 32, int(qx), st)
     return _as_input_dtype(y.reshape(*input.shape[:-1], N), input.dtype)
 
 

@@ -32,7 +32,11 @@
 //     -- and the K loop then reads FQ(X) from LDS and quantizes only W;
 //   * at one or two rows of X whose FQ fits 48 KiB of LDS, the streamed
 //     decode form (fused_decode_kernel) replaces it: a wave per weight row,
-//     VALU products, whole-row loads.
+//     VALU products, whole-row loads;
+//   * past both stagings (axs6_nf5_fused_linear_split), FQ(X) is written
+//     once, in f32 and in the order the instructions read it (XA), by a
+//     first launch, and the MFMA form reads it from there: one contiguous
+//     KiB per load instruction, no FQ of X per workgroup.
 // Unlike the packed fp16 path there is no row shift and no rounding of the
 // operands: the products are those of fp32 FQ values, as in the reference's
 // fused kernel.  For 16-bit inputs the FQ values stay fp32 too, as in the
@@ -159,13 +163,80 @@ __device__ __forceinline__ void stage_x(const FusedK& k, float* xl, const float*
     }
 }
 
-template <int DT, int WM, int TN, int NW, bool QX, bool XL>
+// X in the fragment order of the MFMA form (XA), written by arrange_x_kernel
+// for the two-launch path: K tile kt of 16-row block b takes the 512 floats
+// at (kt * nb + b) * 512 (nb = ceil(M / 16)), half h at + 256 h, and lane
+// l = 16 q + r of the tile's 16x16x4 instructions finds at + 4 l its values
+// for K slots kslot<DT>(q, 4 h .. 4 h + 3) of row 16 b + r.  Each of a
+// wave's two 16-byte X loads per tile then reads 1 KiB contiguously instead
+// of 64-byte pieces of 16 rows (32 x 4096 x 4096: 25.8 -> 19.8 us with X
+// quantized beforehand either way).  f32 for every input dtype: the FQ
+// values the single launch computes, not rounded to the input's type.
+__host__ __device__ inline int64_t xa_floats(int64_t M, int64_t K) { return (M + 15) / 16 * 16 * K; }
+
+// FQ (or, with QX false, a copy) of X into the XA order; the rows from M to
+// the end of the last 16-row block hold zeros.  A thread takes 8 consecutive
+// values of a row, so an NF5 block is a DPP quad (K % 32 == 0) and its two
+// 4-value runs are two 16-byte stores.
+template <int DT, bool QX>
+__global__ __launch_bounds__(256) void arrange_x_kernel(FusedK k, float* xa) {
+    using E = Elem<DT>;
+    using S = typename E::S;
+    __shared__ float lut_s[kLutSize];
+    __shared__ uint32_t band_w[kBandSize / 4];
+    if constexpr (QX) stage_tables(lut_s, band_w, k.lut, k.band);
+    const uint8_t* band_s = reinterpret_cast<const uint8_t*>(band_w);
+    const int per_row = k.K / 8;
+    const int nb = (k.M + 15) / 16;
+    const int c = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    // whole quads leave together (256 and per_row are multiples of 4)
+    if (c >= nb * 16 * per_row) return;
+    const int r = c / per_row, c8 = c - r * per_row;
+    float f[8] = {};
+    if (r < k.M) {
+        const S* p = reinterpret_cast<const S*>(k.x) + (int64_t)r * k.K + 8 * c8;
+        u32x4 v[2];
+        v[0] = *reinterpret_cast<const u32x4*>(p);
+        if constexpr (E::V == 4) v[1] = *reinterpret_cast<const u32x4*>(p + 4);
+        unpack8<DT>(v, f);
+    }
+    if constexpr (QX) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t a = __float_as_uint(f[e]) & 0x7fffffffu;
+            m = m > a ? m : a;
+        }
+        m = group_umax<4>(m);
+        const FqScale s = fq_scale(m, band_s);
+        const float d[8] = {};
+        fq_vector<8>(f, s, lut_s, false, d);
+    }
+    // K offsets 8 j .. 8 j + 7 of the tile (j = c8 % 4): in f32 the slots
+    // 4 q + e (h 0) and 16 + 4 q + e (h 1), so lanes q = 2 (j % 2) and + 1 of
+    // half j / 2; in bf16/f16 8 q + t, so lane q = j, halves 0 and 1
+    const int kt = c8 >> 2, j = c8 & 3, fr = r & 15;
+    float4* tile = reinterpret_cast<float4*>(xa + ((int64_t)kt * nb + (r >> 4)) * 512);
+    const float4 lo = make_float4(f[0], f[1], f[2], f[3]), hi = make_float4(f[4], f[5], f[6], f[7]);
+    if constexpr (E::V == 4) {
+        float4* h = tile + 64 * (j >> 1);
+        const int q0 = 2 * (j & 1);
+        h[16 * q0 + fr] = lo;
+        h[16 * (q0 + 1) + fr] = hi;
+    } else {
+        tile[16 * j + fr] = lo;
+        tile[64 + 16 * j + fr] = hi;
+    }
+}
+
+template <int DT, int WM, int TN, int NW, bool QX, bool XL, bool XA>
 __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
     using E = Elem<DT>;
     using S = typename E::S;
     constexpr int BM = 16 * WM, BN = 16 * TN;
     static_assert(NW * BM * BN * 4 <= kFRed, "partial tiles must fit the reduction LDS");
     static_assert(!XL || WM == 1, "FQ(X) from LDS covers one 16-row block");
+    static_assert(!XA || (!XL && !QX), "XA reads X as arranged, already quantized");
     __shared__ float lut_s[kLutSize];
     __shared__ uint32_t band_w[kBandSize / 4];
     __shared__ __align__(16) float red[NW * BM * BN];
@@ -197,6 +268,13 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
         wlive[j] = r < k.N;
         wrow[j] = ws + (int64_t)(wlive[j] ? r : 0) * k.K;
     }
+    // XA: the workgroup's 16-row blocks of X (a block wholly past M reads
+    // block 0; its rows are not stored)
+    const float* xa = reinterpret_cast<const float*>(k.x);
+    const int nb = (k.M + 15) / 16;
+    int64_t xblk[WM];
+#pragma unroll
+    for (int i = 0; i < WM; ++i) xblk[i] = m0 / 16 + i < nb ? m0 / 16 + i : 0;
 
     // The next K tile is loaded while the current one is quantized and
     // multiplied (two register buffers).  Deeper prefetch was slower: at M 1,
@@ -209,7 +287,14 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
     // stored.
     u32x4 xv[2][WM][2], wv[2][TN][2];
     auto load_tile = [&](int kt, u32x4 (&xd)[WM][2], u32x4 (&wd)[TN][2]) {
-        if constexpr (!XL) {
+        if constexpr (XA) {
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                const float* p = xa + ((int64_t)kt * nb + xblk[i]) * 512 + 4 * lane;
+                xd[i][0] = *reinterpret_cast<const u32x4*>(p);
+                xd[i][1] = *reinterpret_cast<const u32x4*>(p + 256);
+            }
+        } else if constexpr (!XL) {
 #pragma unroll
             for (int i = 0; i < WM; ++i) load8<DT>(xrow[i], kt, q, xd[i]);
         }
@@ -243,8 +328,12 @@ __global__ __launch_bounds__(NW * 64) void fused_linear_kernel(FusedK k) {
         } else {
 #pragma unroll
             for (int i = 0; i < WM; ++i) {
-                unpack8<DT>(xc[i], xf[i]);
-                if constexpr (QX) fq8(xf[i], lut_s, band_s);
+                if constexpr (XA) {
+                    unpack8<AXS6_F32>(xc[i], xf[i]);
+                } else {
+                    unpack8<DT>(xc[i], xf[i]);
+                    if constexpr (QX) fq8(xf[i], lut_s, band_s);
+                }
             }
         }
 #pragma unroll
@@ -580,7 +669,7 @@ void launch_decode(const FusedK& k, bool qx, hipStream_t st) {
     else launch_decode_ks<DT, MR, 1>(k, qx, st);
 }
 
-template <int DT, int WM, int TN, int NW, bool XL = false>
+template <int DT, int WM, int TN, int NW, bool XL = false, bool XA = false>
 void launch_cfg(const FusedK& k, bool qx, hipStream_t st) {
     const int tiles = ((k.M + 16 * WM - 1) / (16 * WM)) * ((k.N + 16 * TN - 1) / (16 * TN));
     const size_t xl_bytes = XL ? (size_t)k.M * (k.K + 4) * sizeof(float) : 0;
@@ -589,51 +678,70 @@ void launch_cfg(const FusedK& k, bool qx, hipStream_t st) {
         // the CU's 160 KiB): raise the per-kernel limit once
         static bool attr_set = false;
         if (!attr_set) {
-            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, true, XL>,
+            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, true, XL, false>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kXlBytes);
-            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, false, XL>,
+            (void)hipFuncSetAttribute((const void*)fused_linear_kernel<DT, WM, TN, NW, false, XL, false>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kXlBytes);
             attr_set = true;
         }
     }
-    if (qx) fused_linear_kernel<DT, WM, TN, NW, true, XL><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
-    else fused_linear_kernel<DT, WM, TN, NW, false, XL><<<dim3((unsigned)tiles), NW * 64, xl_bytes, st>>>(k);
+    const dim3 grid((unsigned)tiles);
+    if constexpr (XA) fused_linear_kernel<DT, WM, TN, NW, false, false, true><<<grid, NW * 64, 0, st>>>(k);
+    else if (qx) fused_linear_kernel<DT, WM, TN, NW, true, XL, false><<<grid, NW * 64, xl_bytes, st>>>(k);
+    else fused_linear_kernel<DT, WM, TN, NW, false, XL, false><<<grid, NW * 64, xl_bytes, st>>>(k);
 }
 
-// Tile and K split by shape: one 16-row block for M <= 16 (decode), else
-// two; the widest column tile (64, 32, 16) that still gives >= 256
-// workgroups; as many K-splitting waves (up to 16, within the reduction LDS)
-// as there are K tiles.
-template <int DT>
-void launch_dt(const FusedK& k, bool qx, hipStream_t st) {
+// The MFMA form's tile and K split by shape: one 16-row block for M <= 16
+// (decode), else two; the widest column tile (64, 32, 16) that still gives
+// >= 256 workgroups; as many K-splitting waves (up to 16, within the
+// reduction LDS) as there are K tiles.  XA: X arranged by arrange_x_kernel.
+template <int DT, bool XA>
+void launch_mfma(const FusedK& k, bool qx, hipStream_t st) {
     const int64_t nkt = k.K / kFBK;
     auto tiles = [&](int bm, int bn) { return ((k.M + bm - 1) / bm) * (int64_t)((k.N + bn - 1) / bn); };
+    if (k.M <= 16) {
+        const bool xl = !XA && (int64_t)k.M * (k.K + 4) * (int64_t)sizeof(float) <= kXlBytes;
+        if (nkt >= 16) {
+            if (xl) launch_cfg<DT, 1, 1, 16, true>(k, qx, st);
+            else launch_cfg<DT, 1, 1, 16, false, XA>(k, qx, st);
+        } else {
+            if (xl) launch_cfg<DT, 1, 1, 4, true>(k, qx, st);
+            else launch_cfg<DT, 1, 1, 4, false, XA>(k, qx, st);
+        }
+        return;
+    }
+    if (tiles(32, 64) >= 256) {
+        if (nkt >= 4) launch_cfg<DT, 2, 4, 4, false, XA>(k, qx, st);
+        else launch_cfg<DT, 2, 4, 1, false, XA>(k, qx, st);
+    } else if (tiles(32, 32) >= 256) {
+        if (nkt >= 8) launch_cfg<DT, 2, 2, 8, false, XA>(k, qx, st);
+        else launch_cfg<DT, 2, 2, 2, false, XA>(k, qx, st);
+    } else {
+        if (nkt >= 16) launch_cfg<DT, 2, 1, 16, false, XA>(k, qx, st);
+        else launch_cfg<DT, 2, 1, 4, false, XA>(k, qx, st);
+    }
+}
+
+template <int DT>
+void launch_dt(const FusedK& k, bool qx, hipStream_t st) {
     if (decode_form_fits(k)) {
         if (k.M == 1) launch_decode<DT, 1>(k, qx, st);
         else launch_decode<DT, 2>(k, qx, st);
         return;
     }
-    if (k.M <= 16) {
-        const bool xl = (int64_t)k.M * (k.K + 4) * (int64_t)sizeof(float) <= kXlBytes;
-        if (nkt >= 16) {
-            if (xl) launch_cfg<DT, 1, 1, 16, true>(k, qx, st);
-            else launch_cfg<DT, 1, 1, 16>(k, qx, st);
-        } else {
-            if (xl) launch_cfg<DT, 1, 1, 4, true>(k, qx, st);
-            else launch_cfg<DT, 1, 1, 4>(k, qx, st);
-        }
-        return;
-    }
-    if (tiles(32, 64) >= 256) {
-        if (nkt >= 4) launch_cfg<DT, 2, 4, 4>(k, qx, st);
-        else launch_cfg<DT, 2, 4, 1>(k, qx, st);
-    } else if (tiles(32, 32) >= 256) {
-        if (nkt >= 8) launch_cfg<DT, 2, 2, 8>(k, qx, st);
-        else launch_cfg<DT, 2, 2, 2>(k, qx, st);
-    } else {
-        if (nkt >= 16) launch_cfg<DT, 2, 1, 16>(k, qx, st);
-        else launch_cfg<DT, 2, 1, 4>(k, qx, st);
-    }
+    launch_mfma<DT, false>(k, qx, st);
+}
+
+// The two-launch path: X (quantized with qx) into the XA order, then the
+// MFMA form on it.
+template <int DT>
+void launch_split(const FusedK& k, float* xa, bool qx, hipStream_t st) {
+    const unsigned blocks = (unsigned)((xa_floats(k.M, k.K) / 8 + 255) / 256);
+    if (qx) arrange_x_kernel<DT, true><<<blocks, 256, 0, st>>>(k, xa);
+    else arrange_x_kernel<DT, false><<<blocks, 256, 0, st>>>(k, xa);
+    FusedK ka = k;
+    ka.x = xa;
+    launch_mfma<DT, true>(ka, false, st);
 }
 
 }  // namespace
@@ -641,18 +749,18 @@ void launch_dt(const FusedK& k, bool qx, hipStream_t st) {
 
 using namespace axs6;
 
-// Whether a caller does better to fake-quantize X on its own first (the
-// streaming FQ kernel, once) and run the fused kernel on FQ(X) without
-// quantize_input: the shapes whose X neither the decode form nor the MFMA
-// form's LDS staging holds, so every workgroup quantizes all of X again in
-// its K tiles, with contractions long enough (K >= 2048) for that to
-// outweigh a second launch.  f32 only: the fused kernel keeps 16-bit inputs'
-// FQ values in f32, which an FQ of the 16-bit tensor would round.  Measured
-// (graph-free pairs, f32): 16 x 4096 x 4096 33.0 -> 22.1 us, 32 x 4096 x
-// 4096 31.0 -> 28.7 us, 16 x 8192 x 512 52.2 -> 34.8 us, 362 x 4096 x 362
-// 58.4 -> 46.9 us; 128 x 1024 x 1024 11.1 against 12.3 us split (K < 2048).
+// Whether a caller does better with the two-launch path
+// (axs6_nf5_fused_linear_split): the shapes whose X neither the decode form
+// nor the MFMA form's LDS staging holds, so every workgroup of the single
+// launch reads (and quantizes) all of X again in its K tiles as 64-byte
+// pieces of 16 rows, with contractions long enough (K >= 1024) for that to
+// outweigh a second launch.  Measured (graph replays, f32, us, two launches
+// against one): 32 x 4096 x 4096 24.0 / 31.0, 16 x 4096 x 4096 18.5 / 32.4,
+// 16 x 8192 x 512 25.4 / 52.3, 362 x 4096 x 362 41.7 / 56.3, 32 x 1024 x
+// 4096 10.4 / 11.2, 256 x 1024 x 512 11.3 / 11.1; K 512: 32 x 512 x 4096
+// 7.7 / 7.4; X within the staging: 8 x 4096 x 4096 18.9 / 17.7.
 extern "C" int32_t axs6_nf5_fused_linear_split_x(int64_t M, int64_t N, int64_t K, int32_t dtype) {
-    if (dtype != AXS6_F32 || M <= 0 || N <= 0 || K < 2048 || K % 32 != 0 || K > (1 << 30) || M > (1 << 30))
+    if (!valid_dtype(dtype) || M <= 0 || N <= 0 || K < 1024 || K % 32 != 0 || K > (1 << 30) || M > (1 << 30))
         return 0;
     const FusedK k{nullptr, nullptr, nullptr, nullptr, (int)M, (int)N, (int)K, nullptr, nullptr};
     if (decode_form_fits(k)) return 0;
@@ -660,10 +768,13 @@ extern "C" int32_t axs6_nf5_fused_linear_split_x(int64_t M, int64_t N, int64_t K
     return xl ? 0 : 1;
 }
 
-extern "C" int axs6_nf5_fused_linear(const void* x, const void* w, const float* bias, void* y, int32_t dtype,
-                                     int64_t M, int64_t N, int64_t K, int32_t block_size, int32_t quantize_input,
-                                     void* stream) {
-    const char* fn = "axs6_nf5_fused_linear";
+namespace {
+
+// Arguments of both fused entry points; *empty set when there is nothing to
+// compute (M or N zero).
+int fused_args(const char* fn, const void* x, const void* w, const void* y, int32_t dtype, int64_t M, int64_t N,
+               int64_t K, int32_t block_size, bool* empty) {
+    *empty = false;
     if (!valid_dtype(dtype)) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: unknown dtype code %d", fn, dtype);
     if (block_size != 32)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: the fused linear requires block_size=32 (got %d)", fn, block_size);
@@ -673,13 +784,28 @@ extern "C" int axs6_nf5_fused_linear(const void* x, const void* w, const float* 
                     (long long)K);
     if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30) || M * ((N + 15) / 16) > (int64_t)INT32_MAX)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: dimension too large", fn);
-    if (M == 0 || N == 0) return AXS6_OK;
+    if (M == 0 || N == 0) {
+        *empty = true;
+        return AXS6_OK;
+    }
     if (K == 0) return fail(AXS6_ERR_UNSUPPORTED, "%s: empty contraction (K = 0)", fn);
     if (!x || !w || !y) return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
     if ((uintptr_t)x % 16 || (uintptr_t)w % 16)
         return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: x and w must be 16-byte aligned", fn);
+    return AXS6_OK;
+}
+
+}  // namespace
+
+extern "C" int axs6_nf5_fused_linear(const void* x, const void* w, const float* bias, void* y, int32_t dtype,
+                                     int64_t M, int64_t N, int64_t K, int32_t block_size, int32_t quantize_input,
+                                     void* stream) {
+    const char* fn = "axs6_nf5_fused_linear";
+    bool empty;
+    int rc = fused_args(fn, x, w, y, dtype, M, N, K, block_size, &empty);
+    if (rc || empty) return rc;
     DeviceTables t;
-    int rc = device_tables(&t);
+    rc = device_tables(&t);
     if (rc) return rc;
     const FusedK k{x, w, bias, y, (int)M, (int)N, (int)K, t.lut, t.band};
     hipStream_t st = (hipStream_t)stream;
@@ -687,5 +813,32 @@ extern "C" int axs6_nf5_fused_linear(const void* x, const void* w, const float* 
     if (dtype == AXS6_F32) launch_dt<AXS6_F32>(k, qx, st);
     else if (dtype == AXS6_BF16) launch_dt<AXS6_BF16>(k, qx, st);
     else launch_dt<AXS6_F16>(k, qx, st);
+    return check_launch(fn);
+}
+
+extern "C" int64_t axs6_nf5_fused_linear_split_workspace(int64_t M, int64_t K) {
+    return M > 0 && K > 0 && M <= (1 << 30) && K <= (1 << 30) ? xa_floats(M, K) * (int64_t)sizeof(float) : 0;
+}
+
+extern "C" int axs6_nf5_fused_linear_split(const void* x, const void* w, const float* bias, void* y,
+                                           float* x_arranged, int32_t dtype, int64_t M, int64_t N, int64_t K,
+                                           int32_t block_size, int32_t quantize_input, void* stream) {
+    const char* fn = "axs6_nf5_fused_linear_split";
+    bool empty;
+    int rc = fused_args(fn, x, w, y, dtype, M, N, K, block_size, &empty);
+    if (rc || empty) return rc;
+    if (xa_floats(M, K) > (int64_t)INT32_MAX)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: x too large for the arranged workspace", fn);
+    if (!x_arranged || (uintptr_t)x_arranged % 16)
+        return fail(AXS6_ERR_INVALID_ARGUMENT, "%s: x_arranged must be a 16-byte aligned device buffer", fn);
+    DeviceTables t;
+    rc = device_tables(&t);
+    if (rc) return rc;
+    const FusedK k{x, w, bias, y, (int)M, (int)N, (int)K, t.lut, t.band};
+    hipStream_t st = (hipStream_t)stream;
+    const bool qx = quantize_input != 0;
+    if (dtype == AXS6_F32) launch_split<AXS6_F32>(k, x_arranged, qx, st);
+    else if (dtype == AXS6_BF16) launch_split<AXS6_BF16>(k, x_arranged, qx, st);
+    else launch_split<AXS6_F16>(k, x_arranged, qx, st);
     return check_launch(fn);
 }

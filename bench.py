@@ -411,8 +411,9 @@ def bench_fused(reps: int = 100, warmup: int = 10):
     where accelerated_linear / triton_fused_linear dispatch to it: decode-like
     M against a 4096 x 4096 weight and a small square layer, device time per
     call from HIP-graph replays, beside the packing + fp16-GEMM path on the
-    same inputs.  fused_us is hip_linear.fused_forward (one launch, or the
-    FQ kernel on X first where the library advises it, split_x);
+    same inputs.  fused_us is hip_linear.fused_forward (one launch, or where
+    the library advises it, split_x, two: FQ(X) once into the contraction's
+    read order, then the contraction);
     one_launch_us the single fused launch.  They replay one weight (the
     last-level cache may hold it); for the 4096 x 4096 weights fused_cold_us
     rotates 5 (320 MiB, past the cache)."""
@@ -438,8 +439,8 @@ def bench_fused(reps: int = 100, warmup: int = 10):
         y = torch.empty(M, N, device="cuda")
 
         def fused_call(w):
-            # the public path (triton_fused_linear's): one launch, or FQ(X)
-            # first where axs6_nf5_fused_linear_split_x advises it
+            # the public path (triton_fused_linear's): one launch, or the
+            # two-launch entry where axs6_nf5_fused_linear_split_x advises it
             return hip_linear.fused_forward(X, w, b)
 
         def one_launch(w):

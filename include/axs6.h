@@ -240,15 +240,31 @@ int axs6_nf5_fused_linear(const void* x, const void* w, const float* bias, void*
                           int64_t M, int64_t N, int64_t K, int32_t block_size, int32_t quantize_input,
                           void* stream);
 
-/* 1 when the caller of axs6_nf5_fused_linear does better to fake-quantize x
- * first (axs6_nf5_fake_quantize, nearest, into an f32 buffer) and call it on
- * FQ(x) with quantize_input = 0 -- the same results, bit for bit: f32 inputs
- * whose rows neither of the kernel's LDS stagings of FQ(x) holds and K >= 2048,
- * where every workgroup would quantize all of x again; else 0.  A host-only
- * query (no device work), the dispatch of triton_fused_linear
- * (axs/unified/triton_kernels.py:385-482) split in two launches; the
- * reference has no counterpart. */
+/* 1 when the caller of axs6_nf5_fused_linear does better to call
+ * axs6_nf5_fused_linear_split instead -- the same results, bit for bit: x
+ * whose rows neither of the single launch's LDS stagings of FQ(x) holds and
+ * K >= 1024, where every workgroup would read and quantize all of x again;
+ * else 0.  A host-only query (no device work), the dispatch of
+ * triton_fused_linear (axs/unified/triton_kernels.py:385-482) split in two
+ * launches; the reference has no counterpart. */
 int32_t axs6_nf5_fused_linear_split_x(int64_t M, int64_t N, int64_t K, int32_t dtype);
+
+/* Bytes of the x_arranged workspace axs6_nf5_fused_linear_split takes:
+ * 16 * ceil(M / 16) * K floats (0 for an empty or oversized shape).  The
+ * reference has no counterpart. */
+int64_t axs6_nf5_fused_linear_split_workspace(int64_t M, int64_t K);
+
+/* axs6_nf5_fused_linear in two launches: FQ(x) (x itself with
+ * quantize_input = 0) is written once to x_arranged in f32, in the order the
+ * contraction's 16x16x4 MFMA instructions read it, and the contraction then
+ * reads it from there instead of quantizing x in every workgroup.  Same
+ * arguments and results, bit for bit, plus x_arranged: a 16-byte aligned
+ * device buffer of axs6_nf5_fused_linear_split_workspace(M, K) bytes,
+ * overwritten.  Replaces the same reference call as axs6_nf5_fused_linear
+ * (axs/unified/triton_kernels.py:185-282,385-482). */
+int axs6_nf5_fused_linear_split(const void* x, const void* w, const float* bias, void* y, float* x_arranged,
+                                int32_t dtype, int64_t M, int64_t N, int64_t K, int32_t block_size,
+                                int32_t quantize_input, void* stream);
 
 /* Device workspace (bytes) axs6_nf5_linear_backward needs for the requested
  * gradients. */

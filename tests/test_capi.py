@@ -180,12 +180,37 @@ def test_noalloc_backward_rejects_shapes_beyond_its_scratch_without_device():
 def test_fused_linear_split_x_rule_without_device():
     """The host-only query behind fused_forward's two-launch path, (M, N, K)."""
     f = _lib.lib().axs6_nf5_fused_linear_split_x
-    # X past both LDS stagings of FQ(X) and K >= 2048: quantize X first
+    # X past both LDS stagings of FQ(X) and K >= 1024: the two-launch path
     assert f(16, 4096, 4096, _lib.F32) == 1 and f(32, 4096, 4096, _lib.F32) == 1
     assert f(17, 300, 2080, _lib.F32) == 1 and f(9, 4096, 4096, _lib.F32) == 1
     # the streamed decode form (M <= 2) or the MFMA form's staging holds X
     assert f(1, 4096, 4096, _lib.F32) == 0 and f(8, 4096, 4096, _lib.F32) == 0
     assert f(2, 4096, 8192, _lib.F32) == 0
-    # short contractions, 16-bit inputs, empty or unaligned shapes
-    assert f(128, 1024, 1024, _lib.F32) == 0 and f(16, 4096, 4096, _lib.BF16) == 0
+    # every input dtype (the arranged FQ(X) is f32 either way)
+    assert f(16, 4096, 4096, _lib.BF16) == 1 and f(32, 4096, 4096, _lib.F16) == 1
+    assert f(128, 1024, 1024, _lib.F32) == 1 and f(64, 2048, 1024, _lib.F32) == 1
+    # short contractions, empty or unaligned shapes, unknown dtypes
+    assert f(128, 1024, 992, _lib.F32) == 0 and f(32, 4096, 512, _lib.F32) == 0
+    assert f(16, 4096, 4096, 7) == 0
     assert f(0, 4096, 4096, _lib.F32) == 0 and f(16, 4096, 4100, _lib.F32) == 0
+
+
+def test_fused_linear_split_workspace_and_arguments_without_device():
+    """The arranged-X workspace is 16 * ceil(M / 16) * K floats; the split
+    entry rejects a missing or unaligned workspace before any device work."""
+    ws = _lib.lib().axs6_nf5_fused_linear_split_workspace
+    assert ws(1, 4096) == 16 * 4096 * 4 and ws(16, 64) == 16 * 64 * 4
+    assert ws(17, 2080) == 32 * 2080 * 4 and ws(40, 8192) == 48 * 8192 * 4
+    assert ws(0, 64) == 0 and ws(16, 0) == 0 and ws(-1, 64) == 0
+    name = "axs6_nf5_fused_linear_split"
+    fake = 4096       # never dereferenced: the checks fail first
+    rc, msg = _status(name, fake, fake, None, fake, None, _lib.F32, 32, 64, 2048, 32, 1, None)
+    assert rc == 1 and "x_arranged" in msg
+    rc, msg = _status(name, fake, fake, None, fake, fake + 4, _lib.F32, 32, 64, 2048, 32, 1, None)
+    assert rc == 1 and "x_arranged" in msg
+    rc, msg = _status(name, fake, fake, None, fake, fake, _lib.F32, 32, 64, 2050, 32, 1, None)
+    assert rc == 1 and "multiple of 32" in msg
+    rc, msg = _status(name, fake, fake, None, fake, fake, _lib.F32, 32, 64, 2048, 16, 1, None)
+    assert rc == 1 and "block_size" in msg
+    rc, _ = _status(name, fake, fake, None, fake, None, _lib.F32, 0, 64, 2048, 32, 1, None)
+    assert rc == 0      # nothing to compute

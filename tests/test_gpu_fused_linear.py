@@ -92,10 +92,11 @@ def test_fused_linear_decode_form(m, K, N):
     assert torch.equal(hip_linear.fused_forward(x.to(DEV), w.to(DEV), b.to(DEV)), y)
 
 
-@pytest.mark.parametrize("m", [1, 2, 3])
+@pytest.mark.parametrize("m", [1, 2, 3, 20])
 def test_fused_linear_special_blocks(m):
     """Blocks the short FQ sequence does not cover take the general one
-    (m 1, 2: the decode form's per-step fallback; m 3: the MFMA form): a NaN
+    (m 1, 2: the decode form's per-step fallback; m 3: the MFMA form; m 20:
+    the two-launch path, X arranged first): a NaN
     block (the whole row's output NaN), an inf block, a row of 1e-33 values
     (every block's e1 below -100), a row scaled by 1e30, a block with
     subnormals beside normal values."""
@@ -124,7 +125,7 @@ def test_fused_linear_special_blocks(m):
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m", [1, 2, 3])
+@pytest.mark.parametrize("m", [1, 2, 3, 20])
 def test_fused_linear_special_blocks_16bit(dt, m):
     """The same special blocks with 16-bit operands (FQ of the upcast values,
     Y rounded to the dtype): a NaN block, an inf block, a row far above and a
@@ -159,27 +160,59 @@ def test_fused_linear_special_blocks_16bit(dt, m):
 
 
 @pytest.mark.parametrize("m,K,N", [(9, 4096, 4096), (16, 4096, 4096), (32, 4096, 4096), (64, 2048, 512),
-                                   (17, 2080, 300), (40, 8192, 64)])
+                                   (17, 2080, 300), (40, 8192, 64), (128, 1024, 1024), (200, 1056, 100)])
 def test_fused_linear_split_x_is_bit_identical(m, K, N):
-    """Where the library advises it (axs6_nf5_fused_linear_split_x: f32, K >=
-    2048, X past both LDS stagings), fused_forward quantizes X with the FQ
-    kernel first and runs the fused kernel on FQ(X) without quantize_input:
-    the output equals the single launch bit for bit, and the oracle's fp64
-    product to the usual bar."""
+    """Where the library advises it (axs6_nf5_fused_linear_split_x: K >= 1024,
+    X past both LDS stagings), fused_forward takes the two-launch entry: FQ(X)
+    once into the contraction's read order (rows past M zero to the 16-row
+    block), then the contraction on it.  The output equals the single launch
+    bit for bit, and the oracle's fp64 product to the usual bar; so does the
+    entry with quantize_input 0 (X arranged as given)."""
     from axs import _lib
     from axs.unified import hip_linear
 
+    print(f"[fused split m={m} K={K} N={N}]", flush=True)
     x, w, b = _inputs((m,), K, N, 5 * K + m)
     assert _lib.lib().axs6_nf5_fused_linear_split_x(m, N, K, _lib.F32) == 1
     y = hip_linear.fused_forward(x.to(DEV), w.to(DEV), b.to(DEV))
     xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
-    one = torch.empty(m, N, device=DEV)
-    _lib.call("axs6_nf5_fused_linear", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), one.data_ptr(), _lib.F32, m, N,
-              K, 32, 1, torch.cuda.current_stream().cuda_stream)
-    assert torch.equal(y, one)
+    st = torch.cuda.current_stream().cuda_stream
+    for qx in (1, 0):
+        one = torch.empty(m, N, device=DEV)
+        _lib.call("axs6_nf5_fused_linear", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), one.data_ptr(), _lib.F32,
+                  m, N, K, 32, qx, st)
+        if qx:
+            assert torch.equal(y, one)
+        # a workspace of NaNs: every word the contraction reads is written first
+        xa = torch.full((_lib.lib().axs6_nf5_fused_linear_split_workspace(m, K) // 4,), float("nan"), device=DEV)
+        two = torch.empty(m, N, device=DEV)
+        _lib.call("axs6_nf5_fused_linear_split", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), two.data_ptr(),
+                  xa.data_ptr(), _lib.F32, m, N, K, 32, qx, st)
+        assert torch.equal(two, one), qx
     assert oracle.rel_l2(y.cpu().numpy(), _exact(x, w, b)) <= TOL
-    # 16-bit inputs never split (their FQ values stay f32 in the kernel)
-    assert _lib.lib().axs6_nf5_fused_linear_split_x(m, N, K, _lib.BF16) == 0
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,K,N", [(16, 4096, 4096), (40, 2048, 200), (33, 4096, 1024)])
+def test_fused_linear_split_16bit_is_bit_identical(dt, m, K, N):
+    """16-bit inputs take the two-launch path too: the arranged FQ(X) is f32,
+    the values the single launch computes from the 16-bit X, so Y (rounded
+    to the input's dtype) equals the single launch's bit for bit."""
+    from axs import _lib
+    from axs.unified import hip_linear
+
+    print(f"[fused split {dt} m={m} K={K} N={N}]", flush=True)
+    x, w, b = _inputs((m,), K, N, 7 * K + m)
+    xd, wd, bd = x.to(DEV, dt), w.to(DEV, dt), b.to(DEV)
+    code = _lib.DTYPE_CODE[dt]
+    assert _lib.lib().axs6_nf5_fused_linear_split_x(m, N, K, code) == 1
+    y = hip_linear.fused_forward(xd, wd, bd)
+    one = torch.empty(m, N, device=DEV, dtype=dt)
+    _lib.call("axs6_nf5_fused_linear", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), one.data_ptr(), code, m, N, K,
+              32, 1, torch.cuda.current_stream().cuda_stream)
+    assert y.dtype == dt and torch.equal(y, one)
+    ref = _exact(xd.float().cpu(), wd.float().cpu(), b)
+    assert oracle.rel_l2(y.float().cpu().numpy(), ref) <= (4e-3 if dt == torch.bfloat16 else 5e-4)
 
 
 @pytest.mark.parametrize("m,K,N", [(1, 4096, 1024), (2, 8192, 300), (16, 4096, 1024), (5, 512, 512)])
