@@ -442,12 +442,15 @@ __device__ __forceinline__ T ld_stream(const T* p) { return __builtin_nontempora
 template <typename T>
 __device__ __forceinline__ void st_stream(T v, T* p) { __builtin_nontemporal_store(v, p); }
 
-// Stages the LUT (and the band table) in LDS; needs at least 256 threads.
+// Stages the LUT (and the band table) in LDS, with workgroups of any size
+// (one 16-byte piece per thread from 256 threads up; smaller workgroups,
+// such as the fused linear's 64- and 128-thread tilings, loop).
 __device__ __forceinline__ void stage_tables(float* lut_s, uint32_t* band_w, const float* lut_g,
                                              const uint8_t* band_g) {
-    const int tid = threadIdx.x;
-    if (tid < kLutSize / 4) reinterpret_cast<float4*>(lut_s)[tid] = reinterpret_cast<const float4*>(lut_g)[tid];
-    if (tid < kBandSize / 4) band_w[tid] = reinterpret_cast<const uint32_t*>(band_g)[tid];
+    const int tid = threadIdx.x, nt = (int)blockDim.x;
+    for (int i = tid; i < kLutSize / 4; i += nt)
+        reinterpret_cast<float4*>(lut_s)[i] = reinterpret_cast<const float4*>(lut_g)[i];
+    for (int i = tid; i < kBandSize / 4; i += nt) band_w[i] = reinterpret_cast<const uint32_t*>(band_g)[i];
     __syncthreads();
 }
 

@@ -192,6 +192,33 @@ def test_fused_linear_split_x_is_bit_identical(m, K, N):
     assert oracle.rel_l2(y.cpu().numpy(), _exact(x, w, b)) <= TOL
 
 
+@pytest.mark.parametrize("m,K,N", [(512, 1024, 1024), (512, 64, 1024), (256, 512, 1024), (256, 128, 1024),
+                                   (64, 256, 512), (16, 256, 256), (48, 32, 40)])
+def test_fused_linear_split_entry_every_tiling(m, K, N):
+    """axs6_nf5_fused_linear_split called directly, at shapes the advice never
+    picks, so that each tiling of the MFMA form runs on arranged X: 32 x 64
+    tiles (4 K-splitting waves, then 1), 32 x 32 (8, then 2), 32 x 16 with 4
+    waves, 16 x 16 with 4, and a single K tile.  Bit-identical to the single
+    launch, which takes the same tiling; both against the fp64 product (the
+    64- and 128-thread tilings once staged only part of the FQ tables)."""
+    from axs import _lib
+
+    print(f"[fused split entry m={m} K={K} N={N}]", flush=True)
+    x, w, b = _inputs((m,), K, N, 11 * K + m)
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    one = torch.empty(m, N, device=DEV)
+    _lib.call("axs6_nf5_fused_linear", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), one.data_ptr(), _lib.F32, m, N,
+              K, 32, 1, st)
+    xa = torch.full((_lib.lib().axs6_nf5_fused_linear_split_workspace(m, K) // 4,), float("nan"), device=DEV)
+    two = torch.empty(m, N, device=DEV)
+    _lib.call("axs6_nf5_fused_linear_split", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), two.data_ptr(),
+              xa.data_ptr(), _lib.F32, m, N, K, 32, 1, st)
+    exact = _exact(x, w, b)
+    assert oracle.rel_l2(one.cpu().numpy(), exact) <= TOL
+    assert torch.equal(two, one)
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,K,N", [(16, 4096, 4096), (40, 2048, 200), (33, 4096, 1024)])
 def test_fused_linear_split_16bit_is_bit_identical(dt, m, K, N):
