@@ -192,30 +192,34 @@ def test_fused_linear_split_x_is_bit_identical(m, K, N):
     assert oracle.rel_l2(y.cpu().numpy(), _exact(x, w, b)) <= TOL
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("m,K,N", [(512, 1024, 1024), (512, 64, 1024), (256, 512, 1024), (256, 128, 1024),
                                    (64, 256, 512), (16, 256, 256), (48, 32, 40)])
-def test_fused_linear_split_entry_every_tiling(m, K, N):
+def test_fused_linear_split_entry_every_tiling(m, K, N, dt):
     """axs6_nf5_fused_linear_split called directly, at shapes the advice never
     picks, so that each tiling of the MFMA form runs on arranged X: 32 x 64
     tiles (4 K-splitting waves, then 1), 32 x 32 (8, then 2), 32 x 16 with 4
-    waves, 16 x 16 with 4, and a single K tile.  Bit-identical to the single
+    waves, 16 x 16 with 4, and a single K tile; f32 and bf16 weights (two
+    16-byte loads per lane and tile, or one).  Bit-identical to the single
     launch, which takes the same tiling; both against the fp64 product (the
     64- and 128-thread tilings once staged only part of the FQ tables)."""
     from axs import _lib
 
-    print(f"[fused split entry m={m} K={K} N={N}]", flush=True)
+    print(f"[fused split entry {dt} m={m} K={K} N={N}]", flush=True)
     x, w, b = _inputs((m,), K, N, 11 * K + m)
+    x, w = x.to(dt), w.to(dt)
     xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    code = _lib.DTYPE_CODE[dt]
     st = torch.cuda.current_stream().cuda_stream
-    one = torch.empty(m, N, device=DEV)
-    _lib.call("axs6_nf5_fused_linear", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), one.data_ptr(), _lib.F32, m, N,
-              K, 32, 1, st)
+    one = torch.empty(m, N, device=DEV, dtype=dt)
+    _lib.call("axs6_nf5_fused_linear", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), one.data_ptr(), code, m, N, K,
+              32, 1, st)
     xa = torch.full((_lib.lib().axs6_nf5_fused_linear_split_workspace(m, K) // 4,), float("nan"), device=DEV)
-    two = torch.empty(m, N, device=DEV)
+    two = torch.empty(m, N, device=DEV, dtype=dt)
     _lib.call("axs6_nf5_fused_linear_split", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), two.data_ptr(),
-              xa.data_ptr(), _lib.F32, m, N, K, 32, 1, st)
-    exact = _exact(x, w, b)
-    assert oracle.rel_l2(one.cpu().numpy(), exact) <= TOL
+              xa.data_ptr(), code, m, N, K, 32, 1, st)
+    exact = _exact(x.float(), w.float(), b)
+    assert oracle.rel_l2(one.float().cpu().numpy(), exact) <= (TOL if dt == torch.float32 else 4e-3)
     assert torch.equal(two, one)
 
 
