@@ -694,7 +694,11 @@ void launch_cfg(const FusedK& k, bool qx, hipStream_t st) {
 // The MFMA form's tile and K split by shape: one 16-row block for M <= 16
 // (decode), else two; the widest column tile (64, 32, 16) that still gives
 // >= 256 workgroups; as many K-splitting waves (up to 16, within the
-// reduction LDS) as there are K tiles.  XA: X arranged by arrange_x_kernel.
+// reduction LDS) as there are K tiles, but 8 for two 16-row blocks of 16
+// columns (graph replays, 16 -> 8 waves: 48 x 768 x 2048 10.4 -> 9.2 us,
+// 256 x 512 x 512 7.7 -> 7.3; arranged X: 362 x 4096 x 362 34.4 -> 32.3,
+// 32 x 4096 x 4096 19.7 -> 19.3; others within 1%).  XA: X arranged by
+// arrange_x_kernel.
 template <int DT, bool XA>
 void launch_mfma(const FusedK& k, bool qx, hipStream_t st) {
     const int64_t nkt = k.K / kFBK;
@@ -717,7 +721,7 @@ void launch_mfma(const FusedK& k, bool qx, hipStream_t st) {
         if (nkt >= 8) launch_cfg<DT, 2, 2, 8, false, XA>(k, qx, st);
         else launch_cfg<DT, 2, 2, 2, false, XA>(k, qx, st);
     } else {
-        if (nkt >= 16) launch_cfg<DT, 2, 1, 16, false, XA>(k, qx, st);
+        if (nkt >= 16) launch_cfg<DT, 2, 1, 8, false, XA>(k, qx, st);
         else launch_cfg<DT, 2, 1, 4, false, XA>(k, qx, st);
     }
 }
