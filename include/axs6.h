@@ -258,9 +258,11 @@ int64_t axs6_nf5_fused_linear_split_workspace(int64_t M, int64_t K);
  * quantize_input = 0) is written once to x_arranged in f32, in the order the
  * contraction's 16x16x4 MFMA instructions read it, and the contraction then
  * reads it from there instead of quantizing x in every workgroup.  Same
- * arguments and results, bit for bit, plus x_arranged: a 16-byte aligned
- * device buffer of axs6_nf5_fused_linear_split_workspace(M, K) bytes,
- * overwritten.  Replaces the same reference call as axs6_nf5_fused_linear
+ * arguments plus x_arranged: a 16-byte aligned device buffer of
+ * axs6_nf5_fused_linear_split_workspace(M, K) bytes, overwritten.  The
+ * results equal axs6_nf5_fused_linear's bit for bit wherever that takes its
+ * MFMA form (every shape but the one- and two-row ones it streams, where
+ * the two agree to fp32 rounding).  Replaces the same reference call as axs6_nf5_fused_linear
  * (axs/unified/triton_kernels.py:185-282,385-482). */
 int axs6_nf5_fused_linear_split(const void* x, const void* w, const float* bias, void* y, float* x_arranged,
                                 int32_t dtype, int64_t M, int64_t N, int64_t K, int32_t block_size,
