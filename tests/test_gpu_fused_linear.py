@@ -223,6 +223,30 @@ def test_fused_linear_split_entry_every_tiling(m, K, N, dt):
     assert torch.equal(two, one)
 
 
+@pytest.mark.parametrize("m", [1, 2])
+def test_fused_linear_split_entry_streamed_rows(m):
+    """At one and two rows the single launch streams the weight (VALU
+    products, per-lane partial sums), so the split entry's MFMA contraction
+    agrees with it to fp32 rounding rather than bit for bit: both against the
+    fp64 product to the usual bar."""
+    from axs import _lib
+
+    K, N = 4096, 1024
+    x, w, b = _inputs((m,), K, N, 13 * m)
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    one = torch.empty(m, N, device=DEV)
+    _lib.call("axs6_nf5_fused_linear", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), one.data_ptr(), _lib.F32, m, N,
+              K, 32, 1, st)
+    xa = torch.full((_lib.lib().axs6_nf5_fused_linear_split_workspace(m, K) // 4,), float("nan"), device=DEV)
+    two = torch.empty(m, N, device=DEV)
+    _lib.call("axs6_nf5_fused_linear_split", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), two.data_ptr(),
+              xa.data_ptr(), _lib.F32, m, N, K, 32, 1, st)
+    exact = _exact(x, w, b)
+    assert oracle.rel_l2(one.cpu().numpy(), exact) <= TOL
+    assert oracle.rel_l2(two.cpu().numpy(), exact) <= TOL
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,K,N", [(16, 4096, 4096), (40, 2048, 200), (33, 4096, 1024)])
 def test_fused_linear_split_16bit_is_bit_identical(dt, m, K, N):
