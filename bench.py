@@ -427,9 +427,10 @@ def bench_fused(reps: int = 100, warmup: int = 10):
 
     g = torch.Generator(device="cuda").manual_seed(9)
     out = {"metric": "fused FQ + linear (M*N <= 128K outputs), device us per call",
-           "note": "fused: one launch (M <= 2: a weight row per wave, VALU products; else FQ of each 32-wide "
-                   "K tile as it is loaded, fp32 MFMA); packed: FQ + fp16 packing of X and W, then the "
-                   "fp16-MFMA GEMM; HIP-graph replays"}
+           "note": "fused: hip_linear.fused_forward, one launch (M <= 2: a weight row per wave, VALU products; "
+                   "else FQ of each 32-wide K tile as it is loaded, fp32 MFMA) or, where split_x, two (FQ(X) "
+                   "once in the MFMA read order, then the contraction); packed: FQ + fp16 packing of X and W, "
+                   "then the fp16-MFMA GEMM; HIP-graph replays"}
     for M, K, N in ((1, 4096, 4096), (32, 4096, 4096), (128, 1024, 1024), (256, 512, 512)):
         X = torch.randn(M, K, device="cuda", generator=g)
         big = N * K * 4 >= (64 << 20)
